@@ -1,0 +1,141 @@
+/*
+ * tasft_amd — C ABI of the MI355X (gfx950) block-sparse attention hot path.
+ *
+ * Every function launches asynchronously on `stream` (a hipStream_t; pass the
+ * caller's current stream) and never synchronises the device, allocates, frees or
+ * retains a pointer beyond the call. Device buffers — inputs, outputs and
+ * workspaces — are owned by the caller. Tensors are bf16 (as raw 16-bit words)
+ * unless stated; each 4-D tensor is described by element strides for its dims
+ * (b, h, s, d) and the d stride must be 1. Return value: 0 on success, a negative
+ * status on error, with the message available from tasft_last_error() on the
+ * calling thread.
+ *
+ * Layouts: Q [B, Hq, S, D]; K and V [B, Hkv, S, D] (GQA-native: query head h uses
+ * KV head h / (Hq / Hkv)); block masks are one byte per block, non-zero = attend.
+ */
+#ifndef TASFT_AMD_H_
+#define TASFT_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define TASFT_OK 0
+#define TASFT_ERR_INVALID_ARGUMENT (-1)
+#define TASFT_ERR_UNSUPPORTED (-2)
+#define TASFT_ERR_LAUNCH (-3)
+#define TASFT_ERR_WORKSPACE (-4)
+
+/* Message of the last error on this thread ("" if none). */
+const char* tasft_last_error(void);
+
+/* ABI version of this library (1). */
+int tasft_abi_version(void);
+
+/*
+ * Block-sparse flash-attention prefill.
+ * Replaces BlockSparseFlashAttention._triton_forward and the Triton kernel
+ * _block_sparse_attn_fwd_kernel (reference tasft/kernels/block_sparse_fa.py:454-552
+ * and :108-269), and makes the GQA expansion of K/V at
+ * tasft/modules/tasft_attention.py:725-729 unnecessary.
+ *
+ * out[b,h,i,:] = softmax_j(q[b,h,i,:] . k[b,h/G,j,:] * scale + M[i,j]) v[b,h/G,j,:]
+ * with M = 0 where block_mask[b,h,i/bs,j/bs] != 0 (AND j/bs <= i/bs when causal;
+ * AND j <= i inside the diagonal block when causal) and j < seq_len, else -inf.
+ * Rows with no admissible key are 0. P is rounded to bf16 before the PV product.
+ * block_mask: [B, Hq, ceil(S/bs), ceil(S/bs)] bytes, strides in mask_strides (bytes).
+ * head_dim in {64, 128}; block_size in {32, 64, 128}; strides of b/h/s multiples of 8.
+ */
+int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* out,
+                           const uint8_t* block_mask, int64_t batch, int64_t num_q_heads,
+                           int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                           int64_t block_size, const int64_t* q_strides, const int64_t* k_strides,
+                           const int64_t* v_strides, const int64_t* o_strides,
+                           const int64_t* mask_strides, float scale, int causal, void* stream);
+
+/*
+ * Bytes of workspace tasft_bsfa_decode_fwd needs for `num_splits` splits.
+ * No reference counterpart: the reference has no sparse decode
+ * (tasft/inference/vllm_patch.py:189-196 routes decode to dense PagedAttention).
+ */
+size_t tasft_bsfa_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
+                                         int64_t num_splits);
+
+/*
+ * Split-K block-sparse decode: one new query token per sequence.
+ * Stands in for the dense decode branch at tasft/inference/vllm_patch.py:189-196 and
+ * :215-252 (and the S_q != S_k rejection at tasft/modules/attn_gate.py:216-221); its
+ * result equals the last query row of tasft_bsfa_prefill_fwd under the same mask row.
+ *
+ * q [B, Hq, 1, D]; k_cache, v_cache [B, Hkv, kv_len_max, D]; out [B, Hq, 1, D];
+ * block_mask [B, Hq, 1, ceil(kv_len_max/bs)] bytes; kv_lens [B] int32 valid lengths
+ * (NULL = kv_len_max). Every KV block selected by any query head of a KV head is read
+ * once for that KV head. workspace: >= tasft_bsfa_decode_workspace_bytes(...) bytes,
+ * 16-byte aligned. At most 8 query heads per KV head.
+ */
+int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cache, void* out,
+                          const uint8_t* block_mask, const int32_t* kv_lens, void* workspace,
+                          size_t workspace_bytes, int64_t batch, int64_t num_q_heads,
+                          int64_t num_kv_heads, int64_t kv_len_max, int64_t head_dim,
+                          int64_t block_size, int64_t num_splits, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides,
+                          const int64_t* o_strides, const int64_t* mask_strides, float scale,
+                          void* stream);
+
+/* Bytes of workspace tasft_gate_fwd needs (pooled and projected block features). */
+size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                  int64_t seq_len, int64_t block_size, int64_t hidden);
+
+/*
+ * Fused AttnGate forward.
+ * Replaces AttnGate._pool_to_blocks + AttnGate.forward (reference
+ * tasft/modules/attn_gate.py:151-285) for inference, without the [B,H,NB,NB,2D]
+ * concat tensor of :250-257.
+ *
+ * w_in [hidden, 2*D] fp32 (columns [:D] act on pooled Q, [D:] on pooled K), b_in [hidden],
+ * w_out [hidden], thresholds [Hq] fp32 per-head tau. Outputs, all [B, Hq, NB, NB]
+ * contiguous: soft_scores fp32 (sigmoid of the logit, exactly 0 above the block
+ * diagonal when causal), logits fp32 (may be NULL), hard_mask bytes (soft >= tau).
+ * active_count: one uint64 in device memory receiving the number of set mask bytes.
+ * flags: TASFT_GATE_CAUSAL (zero the upper block triangle, reference is_causal) |
+ * TASFT_GATE_FORCE_DIAGONAL (set the diagonal blocks in hard_mask regardless of tau).
+ * head_dim a multiple of 8, at most 256; any block_size >= 1.
+ */
+#define TASFT_GATE_CAUSAL 1
+#define TASFT_GATE_FORCE_DIAGONAL 2
+int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float* b_in,
+                   const float* w_out, const float* thresholds, float* soft_scores, float* logits,
+                   uint8_t* hard_mask, unsigned long long* active_count, void* workspace,
+                   size_t workspace_bytes, int64_t batch, int64_t num_q_heads,
+                   int64_t num_kv_heads, int64_t seq_len, int64_t head_dim, int64_t block_size,
+                   int64_t hidden, const int64_t* q_strides, const int64_t* k_strides, int flags,
+                   void* stream);
+
+/*
+ * Gate target from Q and K, without the [B, H, S, S] score tensor.
+ * Replaces the score producer TASFTAttention._training_forward
+ * (tasft/modules/tasft_attention.py:426-458) followed by
+ * TASFTObjective.compute_gate_target (tasft/training/objectives.py:128-185).
+ *
+ * target [B, Hq, NB, NB] fp32 contiguous receives the block maxima of
+ * q.k^T*scale (causal: -inf above the diagonal and for key > query), then, when
+ * normalize is 0, a softmax over the flat NB*NB grid of each (b, h) (the reference);
+ * 1, a softmax over the key blocks of each row; 2, no normalisation (raw maxima).
+ * Before the softmax, finite maxima are clamped to [-clamp, clamp] when clamp > 0
+ * and divided by temperature (the variant of tasft/modules/tasft_attention.py:272-290).
+ */
+int tasft_gate_target_fwd(const void* q, const void* k, float* target, int64_t batch,
+                          int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                          int64_t head_dim, int64_t block_size, const int64_t* q_strides,
+                          const int64_t* k_strides, float scale, int causal, int normalize,
+                          float temperature, float clamp, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TASFT_AMD_H_ */

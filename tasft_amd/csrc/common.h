@@ -1,0 +1,101 @@
+// Shared device/host helpers for the gfx950 block-sparse attention kernels.
+//
+// Everything here is CDNA4-specific: wave64, bf16 MFMA (v_mfma_f32_32x32x16_bf16),
+// and the 64-bank LDS of gfx950. No CUDA compatibility layer is used.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace tasft {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Status codes returned by every extern "C" entry point.
+enum Status : int {
+  kOk = 0,
+  kErrInvalidArgument = -1,
+  kErrUnsupported = -2,
+  kErrLaunch = -3,
+  kErrWorkspace = -4,
+};
+
+// Thread-local last-error message (defined in capi.cpp).
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Unpack 8 bf16 (as uint4) to 8 floats.
+__device__ __forceinline__ void unpack_bf16x8(const u32x4_t& v, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(v[i] << 16);
+    out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+// Round-to-nearest-even fp32 -> bf16 of two values packed in one dword.
+// gfx950 lowers this conversion to v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  __bf16 a = (__bf16)lo;
+  __bf16 b = (__bf16)hi;
+  uint16_t ua = __builtin_bit_cast(uint16_t, a);
+  uint16_t ub = __builtin_bit_cast(uint16_t, b);
+  return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
+__device__ __forceinline__ f32x16_t mfma_32x32x16_bf16(const bf16x8_t& a, const bf16x8_t& b,
+                                                        const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// Exchange a value with the lane 32 positions away (lane l <-> lane l^32).
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Map a linear workgroup index onto (group, member) so that every member of a
+// group lands on the same XCD. gfx950 in SPX mode dispatches workgroup i to XCD
+// i % 8, so a group of `members` items sharing data (the query heads of one KV
+// head) is placed on one XCD and shares that XCD's L2. Requires
+// num_groups % 8 == 0; otherwise the identity mapping is used.
+__device__ __forceinline__ void xcd_group_map(int64_t idx, int64_t num_groups, int members,
+                                              int64_t* group, int* member) {
+  if ((num_groups & 7) == 0) {
+    const int64_t xcd = idx & 7;
+    const int64_t j = idx >> 3;
+    *group = xcd + 8 * (j / members);
+    *member = (int)(j % members);
+  } else {
+    *group = idx / members;
+    *member = (int)(idx % members);
+  }
+}
+
+}  // namespace tasft

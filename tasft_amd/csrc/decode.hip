@@ -1,0 +1,359 @@
+// Split-K block-sparse decode for gfx950 (memory bound).
+//
+// The reference has no sparse decode: its vLLM patch hands decode to the dense
+// PagedAttention (tasft/inference/vllm_patch.py:189-196, 215-252) and the HF path
+// rejects S_q != S_k (tasft/modules/attn_gate.py:216-221). The semantics implemented
+// here are the closed form of the prefill kernel's last query row
+// (tasft/kernels/block_sparse_fa.py:192-269): for one new query token per sequence,
+//   o[b, h] = softmax(q[b, h] . K_sel^T * scale) . V_sel
+// over the tokens < kv_len of the key blocks selected for query head h; a head with no
+// selected block outputs 0.
+//
+// Data path. A workgroup owns (batch b, KV head kvh, split s). It walks the union of the
+// key blocks selected by the G query heads of kvh, takes every P-th entry (P = number of
+// splits) and hands those to its 4 waves round-robin. Each selected KV block is read from
+// HBM exactly once per KV head (16-byte loads), whatever the number of query heads that
+// chose it; every head that chose it is updated from the same registers. Partial
+// (max, sum, output) triples per (b, h, split) go to a caller-provided workspace and a
+// second kernel merges them.
+#include "common.h"
+
+namespace tasft {
+
+constexpr int kDecodeMaxG = 8;  // query heads per KV head handled by one workgroup
+constexpr int kDecodeWaves = 4;
+
+struct DecodeParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  const uint8_t* mask;     // [B, Hq, 1, NB]
+  const int32_t* kv_lens;  // [B] or null
+  float* ws_o;             // [B, Hq, P, D]
+  float* ws_ml;            // [B, Hq, P, 2]
+  int64_t sq[2], sk[3], sv[3], so[2], sm[3];
+  int B, Hq, Hkv, G, S_kv, NB, P;
+  float scale_log2;
+};
+
+template <int BS, int D>
+__global__ void __launch_bounds__(kDecodeWaves * kWave)
+bsfa_decode_split_kernel(const DecodeParams p) {
+  constexpr int DOCT = D / 8;         // 16-byte chunks per row
+  constexpr int KG = kWave / DOCT;    // key groups in the PV phase
+  constexpr int KPL = (BS + kWave - 1) / kWave;  // keys per lane in the QK phase
+
+  __shared__ float q_lds[kDecodeMaxG][D];
+  __shared__ float p_lds[kDecodeWaves][BS][kDecodeMaxG];
+  __shared__ float comb_ml[kDecodeWaves][kDecodeMaxG][2];
+  __shared__ float comb_o[kDecodeWaves][kDecodeMaxG][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int G = p.G;
+
+  const int64_t item = blockIdx.x;
+  const int s = (int)(item % p.P);
+  const int64_t bk = item / p.P;
+  const int b = (int)(bk / p.Hkv);
+  const int kvh = (int)(bk % p.Hkv);
+  const int h0 = kvh * G;
+
+  const int kv_len = p.kv_lens ? min(max(p.kv_lens[b], 0), p.S_kv) : p.S_kv;
+  const int nb_valid = (kv_len + BS - 1) / BS;
+
+  // Queries of the group, pre-scaled by scale*log2(e), in fp32.
+  for (int i = tid; i < G * D; i += kDecodeWaves * kWave) {
+    const int gg = i / D, d = i % D;
+    const uint16_t qv = p.q[b * p.sq[0] + (int64_t)(h0 + gg) * p.sq[1] + d];
+    q_lds[gg][d] = bf16_bits_to_f32(qv) * p.scale_log2;
+  }
+  __syncthreads();
+
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
+  const uint8_t* mbase = p.mask + b * p.sm[0] + (int64_t)h0 * p.sm[1];
+
+  float m_run[kDecodeMaxG], l_run[kDecodeMaxG], oacc[kDecodeMaxG][8];
+#pragma unroll
+  for (int gg = 0; gg < kDecodeMaxG; ++gg) {
+    m_run[gg] = -INFINITY;
+    l_run[gg] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) oacc[gg][i] = 0.f;
+  }
+
+  const int dc = lane % DOCT;  // PV phase: head-dim chunk of this lane
+  const int kg = lane / DOCT;  // PV phase: key group of this lane
+  int entry = 0;               // rank of the next union entry (uniform)
+  for (int chunk = 0; chunk < nb_valid; chunk += kWave) {
+    const int kbl = chunk + lane;
+    uint32_t heads = 0;
+    if (kbl < nb_valid) {
+      for (int gg = 0; gg < G; ++gg)
+        if (mbase[(int64_t)gg * p.sm[1] + (int64_t)kbl * p.sm[2]]) heads |= 1u << gg;
+    }
+    uint64_t bits = __ballot(heads != 0);
+    while (bits) {
+      const int pos = __builtin_ctzll(bits);
+      bits &= bits - 1;
+      const int e = entry++;
+      if (e % p.P != s || (e / p.P) % kDecodeWaves != wave) continue;
+      const int kb = chunk + pos;
+      const uint32_t hsel = __builtin_amdgcn_readlane(heads, pos);
+      const int key0 = kb * BS;
+
+      // QK: lane owns keys key0 + lane + 64*i.
+      float x[KPL][kDecodeMaxG];
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) {
+        const int kk = lane + i * kWave;
+        const int token = key0 + kk;
+        const bool valid = kk < BS && token < kv_len;
+        float acc[kDecodeMaxG];
+#pragma unroll
+        for (int gg = 0; gg < kDecodeMaxG; ++gg) acc[gg] = 0.f;
+        if (valid) {
+          const uint16_t* krow = kbase + (int64_t)token * p.sk[2];
+#pragma unroll
+          for (int c = 0; c < DOCT; ++c) {
+            const u32x4_t kv = *(const u32x4_t*)(krow + c * 8);
+            float kf[8];
+            unpack_bf16x8(kv, kf);
+#pragma unroll
+            for (int gg = 0; gg < kDecodeMaxG; ++gg) {
+              if (gg < G) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[gg] = fmaf(kf[j], q_lds[gg][c * 8 + j], acc[gg]);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int gg = 0; gg < kDecodeMaxG; ++gg)
+          x[i][gg] = (valid && ((hsel >> gg) & 1u)) ? acc[gg] : -INFINITY;
+      }
+
+      float alpha[kDecodeMaxG];
+#pragma unroll
+      for (int gg = 0; gg < kDecodeMaxG; ++gg) {
+        if (gg >= G) { alpha[gg] = 1.f; continue; }
+        float bm = x[0][gg];
+#pragma unroll
+        for (int i = 1; i < KPL; ++i) bm = fmaxf(bm, x[i][gg]);
+        bm = wave_max(bm);
+        const float m_new = fmaxf(m_run[gg], bm);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        alpha[gg] = __builtin_amdgcn_exp2f(m_run[gg] - m_use);
+        float ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(x[i][gg] - m_use);
+          ls += pv;
+          const int kk = lane + i * kWave;
+          if (kk < BS) p_lds[wave][kk][gg] = pv;
+        }
+        l_run[gg] = l_run[gg] * alpha[gg] + ls;
+        m_run[gg] = m_new;
+      }
+      // p_lds is private to this wave: a wave-level barrier orders its writes and reads.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // PV: lane owns head dims dc*8..+7 for keys kg, kg+KG, ...
+#pragma unroll
+      for (int gg = 0; gg < kDecodeMaxG; ++gg)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) oacc[gg][i] *= alpha[gg];
+      const int kmax = min(BS, kv_len - key0);
+      for (int kk = kg; kk < kmax; kk += KG) {
+        const u32x4_t vv = *(const u32x4_t*)(vbase + (int64_t)(key0 + kk) * p.sv[2] + dc * 8);
+        float vf[8];
+        unpack_bf16x8(vv, vf);
+#pragma unroll
+        for (int gg = 0; gg < kDecodeMaxG; ++gg) {
+          if (gg < G) {
+            const float pw = p_lds[wave][kk][gg];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pw, vf[j], oacc[gg][j]);
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+
+  // Reduce each wave's PV partials over its key groups, then merge the 4 waves.
+#pragma unroll
+  for (int gg = 0; gg < kDecodeMaxG; ++gg) {
+    if (gg >= G) continue;
+#pragma unroll
+    for (int off = DOCT; off < kWave; off <<= 1)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) oacc[gg][j] += __shfl_xor(oacc[gg][j], off, 64);
+    const float lt = wave_sum(l_run[gg]);
+    if (lane < DOCT) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) comb_o[wave][gg][lane * 8 + j] = oacc[gg][j];
+    }
+    if (lane == 0) {
+      comb_ml[wave][gg][0] = m_run[gg];
+      comb_ml[wave][gg][1] = lt;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += kDecodeWaves * kWave) {
+    const int gg = i / D, d = i % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, comb_ml[w][gg][0]);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float f = __builtin_amdgcn_exp2f(comb_ml[w][gg][0] - Mu);
+      L += comb_ml[w][gg][1] * f;
+      O += comb_o[w][gg][d] * f;
+    }
+    const int64_t row = ((int64_t)b * p.Hq + h0 + gg) * p.P + s;
+    p.ws_o[row * D + d] = O;
+    if (d == 0) {
+      p.ws_ml[row * 2 + 0] = M;
+      p.ws_ml[row * 2 + 1] = L;
+    }
+  }
+}
+
+// Merge the P split partials of every (b, h) and write the bf16 output row.
+template <int D>
+__global__ void __launch_bounds__(D)
+bsfa_decode_combine_kernel(const DecodeParams p) {
+  const int64_t bh = blockIdx.x;
+  const int b = (int)(bh / p.Hq);
+  const int h = (int)(bh % p.Hq);
+  const int d = threadIdx.x;
+  const float* ml = p.ws_ml + bh * p.P * 2;
+  const float* os = p.ws_o + bh * p.P * D;
+  float M = -INFINITY;
+  for (int sp = 0; sp < p.P; ++sp) M = fmaxf(M, ml[2 * sp]);
+  const float Mu = (M == -INFINITY) ? 0.f : M;
+  float L = 0.f, O = 0.f;
+  for (int sp = 0; sp < p.P; ++sp) {
+    const float f = __builtin_amdgcn_exp2f(ml[2 * sp] - Mu);
+    L += ml[2 * sp + 1] * f;
+    O += os[(int64_t)sp * D + d] * f;
+  }
+  const float r = L > 0.f ? O / L : 0.f;
+  const __bf16 rb = (__bf16)r;
+  p.o[b * p.so[0] + h * p.so[1] + d] = __builtin_bit_cast(uint16_t, rb);
+}
+
+template <int BS, int D>
+static hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+  const int64_t grid = (int64_t)p.B * p.Hkv * p.P;
+  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D>), dim3((unsigned)grid),
+                     dim3(kDecodeWaves * kWave), 0, stream, p);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((bsfa_decode_combine_kernel<D>), dim3((unsigned)((int64_t)p.B * p.Hq)), dim3(D),
+                     0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace tasft
+
+using namespace tasft;
+
+extern "C" size_t tasft_bsfa_decode_workspace_bytes(int64_t batch, int64_t num_q_heads,
+                                                    int64_t head_dim, int64_t num_splits) {
+  if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
+  return (size_t)(batch * num_q_heads * num_splits) * (size_t)(head_dim + 2) * sizeof(float);
+}
+
+extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
+                                     void* out, const uint8_t* block_mask, const int32_t* kv_lens,
+                                     void* workspace, size_t workspace_bytes, int64_t batch,
+                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t kv_len_max,
+                                     int64_t head_dim, int64_t block_size, int64_t num_splits,
+                                     const int64_t* q_strides, const int64_t* k_strides,
+                                     const int64_t* v_strides, const int64_t* o_strides,
+                                     const int64_t* mask_strides, float scale, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !block_mask || !workspace || !q_strides ||
+      !k_strides || !v_strides || !o_strides || !mask_strides)
+    return set_error(kErrInvalidArgument, "decode: null pointer argument");
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || kv_len_max <= 0 || num_splits <= 0)
+    return set_error(kErrInvalidArgument, "decode: sizes must be positive");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument, "decode: num_q_heads must be a multiple of num_kv_heads");
+  const int64_t G = num_q_heads / num_kv_heads;
+  if (G > kDecodeMaxG)
+    return set_error(kErrUnsupported, "decode: at most %d query heads per KV head, got %lld",
+                     kDecodeMaxG, (long long)G);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(kErrUnsupported, "decode: head_dim must be 64 or 128, got %lld",
+                     (long long)head_dim);
+  if (block_size != 32 && block_size != 64 && block_size != 128)
+    return set_error(kErrUnsupported, "decode: block_size must be 32, 64 or 128, got %lld",
+                     (long long)block_size);
+  const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+  if (workspace_bytes < need)
+    return set_error(kErrWorkspace, "decode: workspace too small: need %zu bytes, got %zu", need,
+                     workspace_bytes);
+  if (q_strides[3] != 1 || k_strides[3] != 1 || v_strides[3] != 1 || o_strides[3] != 1)
+    return set_error(kErrInvalidArgument, "decode: head_dim must be the contiguous dimension");
+  for (int j = 0; j < 3; ++j)
+    if (k_strides[j] % 8 != 0 || v_strides[j] % 8 != 0)
+      return set_error(kErrInvalidArgument, "decode: K/V strides must be multiples of 8 elements");
+  if ((((uintptr_t)k_cache) & 15u) || (((uintptr_t)v_cache) & 15u) || (((uintptr_t)workspace) & 15u))
+    return set_error(kErrInvalidArgument, "decode: K/V cache and workspace must be 16-byte aligned");
+  const int64_t nb = (kv_len_max + block_size - 1) / block_size;
+  if (batch * num_kv_heads * num_splits > 0x7fffffffLL || kv_len_max > 0x3fffffffLL)
+    return set_error(kErrUnsupported, "decode: problem too large for one launch");
+
+  DecodeParams p;
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k_cache;
+  p.v = (const uint16_t*)v_cache;
+  p.o = (uint16_t*)out;
+  p.mask = block_mask;
+  p.kv_lens = kv_lens;
+  const size_t o_bytes = (size_t)(batch * num_q_heads * num_splits) * head_dim * sizeof(float);
+  p.ws_o = (float*)workspace;
+  p.ws_ml = (float*)((char*)workspace + o_bytes);
+  p.sq[0] = q_strides[0];
+  p.sq[1] = q_strides[1];
+  p.so[0] = o_strides[0];
+  p.so[1] = o_strides[1];
+  for (int j = 0; j < 3; ++j) {
+    p.sk[j] = k_strides[j];
+    p.sv[j] = v_strides[j];
+  }
+  p.sm[0] = mask_strides[0];
+  p.sm[1] = mask_strides[1];
+  p.sm[2] = mask_strides[3];
+  p.B = (int)batch;
+  p.Hq = (int)num_q_heads;
+  p.Hkv = (int)num_kv_heads;
+  p.G = (int)G;
+  p.S_kv = (int)kv_len_max;
+  p.NB = (int)nb;
+  p.P = (int)num_splits;
+  p.scale_log2 = scale * kLog2e;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t err;
+  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128>(p, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64>(p, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128>(p, s);
+  else if (block_size == 32 && head_dim == 64) err = launch_decode<32, 64>(p, s);
+  else if (block_size == 128 && head_dim == 128) err = launch_decode<128, 128>(p, s);
+  else err = launch_decode<128, 64>(p, s);
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "decode: launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}

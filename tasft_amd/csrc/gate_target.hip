@@ -1,0 +1,241 @@
+// Training-time gate target without the [B, H, S, S] score tensor.
+//
+// Reference semantics:
+//   scores = Q K^T * scale + triu(-inf, 1)            (tasft/modules/tasft_attention.py:426-443)
+//   pooled = max_pool2d(pad(scores, -inf), bs, bs)    (tasft/training/objectives.py:170-178)
+//   target = softmax(pooled over the flat NB_q*NB_k grid)  (objectives.py:181-185)
+// plus two options: a per-row softmax over key blocks (the BASELINE wording of the
+// target) and the clamp(+-50) / temperature variant of
+// tasft/modules/tasft_attention.py:272-290.
+//
+// Kernel 1 computes each block maximum with the same S^T = K . Q^T bf16 MFMA tiling as
+// the prefill kernel (v_mfma_f32_32x32x16_bf16, fp32 accumulation) and keeps only the
+// maximum of every 64x64 tile, so the work is the QK^T half of a dense causal prefill
+// and nothing of size S^2 touches HBM. Kernel 2 normalises in place.
+#include "common.h"
+
+namespace tasft {
+
+struct GateTargetParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  float* out;  // [B, Hq, NB, NB] contiguous
+  int64_t sq[3], sk[3];
+  int B, Hq, Hkv, G, S, NB;
+  float scale;
+  int causal;
+};
+
+template <int BS, int D>
+__global__ void __launch_bounds__(BS / 32 * kWave)
+gate_target_blockmax_kernel(const GateTargetParams p) {
+  constexpr int WAVES = BS / 32;
+  constexpr int THREADS = WAVES * kWave;
+  constexpr int KSTEPS = D / 16;
+  constexpr int KTILES = BS / 32;
+  constexpr int KST = D + 8;
+
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BS * KST];
+  __shared__ float red[2][WAVES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  const int64_t per_slab = (int64_t)p.B * p.Hq;
+  const int64_t idx = blockIdx.x;
+  const int slab = (int)(idx / per_slab);
+  const int qb = p.causal ? (p.NB - 1 - slab) : slab;
+  int64_t grp;
+  int g;
+  xcd_group_map(idx % per_slab, (int64_t)p.B * p.Hkv, p.G, &grp, &g);
+  const int b = (int)(grp / p.Hkv);
+  const int kvh = (int)(grp % p.Hkv);
+  const int h = kvh * p.G + g;
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NB + qb) * p.NB;
+
+  const int qrow = qb * BS + wave * 32 + col;
+  const bool qvalid = qrow < p.S;
+  bf16x8_t qf[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    u32x4_t val = {0u, 0u, 0u, 0u};
+    if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
+    qf[ks] = as_bf16x8(val);
+  }
+
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  // Key blocks above the diagonal are -inf in the pooled grid (causal triu mask).
+  for (int kb = kb_end + tid; kb < p.NB; kb += THREADS) orow[kb] = -INFINITY;
+
+  for (int kb = 0; kb < kb_end; ++kb) {
+    const int key0 = kb * BS;
+    __syncthreads();
+    if (tid == 0 && kb > 0) {
+      float mx = red[(kb - 1) & 1][0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[(kb - 1) & 1][w]);
+      orow[kb - 1] = mx * p.scale;
+    }
+#pragma unroll
+    for (int c = tid; c < BS * D / 8; c += THREADS) {
+      const int r = c / (D / 8);
+      const int cc = c % (D / 8);
+      u32x4_t val = {0u, 0u, 0u, 0u};
+      if (key0 + r < p.S) val = *(const u32x4_t*)(kbase + (int64_t)(key0 + r) * p.sk[2] + cc * 8);
+      *(u32x4_t*)(k_lds + r * KST + cc * 8) = val;
+    }
+    __syncthreads();
+
+    const bool need_mask = (p.causal && kb == qb) || (key0 + BS > p.S) || !qvalid;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < KTILES; ++t) {
+      f32x16_t s = (f32x16_t){};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const u32x4_t a = *(const u32x4_t*)(k_lds + (t * 32 + col) * KST + ks * 16 + half * 8);
+        s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[r];
+        if (need_mask) {
+          const int key = key0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (!qvalid || key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
+        }
+        mloc = fmaxf(mloc, x);
+      }
+    }
+    mloc = wave_max(mloc);
+    if (lane == 0) red[kb & 1][wave] = mloc;
+  }
+  __syncthreads();
+  if (tid == 0 && kb_end > 0) {
+    float mx = red[(kb_end - 1) & 1][0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[(kb_end - 1) & 1][w]);
+    orow[kb_end - 1] = mx * p.scale;
+  }
+}
+
+// In-place softmax over groups of `group_len` contiguous values. Finite values are
+// optionally clamped to [-clamp, clamp] first, then divided by the temperature;
+// -inf entries map to 0.
+__global__ void __launch_bounds__(256)
+gate_target_normalize_kernel(float* data, int64_t group_len, float inv_temp, float clamp) {
+  __shared__ float red[256 / kWave];
+  float* x = data + (int64_t)blockIdx.x * group_len;
+  const int tid = threadIdx.x;
+  auto xform = [&](float v) {
+    if (clamp > 0.f && v > -INFINITY) v = fminf(fmaxf(v, -clamp), clamp);
+    return v * inv_temp;
+  };
+  float mx = -INFINITY;
+  for (int64_t i = tid; i < group_len; i += 256) mx = fmaxf(mx, xform(x[i]));
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.f;
+  for (int64_t i = tid; i < group_len; i += 256) sum += expf(xform(x[i]) - mx);
+  sum = wave_sum(sum);
+  if ((tid & 63) == 0) red[tid >> 6] = sum;
+  __syncthreads();
+  sum = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.f / sum;
+  for (int64_t i = tid; i < group_len; i += 256) x[i] = expf(xform(x[i]) - mx) * inv;
+}
+
+template <int BS, int D>
+static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream) {
+  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
+  hipLaunchKernelGGL((gate_target_blockmax_kernel<BS, D>), dim3((unsigned)grid),
+                     dim3(BS / 32 * kWave), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace tasft
+
+using namespace tasft;
+
+extern "C" int tasft_gate_target_fwd(const void* q, const void* k, float* target, int64_t batch,
+                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                                     int64_t head_dim, int64_t block_size,
+                                     const int64_t* q_strides, const int64_t* k_strides,
+                                     float scale, int causal, int normalize, float temperature,
+                                     float clamp, void* stream) {
+  if (!q || !k || !target || !q_strides || !k_strides)
+    return set_error(kErrInvalidArgument, "gate_target: null pointer argument");
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0)
+    return set_error(kErrInvalidArgument, "gate_target: batch, heads and seq_len must be positive");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument, "gate_target: num_q_heads must be a multiple of num_kv_heads");
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(kErrUnsupported, "gate_target: head_dim must be 64 or 128, got %lld",
+                     (long long)head_dim);
+  if (block_size != 32 && block_size != 64 && block_size != 128)
+    return set_error(kErrUnsupported, "gate_target: block_size must be 32, 64 or 128, got %lld",
+                     (long long)block_size);
+  if (normalize < 0 || normalize > 2)
+    return set_error(kErrInvalidArgument, "gate_target: normalize must be 0 (flat), 1 (row) or 2 (none)");
+  if (!(temperature > 0.f))
+    return set_error(kErrInvalidArgument, "gate_target: temperature must be > 0");
+  const int64_t* st[2] = {q_strides, k_strides};
+  for (int i = 0; i < 2; ++i) {
+    if (st[i][3] != 1)
+      return set_error(kErrInvalidArgument, "gate_target: head_dim must be the contiguous dimension");
+    for (int j = 0; j < 3; ++j)
+      if (st[i][j] % 8 != 0)
+        return set_error(kErrInvalidArgument, "gate_target: strides must be multiples of 8 elements");
+  }
+  if ((((uintptr_t)q) & 15u) || (((uintptr_t)k) & 15u))
+    return set_error(kErrInvalidArgument, "gate_target: tensors must be 16-byte aligned");
+  const int64_t nb = (seq_len + block_size - 1) / block_size;
+  if (nb * batch * num_q_heads > 0x7fffffffLL)
+    return set_error(kErrUnsupported, "gate_target: problem too large for one launch");
+
+  GateTargetParams p;
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.out = target;
+  for (int j = 0; j < 3; ++j) {
+    p.sq[j] = q_strides[j];
+    p.sk[j] = k_strides[j];
+  }
+  p.B = (int)batch;
+  p.Hq = (int)num_q_heads;
+  p.Hkv = (int)num_kv_heads;
+  p.G = (int)(num_q_heads / num_kv_heads);
+  p.S = (int)seq_len;
+  p.NB = (int)nb;
+  p.scale = scale;
+  p.causal = causal ? 1 : 0;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t err;
+  if (block_size == 64 && head_dim == 128) err = launch_blockmax<64, 128>(p, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_blockmax<64, 64>(p, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_blockmax<32, 128>(p, s);
+  else if (block_size == 32 && head_dim == 64) err = launch_blockmax<32, 64>(p, s);
+  else if (block_size == 128 && head_dim == 128) err = launch_blockmax<128, 128>(p, s);
+  else err = launch_blockmax<128, 64>(p, s);
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "gate_target: block-max launch failed: %s", hipGetErrorString(err));
+
+  if (normalize != 2) {
+    const int64_t groups = normalize == 0 ? batch * num_q_heads : batch * num_q_heads * nb;
+    const int64_t len = normalize == 0 ? nb * nb : nb;
+    hipLaunchKernelGGL(gate_target_normalize_kernel, dim3((unsigned)groups), dim3(256), 0, s,
+                       target, len, 1.f / temperature, clamp);
+    if ((err = hipGetLastError()) != hipSuccess)
+      return set_error(kErrLaunch, "gate_target: normalize launch failed: %s", hipGetErrorString(err));
+  }
+  return kOk;
+}

@@ -1,0 +1,325 @@
+// Causal GQA block-sparse flash-attention prefill for gfx950.
+//
+// Semantics follow the reference Triton kernel (tasft/kernels/block_sparse_fa.py:108-269)
+// and its host preparation (:493-514):
+//   * one query block of BS rows attends to the key blocks whose mask byte is non-zero;
+//     with causal=1 the mask is AND-ed with the block lower triangle and, inside the
+//     diagonal block, key > query is excluded;
+//   * scores are fp32 (bf16 MFMA, fp32 accumulate) times `scale`; online softmax in fp32;
+//     P is rounded to bf16 before the PV product (:252); l stays fp32;
+//   * rows with no active key output 0 (:257-258); rows >= S are never stored (:268-269).
+//
+// GQA is native: query head h reads key/value head h / (Hq / Hkv) in place, so K/V are
+// never expanded (the reference callers repeat_interleave them first,
+// tasft/modules/tasft_attention.py:725-729).
+//
+// Mapping onto CDNA4. A workgroup owns one (batch, query head, query block) and has
+// BS/32 waves; wave w owns 32 query rows. Each key block is computed as
+// S^T = K . Q^T with v_mfma_f32_32x32x16_bf16, so a lane owns one query column of S^T:
+// its running max and sum live in that lane (plus the lane 32 away), and the P^T
+// accumulator registers feed the PV product O^T = V^T . P^T directly as the B operand
+// with no shuffle. K (row major) and V^T (transposed while staging) go through LDS
+// rows padded so the MFMA operand reads are bank-conflict free on the 64-bank LDS.
+#include "common.h"
+
+namespace tasft {
+
+struct PrefillParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  const uint8_t* mask;
+  int64_t sq[3], sk[3], sv[3], so[3];  // element strides of dims (b, h, s); d stride is 1
+  int64_t sm[4];                       // byte strides of the mask dims (b, h, qb, kb)
+  int B, Hq, Hkv, G, S, NB;
+  float scale_log2;  // softmax scale * log2(e)
+  int causal;
+};
+
+template <int BS, int D>
+__global__ void __launch_bounds__(BS / 32 * kWave)
+bsfa_prefill_kernel(const PrefillParams p) {
+  constexpr int WAVES = BS / 32;
+  constexpr int THREADS = WAVES * kWave;
+  constexpr int KSTEPS = D / 16;   // MFMA k-steps over the head dim
+  constexpr int KTILES = BS / 32;  // 32-key tiles per key block
+  constexpr int DTILES = D / 32;   // 32-row head-dim tiles of O^T
+  constexpr int KST = D + 8;       // LDS row stride of K (bf16 elements)
+  constexpr int VST = BS + 4;      // LDS row stride of V^T (bf16 elements)
+
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BS * KST];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VST];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // Work item: query blocks in descending order (causal rows get longer with qb, so the
+  // heaviest rows start first); inside one query-block slab the query heads of a KV
+  // head share an XCD.
+  const int64_t per_slab = (int64_t)p.B * p.Hq;
+  const int64_t idx = blockIdx.x;
+  const int slab = (int)(idx / per_slab);
+  const int qb = p.causal ? (p.NB - 1 - slab) : slab;
+  int64_t grp;
+  int g;
+  xcd_group_map(idx % per_slab, (int64_t)p.B * p.Hkv, p.G, &grp, &g);
+  const int b = (int)(grp / p.Hkv);
+  const int kvh = (int)(grp % p.Hkv);
+  const int h = kvh * p.G + g;
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
+  uint16_t* obase = p.o + b * p.so[0] + h * p.so[1];
+  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
+
+  // Q^T as the B operand: lane (col, half) holds query row `qrow`, head dims
+  // ks*16 + half*8 .. +7 for every k-step.
+  const int qrow = qb * BS + wave * 32 + col;
+  const bool qvalid = qrow < p.S;
+  bf16x8_t qf[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    u32x4_t val = {0u, 0u, 0u, 0u};
+    if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
+    qf[ks] = as_bf16x8(val);
+  }
+
+  f32x16_t oacc[DTILES];
+#pragma unroll
+  for (int dt = 0; dt < DTILES; ++dt) oacc[dt] = (f32x16_t){};
+  float m_run = -INFINITY;  // running max (log2 domain), identical in lanes l and l^32
+  float l_run = 0.f;        // this lane's share of the running denominator
+
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  for (int chunk = 0; chunk < kb_end; chunk += kWave) {
+    // Every wave reads the same 64 mask bytes, so all waves walk the same key blocks.
+    const int kbl = chunk + lane;
+    const bool act = (kbl < kb_end) && (mrow[(int64_t)kbl * p.sm[3]] != 0);
+    uint64_t bits = __ballot(act);
+    while (bits) {
+      const int kb = chunk + __builtin_ctzll(bits);
+      bits &= bits - 1;
+      const int key0 = kb * BS;
+
+      __syncthreads();  // previous block's LDS reads are complete
+      // Stage K rows (16-byte chunks), zero-filling keys >= S.
+#pragma unroll
+      for (int c = tid; c < BS * D / 8; c += THREADS) {
+        const int r = c / (D / 8);
+        const int cc = c % (D / 8);
+        u32x4_t val = {0u, 0u, 0u, 0u};
+        if (key0 + r < p.S) val = *(const u32x4_t*)(kbase + (int64_t)(key0 + r) * p.sk[2] + cc * 8);
+        *(u32x4_t*)(k_lds + r * KST + cc * 8) = val;
+      }
+      // Stage V transposed: a unit is 4 keys x 8 head dims, written as 8 rows of V^T.
+#pragma unroll
+      for (int u = tid; u < (BS / 4) * (D / 8); u += THREADS) {
+        const int kq = u % (BS / 4);
+        const int dc = u / (BS / 4);
+        u32x4_t rows[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = key0 + kq * 4 + j;
+          rows[j] = (u32x4_t){0u, 0u, 0u, 0u};
+          if (key < p.S) rows[j] = *(const u32x4_t*)(vbase + (int64_t)key * p.sv[2] + dc * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          uint32_t e[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            e[j] = (i & 1) ? (rows[j][i >> 1] >> 16) : (rows[j][i >> 1] & 0xffffu);
+          const u32x2_t w = {e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+          *(u32x2_t*)(vt_lds + (dc * 8 + i) * VST + kq * 4) = w;
+        }
+      }
+      __syncthreads();
+
+      // S^T tiles: rows = keys t*32 + ..., cols = this wave's 32 queries.
+      f32x16_t s[KTILES];
+#pragma unroll
+      for (int t = 0; t < KTILES; ++t) {
+        s[t] = (f32x16_t){};
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+          const u32x4_t a = *(const u32x4_t*)(k_lds + (t * 32 + col) * KST + ks * 16 + half * 8);
+          s[t] = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s[t]);
+        }
+      }
+
+      // Register r of tile t holds key t*32 + 8*(r/4) + 4*half + r%4 for query `qrow`.
+      const bool need_mask = (p.causal && kb == qb) || (key0 + BS > p.S);
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < KTILES; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = s[t][r] * p.scale_log2;
+          if (need_mask) {
+            const int key = key0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
+          }
+          s[t][r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      }
+      mloc = fmaxf(mloc, xor32(mloc));
+      const float m_new = fmaxf(m_run, mloc);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      float lsum = 0.f;
+#pragma unroll
+      for (int t = 0; t < KTILES; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = __builtin_amdgcn_exp2f(s[t][r] - m_use);
+          s[t][r] = e;
+          lsum += e;
+        }
+      }
+      l_run = l_run * alpha + lsum;
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) oacc[dt] *= alpha;
+
+      // P^T as the B operand of O^T = V^T P^T: k-step (t, pp) uses registers 8pp..8pp+7
+      // of tile t, i.e. keys t*32 + 16pp + 8*(j/4) + 4*half + j%4 for slot j.
+      bf16x8_t pb[KTILES][2];
+#pragma unroll
+      for (int t = 0; t < KTILES; ++t) {
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const u32x4_t w = {pack_bf16x2(s[t][8 * pp + 0], s[t][8 * pp + 1]),
+                             pack_bf16x2(s[t][8 * pp + 2], s[t][8 * pp + 3]),
+                             pack_bf16x2(s[t][8 * pp + 4], s[t][8 * pp + 5]),
+                             pack_bf16x2(s[t][8 * pp + 6], s[t][8 * pp + 7])};
+          pb[t][pp] = as_bf16x8(w);
+        }
+      }
+      // V^T as the A operand with the same key order: two 4-key runs per slot group.
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+#pragma unroll
+        for (int t = 0; t < KTILES; ++t) {
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp) {
+            const uint16_t* vp = vt_lds + (dt * 32 + col) * VST + t * 32 + pp * 16 + half * 4;
+            const u32x2_t lo = *(const u32x2_t*)vp;
+            const u32x2_t hi = *(const u32x2_t*)(vp + 8);
+            const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
+            oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb[t][pp], oacc[dt]);
+          }
+        }
+      }
+    }
+  }
+
+  // Epilogue: combine the two half-lane denominators, normalise, store bf16.
+  const float l_tot = l_run + xor32(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (qvalid) {
+    uint16_t* orow = obase + (int64_t)qrow * p.so[2];
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d0 = dt * 32 + 8 * gq + 4 * half;
+        const u32x2_t w = {pack_bf16x2(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
+                           pack_bf16x2(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
+        *(u32x2_t*)(orow + d0) = w;
+      }
+    }
+  }
+}
+
+template <int BS, int D>
+static hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
+  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
+  hipLaunchKernelGGL((bsfa_prefill_kernel<BS, D>), dim3((unsigned)grid), dim3(BS / 32 * kWave), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+}  // namespace tasft
+
+using namespace tasft;
+
+extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* out,
+                                      const uint8_t* block_mask, int64_t batch,
+                                      int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                                      int64_t head_dim, int64_t block_size,
+                                      const int64_t* q_strides, const int64_t* k_strides,
+                                      const int64_t* v_strides, const int64_t* o_strides,
+                                      const int64_t* mask_strides, float scale, int causal,
+                                      void* stream) {
+  if (!q || !k || !v || !out || !block_mask || !q_strides || !k_strides || !v_strides ||
+      !o_strides || !mask_strides)
+    return set_error(kErrInvalidArgument, "prefill: null pointer argument");
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0)
+    return set_error(kErrInvalidArgument, "prefill: batch, heads and seq_len must be positive");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument,
+                     "prefill: num_q_heads (%lld) must be a multiple of num_kv_heads (%lld)",
+                     (long long)num_q_heads, (long long)num_kv_heads);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(kErrUnsupported, "prefill: head_dim must be 64 or 128, got %lld",
+                     (long long)head_dim);
+  if (block_size != 32 && block_size != 64 && block_size != 128)
+    return set_error(kErrUnsupported, "prefill: block_size must be 32, 64 or 128, got %lld",
+                     (long long)block_size);
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  for (int i = 0; i < 4; ++i) {
+    if (st[i][3] != 1)
+      return set_error(kErrInvalidArgument, "prefill: head_dim must be the contiguous dimension");
+    for (int j = 0; j < 3; ++j)
+      if (st[i][j] % 8 != 0)
+        return set_error(kErrInvalidArgument,
+                         "prefill: strides must be multiples of 8 elements (16-byte rows)");
+  }
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return set_error(kErrInvalidArgument, "prefill: tensors must be 16-byte aligned");
+  const int64_t nb = (seq_len + block_size - 1) / block_size;
+  if (nb * batch * num_q_heads > 0x7fffffffLL || seq_len > 0x3fffffffLL)
+    return set_error(kErrUnsupported, "prefill: problem too large for one launch");
+
+  PrefillParams p;
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v;
+  p.o = (uint16_t*)out;
+  p.mask = block_mask;
+  for (int j = 0; j < 3; ++j) {
+    p.sq[j] = q_strides[j];
+    p.sk[j] = k_strides[j];
+    p.sv[j] = v_strides[j];
+    p.so[j] = o_strides[j];
+  }
+  for (int j = 0; j < 4; ++j) p.sm[j] = mask_strides[j];
+  p.B = (int)batch;
+  p.Hq = (int)num_q_heads;
+  p.Hkv = (int)num_kv_heads;
+  p.G = (int)(num_q_heads / num_kv_heads);
+  p.S = (int)seq_len;
+  p.NB = (int)nb;
+  p.scale_log2 = scale * kLog2e;
+  p.causal = causal ? 1 : 0;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t err;
+  if (block_size == 64 && head_dim == 128) err = launch_prefill<64, 128>(p, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_prefill<64, 64>(p, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_prefill<32, 128>(p, s);
+  else if (block_size == 32 && head_dim == 64) err = launch_prefill<32, 64>(p, s);
+  else if (block_size == 128 && head_dim == 128) err = launch_prefill<128, 128>(p, s);
+  else err = launch_prefill<128, 64>(p, s);
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "prefill: launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}

@@ -1,0 +1,392 @@
+"""Block-sparse flash attention on MI355X (gfx950) behind the reference API.
+
+Mirrors ``tasft.kernels.block_sparse_fa`` (reference ``tasft/kernels/block_sparse_fa.py:54-618``):
+same class, constructor, ``forward`` signature, validation order and messages, sparsity
+statistics and low-sparsity policy. The compute backend is the hand-written HIP library
+``libtasft_amd.so`` reached through its C ABI; there is no Triton and no second kernel
+backend. ``DENSE_FALLBACK`` stays what it is in the reference: torch SDPA, which ignores
+the block mask, used only when explicitly requested or when the mask is denser than
+``min_sparsity_for_speedup`` (reference ``:392-399``).
+
+Additive, keyword-compatible extensions:
+  * GQA-native ``forward``: ``k``/``v`` may carry ``Hkv`` heads with ``Hq % Hkv == 0``
+    (query head ``h`` reads KV head ``h // (Hq // Hkv)``, the ``repeat_interleave``
+    mapping of ``tasft/modules/tasft_attention.py:725-729``), so callers no longer
+    expand K/V.
+  * ``forward_decode``: split-K block-sparse decode for one new token per sequence.
+"""
+from __future__ import annotations
+
+import math
+import warnings
+from dataclasses import dataclass
+from enum import Enum, auto
+
+import torch
+from torch.nn import functional
+
+from tasft_amd import _native
+from tasft_amd.exceptions import KernelError
+from tasft_amd.types import VALID_BLOCK_SIZES
+
+_VALID_HEAD_DIMS = frozenset({64, 128})
+_EXPECTED_TENSOR_NDIM = 4
+
+
+class KernelBackend(Enum):
+    """Backends of the reference enum plus the gfx950 HIP backend.
+
+    ``FLASH_ATTN_SPARSE`` and ``TRITON`` are kept so reference code that names them still
+    imports; they are never available here. ``HIP_GFX950`` is the only compute backend.
+    """
+
+    AUTO = auto()
+    FLASH_ATTN_SPARSE = auto()
+    TRITON = auto()
+    HIP_GFX950 = auto()
+    DENSE_FALLBACK = auto()
+
+
+def detect_kernels() -> list[KernelBackend]:
+    """Available backends, highest priority first; ``DENSE_FALLBACK`` is always last.
+
+    Reference: ``block_sparse_fa.py:63-90``. Probes only whether the C-ABI library loads;
+    it never touches the GPU.
+    """
+    available: list[KernelBackend] = []
+    if _native.is_available():
+        available.append(KernelBackend.HIP_GFX950)
+    available.append(KernelBackend.DENSE_FALLBACK)
+    return available
+
+
+@dataclass(frozen=True, slots=True)
+class SparsityStats:
+    """Block-mask statistics (reference ``block_sparse_fa.py:277-291``).
+
+    ``sparsity_ratio`` counts the full NB x NB grid, upper triangle included, exactly as
+    the reference does (``:586-588``).
+    """
+
+    total_blocks: int
+    active_blocks: int
+    sparsity_ratio: float
+    estimated_speedup: float
+
+
+def _kv_compatible(q: torch.Tensor, kv: torch.Tensor) -> bool:
+    if kv.ndim != _EXPECTED_TENSOR_NDIM:
+        return False
+    b, hq, s, d = q.shape
+    bk, hk, sk, dk = kv.shape
+    return bk == b and sk == s and dk == d and hk > 0 and hq % hk == 0
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` if its layout suits the kernels (unit d stride, 16-byte rows), else a copy."""
+    st = t.stride()
+    if st[-1] == 1 and all(s % 8 == 0 for s in st[:-1]) and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
+
+
+def _mask_bytes(mask: torch.Tensor) -> torch.Tensor:
+    """One byte per block, non-zero = attend, without a copy for bool masks."""
+    if mask.dtype == torch.bool:
+        return mask.view(torch.uint8)
+    if mask.dtype in (torch.uint8, torch.int8):
+        return mask.view(torch.uint8) if mask.dtype == torch.int8 else mask
+    return (mask != 0).view(torch.uint8)
+
+
+class BlockSparseFlashAttention:
+    """Block-sparse flash attention with the reference constructor and ``forward``.
+
+    Args:
+        block_size: Attention block granularity in tokens; one of {32, 64, 128}.
+        min_sparsity_for_speedup: Below this mask sparsity (full-grid count), ``forward``
+            warns and returns dense SDPA, ignoring the mask (reference behaviour).
+        backend: ``AUTO`` or ``HIP_GFX950`` (the HIP kernels), or ``DENSE_FALLBACK``.
+
+    Raises:
+        ValueError: ``block_size`` or ``min_sparsity_for_speedup`` out of range.
+        KernelError: the requested backend is not available.
+    """
+
+    def __init__(
+        self,
+        block_size: int = 64,
+        min_sparsity_for_speedup: float = 0.5,
+        backend: KernelBackend = KernelBackend.AUTO,
+    ) -> None:
+        if block_size not in VALID_BLOCK_SIZES:
+            raise ValueError(
+                f"block_size must be one of {sorted(VALID_BLOCK_SIZES)}, got {block_size}"
+            )
+        if not 0.0 <= min_sparsity_for_speedup <= 1.0:
+            raise ValueError(
+                f"min_sparsity_for_speedup must be in [0, 1], got {min_sparsity_for_speedup}"
+            )
+        self.block_size = block_size
+        self.min_sparsity_for_speedup = min_sparsity_for_speedup
+        self._available_backends = detect_kernels()
+        if backend == KernelBackend.AUTO:
+            # The HIP backend is selected even if the library is absent, so a missing
+            # build surfaces as a KernelError at the first forward instead of a silent
+            # switch to dense attention.
+            self.backend = KernelBackend.HIP_GFX950
+        elif backend in (KernelBackend.HIP_GFX950, KernelBackend.DENSE_FALLBACK):
+            self.backend = backend
+        else:
+            available_names = [b.name for b in self._available_backends]
+            msg = f"Requested backend {backend.name} is not available. Available: {available_names}"
+            raise KernelError(msg, context={"requested": backend.name, "available": available_names})
+
+    # ------------------------------------------------------------------ prefill
+    def forward(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        block_mask: torch.Tensor,
+        *,
+        causal: bool = True,
+    ) -> torch.Tensor:
+        """Block-sparse attention ``[B, Hq, S, D]`` (reference ``block_sparse_fa.py:361-411``).
+
+        ``k``/``v`` are ``[B, Hkv, S, D]`` with ``Hq % Hkv == 0`` (``Hkv == Hq`` is the
+        reference case). ``block_mask`` is ``[B, Hq, NB, NB]``; with ``causal`` it is
+        AND-ed with the block lower triangle and the diagonal blocks are masked
+        element-wise. Rows with no active block are zero.
+        """
+        self._validate_inputs(q, k, v, block_mask)
+        if self.min_sparsity_for_speedup > 0.0:
+            # The statistics need a device->host sync; with a 0.0 threshold the
+            # comparison below can never fire, so it is skipped.
+            stats = self.compute_sparsity_stats(block_mask)
+            if stats.sparsity_ratio < self.min_sparsity_for_speedup:
+                warnings.warn(
+                    f"Sparsity {stats.sparsity_ratio:.2%} below threshold "
+                    f"{self.min_sparsity_for_speedup:.2%}; using dense fallback.",
+                    stacklevel=2,
+                )
+                return self._dense_fallback(q, k, v, causal)
+        if self.backend == KernelBackend.DENSE_FALLBACK:
+            return self._dense_fallback(q, k, v, causal)
+        return self._hip_forward(q, k, v, block_mask, causal)
+
+    __call__ = forward
+
+    def _validate_inputs(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        block_mask: torch.Tensor,
+    ) -> None:
+        """Reference checks and messages (``block_sparse_fa.py:413-452``), GQA-aware."""
+        if q.ndim != _EXPECTED_TENSOR_NDIM:
+            msg = f"Expected 4D tensors [B, H, S, D], got q.ndim={q.ndim}"
+            raise KernelError(msg, context={"q_shape": list(q.shape)})
+        if k.shape != v.shape or not _kv_compatible(q, k):
+            raise KernelError(
+                "Q, K, V shapes must match",
+                context={"q": list(q.shape), "k": list(k.shape), "v": list(v.shape)},
+            )
+        if not q.is_cuda:
+            raise KernelError("Tensors must be on CUDA device", context={"device": str(q.device)})
+        B, H, S, _D = q.shape
+        num_blocks = math.ceil(S / self.block_size)
+        expected_mask_shape = (B, H, num_blocks, num_blocks)
+        if tuple(block_mask.shape) != expected_mask_shape:
+            raise KernelError(
+                f"block_mask shape mismatch: expected {expected_mask_shape}, "
+                f"got {tuple(block_mask.shape)}",
+                context={
+                    "expected": list(expected_mask_shape),
+                    "got": list(block_mask.shape),
+                    "block_size": self.block_size,
+                },
+            )
+
+    def _hip_forward(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        block_mask: torch.Tensor,
+        causal: bool,
+    ) -> torch.Tensor:
+        """Launch ``tasft_bsfa_prefill_fwd`` on the current stream (replaces ``:454-552``)."""
+        B, H, S, D = q.shape
+        if D not in _VALID_HEAD_DIMS:
+            raise KernelError(
+                f"HIP kernel supports head_dim in {sorted(_VALID_HEAD_DIMS)}, got {D}",
+                context={"head_dim": D, "supported": sorted(_VALID_HEAD_DIMS)},
+            )
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if t.dtype != torch.bfloat16:
+                raise KernelError(
+                    f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
+                    context={"tensor": name, "dtype": str(t.dtype)},
+                )
+            if t.device != q.device:
+                raise KernelError("Q, K, V must be on the same device", context={"device": str(t.device)})
+        lib = _native.load_library()
+        q = _kernel_ready(q)
+        k = _kernel_ready(k)
+        v = _kernel_ready(v)
+        mask = _mask_bytes(block_mask.to(q.device))
+        out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+        scale = 1.0 / math.sqrt(D)
+        status = lib.tasft_bsfa_prefill_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
+            B, H, k.shape[1], S, D, self.block_size,
+            _native.strides(q), _native.strides(k), _native.strides(v), _native.strides(out),
+            _native.strides(mask), scale, 1 if causal else 0, _native.stream_handle(q.device),
+        )
+        _native.check(status, "tasft_bsfa_prefill_fwd", {"shape": [B, H, S, D]})
+        return out
+
+    def _dense_fallback(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        causal: bool,
+    ) -> torch.Tensor:
+        """Dense SDPA ignoring the mask (reference ``block_sparse_fa.py:554-572``)."""
+        gqa = k.shape[1] != q.shape[1]
+        return functional.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa)
+
+    # ------------------------------------------------------------------ decode
+    def forward_decode(
+        self,
+        q: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        block_mask: torch.Tensor,
+        *,
+        kv_lens: torch.Tensor | None = None,
+        num_splits: int | None = None,
+    ) -> torch.Tensor:
+        """Block-sparse decode of one new token per sequence.
+
+        Args:
+            q: ``[B, Hq, 1, D]`` bf16, the new token's queries.
+            k_cache, v_cache: ``[B, Hkv, S_kv, D]`` bf16; the new token's K/V are included.
+            block_mask: ``[B, Hq, 1, ceil(S_kv / block_size)]``; non-zero selects a block.
+            kv_lens: optional ``[B]`` int32 valid lengths (default ``S_kv``).
+            num_splits: split-K factor (default: sized so the launch fills the GPU).
+
+        Returns:
+            ``[B, Hq, 1, D]``: ``softmax(q K_sel^T / sqrt(D)) V_sel`` per head, 0 for a head
+            with no selected block. There is no reference counterpart: reference decode is
+            dense (``tasft/inference/vllm_patch.py:189-196``).
+        """
+        if q.ndim != _EXPECTED_TENSOR_NDIM or q.shape[2] != 1:
+            raise KernelError(
+                f"Expected q of shape [B, H, 1, D], got {tuple(q.shape)}",
+                context={"q_shape": list(q.shape)},
+            )
+        if (
+            k_cache.ndim != _EXPECTED_TENSOR_NDIM
+            or k_cache.shape != v_cache.shape
+            or k_cache.shape[0] != q.shape[0]
+            or k_cache.shape[3] != q.shape[3]
+            or q.shape[1] % k_cache.shape[1] != 0
+        ):
+            raise KernelError(
+                "KV cache shape incompatible with q",
+                context={"q": list(q.shape), "k": list(k_cache.shape), "v": list(v_cache.shape)},
+            )
+        if not q.is_cuda:
+            raise KernelError("Tensors must be on CUDA device", context={"device": str(q.device)})
+        B, H, _, D = q.shape
+        Hkv, S_kv = k_cache.shape[1], k_cache.shape[2]
+        nb = math.ceil(S_kv / self.block_size)
+        if tuple(block_mask.shape) != (B, H, 1, nb):
+            raise KernelError(
+                f"block_mask shape mismatch: expected {(B, H, 1, nb)}, got {tuple(block_mask.shape)}",
+                context={"expected": [B, H, 1, nb], "got": list(block_mask.shape)},
+            )
+        if D not in _VALID_HEAD_DIMS:
+            raise KernelError(
+                f"HIP kernel supports head_dim in {sorted(_VALID_HEAD_DIMS)}, got {D}",
+                context={"head_dim": D},
+            )
+        for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+            if t.dtype != torch.bfloat16:
+                raise KernelError(f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
+                                  context={"tensor": name, "dtype": str(t.dtype)})
+        lib = _native.load_library()
+        if num_splits is None:
+            num_splits = default_decode_splits(B, Hkv, nb)
+        q = q.contiguous()
+        k_cache = _kernel_ready(k_cache)
+        v_cache = _kernel_ready(v_cache)
+        mask = _mask_bytes(block_mask.to(q.device))
+        lens = None
+        if kv_lens is not None:
+            lens = kv_lens.to(device=q.device, dtype=torch.int32).contiguous()
+            if lens.shape != (B,):
+                raise KernelError(f"kv_lens must have shape ({B},), got {tuple(lens.shape)}",
+                                  context={"kv_lens": list(lens.shape)})
+        ws_bytes = lib.tasft_bsfa_decode_workspace_bytes(B, H, D, num_splits)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        out = torch.empty((B, H, 1, D), dtype=q.dtype, device=q.device)
+        status = lib.tasft_bsfa_decode_fwd(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), mask.data_ptr(),
+            _native.ptr(lens), workspace.data_ptr(), ws_bytes, B, H, Hkv, S_kv, D,
+            self.block_size, num_splits,
+            _native.strides(q), _native.strides(k_cache), _native.strides(v_cache),
+            _native.strides(out), _native.strides(mask), 1.0 / math.sqrt(D),
+            _native.stream_handle(q.device),
+        )
+        _native.check(status, "tasft_bsfa_decode_fwd", {"shape": [B, H, S_kv, D]})
+        return out
+
+    # ------------------------------------------------------------------ stats
+    def compute_sparsity_stats(self, block_mask: torch.Tensor) -> SparsityStats:
+        """Full-grid statistics (reference ``block_sparse_fa.py:574-595``; syncs the device)."""
+        total_blocks = block_mask.numel()
+        active_blocks = int(block_mask.sum().item())
+        sparsity_ratio = 1.0 - (active_blocks / max(total_blocks, 1))
+        return SparsityStats(
+            total_blocks=total_blocks,
+            active_blocks=active_blocks,
+            sparsity_ratio=sparsity_ratio,
+            estimated_speedup=self.estimate_speedup(sparsity_ratio),
+        )
+
+    @staticmethod
+    def estimate_speedup(sparsity_ratio: float) -> float:
+        """``1 / max(1e-6, 1 - 0.98 s)``: the reference's model (``block_sparse_fa.py:597-618``)."""
+        gate_overhead = 0.02
+        denominator = 1.0 - sparsity_ratio * (1.0 - gate_overhead)
+        return 1.0 / max(1e-6, denominator)
+
+
+def default_decode_splits(batch: int, num_kv_heads: int, num_blocks: int) -> int:
+    """Split-K factor giving about 2048 decode workgroups (8 per CU on 256 CUs)."""
+    groups = max(1, batch * num_kv_heads)
+    return int(max(1, min(max(1, num_blocks // 4), math.ceil(2048 / groups))))
+
+
+def executed_blocks(block_mask: torch.Tensor, causal: bool = True) -> torch.Tensor:
+    """Number of (query block, key block) tiles the prefill kernel computes (device tensor)."""
+    m = block_mask != 0
+    if causal:
+        nb = m.shape[-1]
+        m = m & torch.ones(nb, nb, dtype=torch.bool, device=m.device).tril()
+    return m.sum()
+
+
+__all__ = [
+    "BlockSparseFlashAttention",
+    "KernelBackend",
+    "SparsityStats",
+    "default_decode_splits",
+    "detect_kernels",
+    "executed_blocks",
+]

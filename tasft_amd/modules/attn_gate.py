@@ -1,0 +1,298 @@
+"""AttnGate on MI355X: block mean-pool -> pairwise MLP -> sigmoid -> threshold.
+
+Mirrors ``tasft.modules.attn_gate`` (reference ``tasft/modules/attn_gate.py:30-314``):
+same constructor and defaults, the same parameters and state-dict keys
+(``gate_proj_in.weight/.bias``, ``gate_proj_out.weight``) created and initialised in the
+same order, the same validation order and messages, and the same ``GateOutput`` fields.
+
+Inference (no autograd) runs the fused HIP kernels of ``libtasft_amd.so``: one pass over
+Q and K for the pooling (GQA-native, K pooled per KV head) and one pairwise kernel that
+keeps logits, sigmoid and threshold in fp32 — gate scores cluster within ~1e-3 of 0.5,
+below one bf16 ulp, so the reference's bf16 cast of the gate would move mask bits.
+
+Additive, keyword-compatible extensions: ``k`` may have ``Hkv`` heads (``Hq % Hkv == 0``);
+``threshold`` may be a per-head tensor ``[Hq]``; ``return_logits=True`` adds fp32 logits.
+Differences: ``soft_scores`` are fp32 whatever the module dtype; ``sparsity_ratio`` is
+computed from a device counter on first access instead of a sync inside ``forward``.
+
+When autograd is needed (gate training), ``forward`` evaluates the same formula with
+differentiable torch operations on the GPU; that path is the training side, not the
+inference kernel path.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from tasft_amd import _native
+from tasft_amd.exceptions import KernelError, ValidationError
+
+
+class GateOutput:
+    """Gate result (reference ``attn_gate.py:30-46``); immutable after construction.
+
+    Attributes:
+        soft_scores: ``[B, H, NB_q, NB_k]`` fp32 scores in [0, 1] (0 above the block
+            diagonal when causal).
+        hard_mask: ``[B, H, NB_q, NB_k]`` bool, ``soft_scores >= threshold``.
+        sparsity_ratio: fraction of False entries over the full grid (reference
+            ``attn_gate.py:277``); read lazily from a device counter.
+        num_blocks_q, num_blocks_k: block grid size.
+        logits: fp32 pre-sigmoid logits when requested, else None.
+    """
+
+    __slots__ = ("soft_scores", "hard_mask", "num_blocks_q", "num_blocks_k", "logits",
+                 "_sparsity", "_active", "_total")
+
+    def __init__(
+        self,
+        soft_scores: torch.Tensor,
+        hard_mask: torch.Tensor,
+        sparsity_ratio: float | None = None,
+        num_blocks_q: int = 0,
+        num_blocks_k: int = 0,
+        *,
+        logits: torch.Tensor | None = None,
+        active_count: torch.Tensor | None = None,
+    ) -> None:
+        if sparsity_ratio is None and active_count is None:
+            raise ValueError("GateOutput needs sparsity_ratio or active_count")
+        init = object.__setattr__
+        init(self, "soft_scores", soft_scores)
+        init(self, "hard_mask", hard_mask)
+        init(self, "num_blocks_q", num_blocks_q)
+        init(self, "num_blocks_k", num_blocks_k)
+        init(self, "logits", logits)
+        init(self, "_sparsity", None if sparsity_ratio is None else float(sparsity_ratio))
+        init(self, "_active", active_count)
+        init(self, "_total", hard_mask.numel())
+
+    @property
+    def sparsity_ratio(self) -> float:
+        if self._sparsity is None:
+            active = int(self._active.item())
+            object.__setattr__(self, "_sparsity", 1.0 - active / max(self._total, 1))
+        return self._sparsity
+
+    def __setattr__(self, name: str, value: Any) -> None:
+        raise dataclasses.FrozenInstanceError(f"cannot assign to field '{name}'")
+
+    def __delattr__(self, name: str) -> None:
+        raise dataclasses.FrozenInstanceError(f"cannot delete field '{name}'")
+
+    def __repr__(self) -> str:
+        return (f"GateOutput(shape={tuple(self.hard_mask.shape)}, "
+                f"num_blocks_q={self.num_blocks_q}, num_blocks_k={self.num_blocks_k})")
+
+
+class AttnGate(nn.Module):
+    """Learnable block-importance predictor (reference ``attn_gate.py:49-311``)."""
+
+    def __init__(
+        self,
+        num_heads: int,
+        head_dim: int,
+        block_size: int = 64,
+        gate_hidden_dim: int | None = None,
+        default_threshold: float = 0.5,
+        is_causal: bool = True,
+    ) -> None:
+        super().__init__()
+        if num_heads <= 0:
+            raise ValidationError(f"num_heads must be positive, got {num_heads}",
+                                  context={"num_heads": num_heads})
+        if head_dim <= 0:
+            raise ValidationError(f"head_dim must be positive, got {head_dim}",
+                                  context={"head_dim": head_dim})
+        if block_size <= 0:
+            raise ValidationError(f"block_size must be positive, got {block_size}",
+                                  context={"block_size": block_size})
+        if not 0.0 <= default_threshold <= 1.0:
+            raise ValidationError(f"default_threshold must be in [0, 1], got {default_threshold}",
+                                  context={"default_threshold": default_threshold})
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.block_size = block_size
+        self.default_threshold = default_threshold
+        self.is_causal = is_causal
+        hidden = gate_hidden_dim if gate_hidden_dim is not None else max(32, head_dim // 4)
+        self.gate_hidden_dim = hidden
+        # Same modules in the same order as the reference, so seeded construction draws
+        # the same random numbers (nn.Linear default init, then _init_weights).
+        self.gate_proj_in = nn.Linear(2 * head_dim, hidden, bias=True)
+        self.gate_proj_out = nn.Linear(hidden, 1, bias=False)
+        self._init_weights()
+
+    def _init_weights(self) -> None:
+        """Xavier-uniform W_in, zero b_in, N(0, 0.01) W_out (reference ``attn_gate.py:140-149``)."""
+        nn.init.xavier_uniform_(self.gate_proj_in.weight)
+        nn.init.zeros_(self.gate_proj_in.bias)
+        nn.init.normal_(self.gate_proj_out.weight, std=0.01)
+
+    def _pool_to_blocks(self, x: torch.Tensor) -> torch.Tensor:
+        """Zero-padded block mean ``[B, H, S, D] -> [B, H, NB, D]`` (reference ``:151-175``).
+
+        Used by the differentiable training path; the inference kernel pools on device.
+        """
+        B, H, S, D = x.shape
+        pad = (self.block_size - S % self.block_size) % self.block_size
+        if pad > 0:
+            x = F.pad(x, (0, 0, 0, pad))
+        nb = x.shape[2] // self.block_size
+        return x.view(B, H, nb, self.block_size, D).mean(dim=3)
+
+    def _validate(self, q: torch.Tensor, k: torch.Tensor) -> None:
+        """Reference checks and messages (``attn_gate.py:201-239``), GQA-aware."""
+        if q.ndim != 4:
+            raise ValidationError(f"Expected 4D Q tensor [B, H, S, D], got ndim={q.ndim}",
+                                  context={"q_shape": list(q.shape)})
+        if k.ndim != 4:
+            raise ValidationError(f"Expected 4D K tensor [B, H, S, D], got ndim={k.ndim}",
+                                  context={"k_shape": list(k.shape)})
+        B, H, S, D = q.shape
+        same = k.shape == q.shape
+        gqa = (k.shape[0] == B and k.shape[2] == S and k.shape[3] == D and k.shape[1] > 0
+               and H % k.shape[1] == 0)
+        if not (same or gqa):
+            raise ValidationError(f"Q and K must have same shape, got {q.shape} vs {k.shape}",
+                                  context={"q_shape": list(q.shape), "k_shape": list(k.shape)})
+        if self.num_heads != H:
+            raise ValidationError(f"Expected {self.num_heads} heads, got {H}",
+                                  context={"expected_heads": self.num_heads, "actual_heads": H})
+        if self.head_dim != D:
+            raise ValidationError(f"Expected head_dim={self.head_dim}, got {D}",
+                                  context={"expected_dim": self.head_dim, "actual_dim": D})
+        if S == 0:
+            raise ValidationError("Sequence length must be > 0", context={"seq_len": S})
+
+    def _needs_grad(self, q: torch.Tensor, k: torch.Tensor) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        return q.requires_grad or k.requires_grad or any(p.requires_grad for p in self.parameters())
+
+    def forward(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        threshold: float | torch.Tensor | None = None,
+        *,
+        return_logits: bool = False,
+        force_diagonal: bool = False,
+    ) -> GateOutput:
+        """Block scores, hard mask and sparsity for ``q [B,H,S,D]``, ``k [B,H or Hkv,S,D]``.
+
+        ``force_diagonal=True`` sets the diagonal blocks of ``hard_mask`` whatever their
+        score (every query block then attends at least to itself).
+        """
+        tau = threshold if threshold is not None else self.default_threshold
+        self._validate(q, k)
+        if not q.is_cuda or not k.is_cuda:
+            raise KernelError("AttnGate runs on a ROCm device; got a CPU tensor",
+                              context={"device": str(q.device)})
+        if self._needs_grad(q, k):
+            return self._forward_autograd(q, k, tau, return_logits, force_diagonal)
+        return self._forward_hip(q, k, tau, return_logits, force_diagonal)
+
+    def _thresholds(self, tau: float | torch.Tensor, device: torch.device) -> torch.Tensor:
+        if isinstance(tau, torch.Tensor):
+            t = tau.to(device=device, dtype=torch.float32).reshape(-1)
+            if t.numel() == 1:
+                return t.expand(self.num_heads).contiguous()
+            if t.numel() != self.num_heads:
+                raise ValidationError(
+                    f"threshold tensor must have {self.num_heads} entries, got {t.numel()}",
+                    context={"threshold_shape": list(tau.shape)})
+            return t.contiguous()
+        return torch.full((self.num_heads,), float(tau), dtype=torch.float32, device=device)
+
+    def _forward_hip(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
+                     return_logits: bool, force_diagonal: bool) -> GateOutput:
+        B, H, S, D = q.shape
+        Hkv = k.shape[1]
+        for name, t in (("q", q), ("k", k)):
+            if t.dtype != torch.bfloat16:
+                raise KernelError(f"AttnGate kernel reads bfloat16; {name} is {t.dtype}",
+                                  context={"tensor": name, "dtype": str(t.dtype)})
+        if D % 8 != 0 or D > 256:
+            raise KernelError(f"AttnGate kernel supports head_dim multiple of 8 up to 256, got {D}",
+                              context={"head_dim": D})
+        lib = _native.load_library()
+        dev = q.device
+        q = q if (q.stride(-1) == 1 and all(s % 8 == 0 for s in q.stride()[:-1])) else q.contiguous()
+        k = k if (k.stride(-1) == 1 and all(s % 8 == 0 for s in k.stride()[:-1])) else k.contiguous()
+        w_in = self.gate_proj_in.weight.detach().to(device=dev, dtype=torch.float32).contiguous()
+        b_in = self.gate_proj_in.bias.detach().to(device=dev, dtype=torch.float32).contiguous()
+        w_out = self.gate_proj_out.weight.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        taus = self._thresholds(tau, dev)
+        nb = math.ceil(S / self.block_size)
+        hidden = self.gate_hidden_dim
+        soft = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev)
+        mask = torch.empty((B, H, nb, nb), dtype=torch.uint8, device=dev)
+        logits = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev) if return_logits else None
+        active = torch.empty((1,), dtype=torch.int64, device=dev)
+        ws_bytes = lib.tasft_gate_workspace_bytes(B, H, Hkv, S, self.block_size, hidden)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        status = lib.tasft_gate_fwd(
+            q.data_ptr(), k.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(),
+            taus.data_ptr(), soft.data_ptr(), _native.ptr(logits), mask.data_ptr(),
+            active.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, Hkv, S, D,
+            self.block_size, hidden, _native.strides(q), _native.strides(k),
+            (1 if self.is_causal else 0) | (2 if force_diagonal else 0), _native.stream_handle(dev),
+        )
+        _native.check(status, "tasft_gate_fwd", {"shape": [B, H, S, D]})
+        return GateOutput(soft_scores=soft, hard_mask=mask.view(torch.bool), num_blocks_q=nb,
+                          num_blocks_k=nb, logits=logits, active_count=active)
+
+    def _forward_autograd(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
+                          return_logits: bool, force_diagonal: bool) -> GateOutput:
+        """Differentiable evaluation of the same formula for gate training.
+
+        Uses ``W_in . cat(x, y) = W_q x + W_k y`` so no ``[B,H,NB,NB,2D]`` tensor is built.
+        """
+        B, H, S, D = q.shape
+        Hkv = k.shape[1]
+        w = self.gate_proj_in.weight.float()
+        qb = self._pool_to_blocks(q.float())
+        kb = self._pool_to_blocks(k.float())
+        if Hkv != H:
+            kb = kb.repeat_interleave(H // Hkv, dim=1)
+        uq = qb @ w[:, :D].t() + self.gate_proj_in.bias.float()
+        uk = kb @ w[:, D:].t()
+        hidden = F.relu(uq.unsqueeze(3) + uk.unsqueeze(2))
+        logits = (hidden @ self.gate_proj_out.weight.float().t()).squeeze(-1)
+        soft = torch.sigmoid(logits)
+        nb = soft.shape[2]
+        if self.is_causal:
+            soft = soft * torch.ones(nb, nb, dtype=torch.bool, device=soft.device).tril()
+        taus = self._thresholds(tau, soft.device).view(1, H, 1, 1)
+        hard = soft >= taus
+        if force_diagonal:
+            hard = hard | torch.eye(nb, dtype=torch.bool, device=soft.device)
+        active = hard.sum().reshape(1)
+        return GateOutput(soft_scores=soft, hard_mask=hard, num_blocks_q=nb, num_blocks_k=nb,
+                          logits=logits if return_logits else None, active_count=active)
+
+    def compute_sparsity(self, soft_scores: torch.Tensor, threshold: float) -> float:
+        """Fraction of scores below ``threshold`` (reference ``attn_gate.py:287-297``)."""
+        return 1.0 - (soft_scores >= threshold).float().mean().item()
+
+    @property
+    def num_parameters(self) -> int:
+        """Trainable parameter count (reference ``attn_gate.py:299-302``)."""
+        return sum(p.numel() for p in self.parameters() if p.requires_grad)
+
+    def extra_repr(self) -> str:
+        return (
+            f"num_heads={self.num_heads}, head_dim={self.head_dim}, "
+            f"block_size={self.block_size}, gate_hidden_dim={self.gate_hidden_dim}, "
+            f"default_threshold={self.default_threshold}, "
+            f"is_causal={self.is_causal}, params={self.num_parameters}"
+        )
+
+
+__all__ = ["AttnGate", "GateOutput"]

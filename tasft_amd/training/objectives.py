@@ -1,0 +1,113 @@
+"""Gate distillation target: softmax of block-max-pooled attention scores.
+
+Two entry points:
+
+* ``TASFTObjective.compute_gate_target(attn_scores, block_size)`` keeps the reference
+  API and semantics (``tasft/training/objectives.py:128-185``) for callers that already
+  hold a dense ``[B, H, S, S]`` score tensor: NaN/+inf rejection, -inf padding,
+  ``max_pool2d``, softmax over the flat block grid.
+* ``gate_target_from_qk(q, k, ...)`` is the MI355X kernel path: it takes Q and K and never
+  forms the score tensor. The HIP kernel computes each 64x64 block maximum of
+  ``Q K^T * scale`` with bf16 MFMA (causal: -inf above the diagonal), then normalises.
+  It replaces the score producer ``tasft/modules/tasft_attention.py:426-458`` followed by
+  ``compute_gate_target``; ``normalize="row"`` gives the per-row variant and
+  ``temperature``/``clamp`` the variant of ``tasft/modules/tasft_attention.py:272-290``.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from tasft_amd import _native
+from tasft_amd.exceptions import KernelError, NaNDetectedError
+
+_NORMALIZE = {"flat": 0, "row": 1, "none": 2}
+
+
+class TASFTObjective:
+    """Holder of the gate-target operator (the loss algebra of the reference is out of scope)."""
+
+    @staticmethod
+    def compute_gate_target(attn_scores: torch.Tensor, block_size: int) -> torch.Tensor:
+        """Reference dense path on a given score tensor (``objectives.py:128-185``)."""
+        has_nan = bool(torch.isnan(attn_scores).any())
+        has_pos_inf = bool((attn_scores == float("inf")).any())
+        if has_nan or has_pos_inf:
+            raise NaNDetectedError(
+                f"Non-finite values detected in attn_scores: NaN={has_nan}, Inf={has_pos_inf}",
+                context={
+                    "tensor_name": "attn_scores",
+                    "has_nan": has_nan,
+                    "has_inf": has_pos_inf,
+                    "shape": list(attn_scores.shape),
+                    "dtype": str(attn_scores.dtype),
+                },
+            )
+        b, h, s_q, s_k = attn_scores.shape
+        if block_size <= 0:
+            raise ValueError(f"block_size must be > 0, got {block_size}")
+        pad_q = (block_size - s_q % block_size) % block_size
+        pad_k = (block_size - s_k % block_size) % block_size
+        if pad_q > 0 or pad_k > 0:
+            attn_scores = F.pad(attn_scores, (0, pad_k, 0, pad_q), value=-math.inf)
+        pooled = F.max_pool2d(attn_scores, kernel_size=block_size, stride=block_size)
+        nb_q, nb_k = pooled.shape[2], pooled.shape[3]
+        target = F.softmax(pooled.reshape(b, h, nb_q * nb_k), dim=-1)
+        return target.reshape(b, h, nb_q, nb_k)
+
+
+def gate_target_from_qk(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    block_size: int = 64,
+    *,
+    causal: bool = True,
+    scale: float | None = None,
+    normalize: str = "flat",
+    temperature: float = 1.0,
+    clamp: float | None = None,
+) -> torch.Tensor:
+    """Gate target ``[B, Hq, NB, NB]`` fp32 from ``q [B,Hq,S,D]`` and ``k [B,Hkv,S,D]`` (bf16).
+
+    Args:
+        block_size: pooling block (32, 64 or 128).
+        causal: add the ``triu(-inf, 1)`` mask of ``tasft_attention.py:434-443``.
+        scale: score scale, default ``1/sqrt(D)`` (``tasft_attention.py:427``).
+        normalize: ``"flat"`` softmax over all NB*NB blocks of a head (reference trainer),
+            ``"row"`` over the key blocks of each query block, ``"none"`` raw block maxima.
+        temperature: divide pooled maxima by this before the softmax.
+        clamp: if set, clamp finite maxima to ``[-clamp, clamp]`` first.
+    """
+    if q.ndim != 4 or k.ndim != 4:
+        raise KernelError("Expected 4D q and k [B, H, S, D]", context={"q": list(q.shape), "k": list(k.shape)})
+    B, H, S, D = q.shape
+    if k.shape[0] != B or k.shape[2] != S or k.shape[3] != D or H % k.shape[1] != 0:
+        raise KernelError("q and k shapes are incompatible", context={"q": list(q.shape), "k": list(k.shape)})
+    if not q.is_cuda or not k.is_cuda:
+        raise KernelError("Tensors must be on CUDA device", context={"device": str(q.device)})
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise KernelError("gate target kernel computes in bfloat16",
+                          context={"q": str(q.dtype), "k": str(k.dtype)})
+    if normalize not in _NORMALIZE:
+        raise ValueError(f"normalize must be one of {sorted(_NORMALIZE)}, got {normalize!r}")
+    if not temperature > 0.0:
+        raise ValueError(f"temperature must be > 0, got {temperature}")
+    lib = _native.load_library()
+    q = q if (q.stride(-1) == 1 and all(s % 8 == 0 for s in q.stride()[:-1])) else q.contiguous()
+    k = k if (k.stride(-1) == 1 and all(s % 8 == 0 for s in k.stride()[:-1])) else k.contiguous()
+    nb = math.ceil(S / block_size)
+    out = torch.empty((B, H, nb, nb), dtype=torch.float32, device=q.device)
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    status = lib.tasft_gate_target_fwd(
+        q.data_ptr(), k.data_ptr(), out.data_ptr(), B, H, k.shape[1], S, D, block_size,
+        _native.strides(q), _native.strides(k), sc, 1 if causal else 0, _NORMALIZE[normalize],
+        float(temperature), float(clamp) if clamp is not None else 0.0,
+        _native.stream_handle(q.device),
+    )
+    _native.check(status, "tasft_gate_target_fwd", {"shape": [B, H, S, D]})
+    return out
+
+
+__all__ = ["TASFTObjective", "gate_target_from_qk"]

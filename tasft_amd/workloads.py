@@ -1,0 +1,170 @@
+"""Seeded synthetic inputs for the benchmark configurations of the block-sparse path.
+
+Every tensor is drawn on the CPU in fp32 from ``torch.Generator().manual_seed(seed)``,
+scaled by 1/sqrt(128) and rounded to bf16, so the GPU and a CPU checker see identical
+values. Tensor seeds are ``1000 + k`` and mask seeds ``2000 + k`` for config ``k``.
+
+Config numbering (1-based) follows the benchmark list:
+  1  prefill parity case: B=1, S=2048, 32/8 heads, D=128, bs=64, Bernoulli(0.2) lower blocks
+  2  gate + prefill, Llama-3-8B: B=4, S=8192, 32/8 heads, gate hidden 128, 80% causal sparsity
+  3  decode: B=64, S_kv=32768, 32/8 heads, 51 of 512 blocks per KV head (sink + recent kept)
+  4  Qwen-2.5-7B prefill: B=2, S=16384, 28/4 heads, band 8 + 4 global + random, s_h~U(.5,.9)
+  5  gate target: B=4, S=4096, 32/8 heads, causal
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+HEAD_DIM = 128
+BLOCK = 64
+
+
+@dataclass(frozen=True)
+class Shape:
+    batch: int
+    q_heads: int
+    kv_heads: int
+    seq: int
+    head_dim: int = HEAD_DIM
+    block: int = BLOCK
+
+    @property
+    def nb(self) -> int:
+        return math.ceil(self.seq / self.block)
+
+
+CONFIG_SHAPES = {
+    1: Shape(1, 32, 8, 2048),
+    2: Shape(4, 32, 8, 8192),
+    3: Shape(64, 32, 8, 32768),
+    4: Shape(2, 28, 4, 16384),
+    5: Shape(4, 32, 8, 4096),
+}
+
+
+def randn_bf16(shape: tuple[int, ...], seed: int, scale: float = 1.0 / math.sqrt(HEAD_DIM)) -> torch.Tensor:
+    """N(0,1)*scale in fp32 from a seeded CPU generator, rounded to bf16 (CPU tensor)."""
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g, dtype=torch.float32) * scale).to(torch.bfloat16)
+
+
+def qkv(shape: Shape, seed: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Q [B,Hq,S,D], K and V [B,Hkv,S,D] bf16 on the CPU; K and V use seeds seed+1, seed+2."""
+    q = randn_bf16((shape.batch, shape.q_heads, shape.seq, shape.head_dim), seed)
+    k = randn_bf16((shape.batch, shape.kv_heads, shape.seq, shape.head_dim), seed + 1)
+    v = randn_bf16((shape.batch, shape.kv_heads, shape.seq, shape.head_dim), seed + 2)
+    return q, k, v
+
+
+def bernoulli_causal_mask(shape: Shape, keep: float, seed: int) -> torch.Tensor:
+    """Config 1 mask: diagonal kept, strictly-lower blocks kept with probability ``keep``."""
+    g = torch.Generator().manual_seed(seed)
+    nb = shape.nb
+    r = torch.rand((shape.batch, shape.q_heads, nb, nb), generator=g)
+    lower = torch.ones(nb, nb, dtype=torch.bool).tril(-1)
+    return ((r < keep) & lower) | torch.eye(nb, dtype=torch.bool)
+
+
+def qwen_mask(shape: Shape, seed: int, band: int = 8, n_global: int = 4,
+              sparsity_range: tuple[float, float] = (0.5, 0.9)) -> tuple[torch.Tensor, torch.Tensor]:
+    """Config 4 mask and the per-(b,h) target sparsity.
+
+    Per head: a band of ``band`` blocks (diagonal + ``band-1`` previous), ``n_global`` seeded
+    key-block columns, then random extra causal blocks until the active count reaches
+    ``(1 - s_h) * NB(NB+1)/2`` with ``s_h ~ U(sparsity_range)``. Band and global blocks
+    are always kept, even if they exceed the target.
+    """
+    g = torch.Generator().manual_seed(seed)
+    nb = shape.nb
+    causal = torch.ones(nb, nb, dtype=torch.bool).tril()
+    idx = torch.arange(nb)
+    band_m = (idx[:, None] - idx[None, :] >= 0) & (idx[:, None] - idx[None, :] < band)
+    n_causal = nb * (nb + 1) // 2
+    masks = torch.zeros((shape.batch, shape.q_heads, nb, nb), dtype=torch.bool)
+    s_h = torch.empty((shape.batch, shape.q_heads))
+    lo, hi = sparsity_range
+    for b in range(shape.batch):
+        for h in range(shape.q_heads):
+            s = lo + (hi - lo) * torch.rand((), generator=g).item()
+            s_h[b, h] = s
+            cols = torch.randperm(nb, generator=g)[:n_global]
+            m = band_m.clone()
+            m[:, cols] = True
+            m &= causal
+            target = int(round((1.0 - s) * n_causal))
+            have = int(m.sum())
+            if target > have:
+                cand = torch.nonzero(causal & ~m, as_tuple=False)
+                pick = cand[torch.randperm(cand.shape[0], generator=g)[: target - have]]
+                m[pick[:, 0], pick[:, 1]] = True
+            masks[b, h] = m
+    return masks, s_h
+
+
+def decode_mask(shape: Shape, keep_blocks: int, seed: int) -> torch.Tensor:
+    """Config 3 mask ``[B, Hq, 1, NB]``: per KV head, ``keep_blocks`` blocks including block 0
+    (attention sink) and the last block (most recent tokens); the selection is shared by
+    the query heads of the KV head."""
+    g = torch.Generator().manual_seed(seed)
+    nb = shape.nb
+    grp = shape.q_heads // shape.kv_heads
+    m = torch.zeros((shape.batch, shape.kv_heads, nb), dtype=torch.bool)
+    for b in range(shape.batch):
+        for kh in range(shape.kv_heads):
+            rest = 1 + torch.randperm(nb - 2, generator=g)[: keep_blocks - 2]
+            m[b, kh, 0] = True
+            m[b, kh, nb - 1] = True
+            m[b, kh, rest] = True
+    return m.repeat_interleave(grp, dim=1).unsqueeze(2)
+
+
+def gate_params(hidden: int, head_dim: int, seed: int) -> dict[str, torch.Tensor]:
+    """AttnGate parameters initialised as the reference does (attn_gate.py:135-149) from ``seed``."""
+    torch.manual_seed(seed)
+    lin_in = torch.nn.Linear(2 * head_dim, hidden, bias=True)
+    lin_out = torch.nn.Linear(hidden, 1, bias=False)
+    torch.nn.init.xavier_uniform_(lin_in.weight)
+    torch.nn.init.zeros_(lin_in.bias)
+    torch.nn.init.normal_(lin_out.weight, std=0.01)
+    return {
+        "gate_proj_in.weight": lin_in.weight.detach().clone(),
+        "gate_proj_in.bias": lin_in.bias.detach().clone(),
+        "gate_proj_out.weight": lin_out.weight.detach().clone(),
+    }
+
+
+def per_head_threshold(soft: torch.Tensor, keep_causal: float) -> torch.Tensor:
+    """Per-head tau so that, with the diagonal forced on, ``keep_causal`` of the causal
+    blocks of each head (pooled over the batch) are active.
+
+    ``soft`` is ``[B, H, NB, NB]`` fp32. Off-diagonal causal scores of head h over all
+    batches are ranked; tau_h is the score of rank ``round(keep*n_causal) - NB`` per batch.
+    """
+    B, H, nb, _ = soft.shape
+    off = torch.ones(nb, nb, dtype=torch.bool, device=soft.device).tril(-1)
+    n_causal = nb * (nb + 1) // 2
+    k_off = max(1, int(round(keep_causal * n_causal)) - nb)
+    taus = torch.empty(H, dtype=torch.float32, device=soft.device)
+    for h in range(H):
+        vals = soft[:, h][:, off].reshape(-1)
+        kth = min(vals.numel(), k_off * B)
+        taus[h] = torch.topk(vals, kth).values[-1]
+    return taus
+
+
+__all__ = [
+    "BLOCK",
+    "CONFIG_SHAPES",
+    "HEAD_DIM",
+    "Shape",
+    "bernoulli_causal_mask",
+    "decode_mask",
+    "gate_params",
+    "per_head_threshold",
+    "qkv",
+    "qwen_mask",
+    "randn_bf16",
+]

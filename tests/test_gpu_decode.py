@@ -1,0 +1,97 @@
+"""Split-K decode parity: HIP vs the CPU oracle, and vs the prefill kernel's last row."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_bf16, require_gpu, to_np
+from oracle import tasft_oracle as orc
+from tasft_amd import workloads as wl
+from tasft_amd.kernels import BlockSparseFlashAttention
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode(q, kc, vc, mask, bs, kv_lens=None, num_splits=None):
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward_decode(q, kc, vc, mask, kv_lens=kv_lens, num_splits=num_splits)
+    torch.cuda.synchronize()
+    return out
+
+
+CASES = [
+    # B, Hq, Hkv, S_kv, D, bs, density, splits
+    (3, 8, 2, 1000, 128, 64, 0.3, None),
+    (2, 4, 4, 640, 128, 64, 0.5, 1),        # MHA, single split
+    (2, 7, 1, 777, 128, 64, 0.25, 3),       # G=7, ragged, odd split count
+    (1, 8, 8, 300, 64, 32, 0.4, 64),        # D=64, bs=32, more splits than blocks
+    (2, 8, 2, 1024, 128, 128, 0.5, None),   # bs=128
+    (4, 32, 8, 4096, 128, 64, 0.1, None),   # config-3 grouping at a smaller cache
+]
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "density", "splits"), CASES)
+def test_decode_matches_oracle(B, Hq, Hkv, S, D, bs, density, splits):
+    dev = require_gpu()
+    seed = 100 + S
+    q = wl.randn_bf16((B, Hq, 1, D), seed)
+    kc = wl.randn_bf16((B, Hkv, S, D), seed + 1)
+    vc = wl.randn_bf16((B, Hkv, S, D), seed + 2)
+    nb = math.ceil(S / bs)
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.rand((B, Hq, 1, nb), generator=g) < density  # independent per query head
+    mask[0, 0] = False  # a head with nothing selected -> exact 0
+    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), bs, num_splits=splits)
+    assert (out[0, 0].cpu() == 0).all()
+    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), bs)
+    assert_close_bf16(out, ref, f"decode {B}x{Hq}/{Hkv}x{S} bs={bs} splits={splits}")
+
+
+def test_decode_kv_lens():
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs = 4, 8, 2, 700, 128, 64
+    q = wl.randn_bf16((B, Hq, 1, D), 7)
+    kc = wl.randn_bf16((B, Hkv, S, D), 8)
+    vc = wl.randn_bf16((B, Hkv, S, D), 9)
+    nb = math.ceil(S / bs)
+    mask = torch.rand((B, Hq, 1, nb), generator=torch.Generator().manual_seed(7)) < 0.6
+    lens = torch.tensor([700, 1, 64, 333], dtype=torch.int32)
+    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), bs, kv_lens=lens.to(dev))
+    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), bs, kv_lens=lens.numpy())
+    assert_close_bf16(out, ref, "decode kv_lens")
+
+
+def test_decode_equals_prefill_last_row():
+    """The decode of token S-1 equals row S-1 of the prefill under the same mask row."""
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs = 2, 8, 2, 960, 128, 64
+    q, k, v = wl.qkv(wl.Shape(B, Hq, Hkv, S, D), 55)
+    nb = S // bs
+    row = torch.rand((B, Hq, 1, nb), generator=torch.Generator().manual_seed(55)) < 0.4
+    row[..., nb - 1] = True
+    full = torch.zeros((B, Hq, nb, nb), dtype=torch.bool)
+    full[:, :, nb - 1, :] = row[:, :, 0, :]
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    pre = bsfa.forward(qd, kd, vd, full.to(dev), causal=True)
+    dec = bsfa.forward_decode(qd[:, :, S - 1 : S].contiguous(), kd, vd, row.to(dev))
+    torch.cuda.synchronize()
+    diff = (pre[:, :, S - 1].float() - dec[:, :, 0].float()).abs()
+    assert float(diff.max()) <= 1e-2, f"decode vs prefill last row: {float(diff.max())}"
+
+
+def test_config3_geometry_shared_kv_selection():
+    """Config-3 selection (51 of 512 blocks per KV head, sink + recent kept) at B=4."""
+    dev = require_gpu()
+    shape = wl.Shape(4, 32, 8, 32768)
+    q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1003)
+    kc = wl.randn_bf16((shape.batch, shape.kv_heads, shape.seq, shape.head_dim), 1004)
+    vc = wl.randn_bf16((shape.batch, shape.kv_heads, shape.seq, shape.head_dim), 1005)
+    mask = wl.decode_mask(shape, 51, 2003)
+    assert int(mask[0, 0, 0].sum()) == 51 and bool(mask[0, 0, 0, 0]) and bool(mask[0, 0, 0, -1])
+    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), shape.block)
+    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), shape.block)
+    assert_close_bf16(out, ref, "config-3 geometry")

@@ -1,0 +1,147 @@
+"""Fused AttnGate parity: HIP logits vs the oracle, and bit-exact masks from identical logits.
+
+Bar (north star): masks bit-exact when computed from identical fp32 logits, excluding
+scores within 1e-6 of the threshold; logits compared separately with a tolerance.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import require_gpu, to_np
+from oracle import tasft_oracle as orc
+from tasft_amd import workloads as wl
+from tasft_amd.modules import AttnGate
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL = 1e-5
+LOGIT_RTOL = 1e-4
+TAU_BAND = 1e-6
+
+
+def _gate(H, D, bs, hidden, causal=True, seed=0):
+    torch.manual_seed(seed)
+    return AttnGate(num_heads=H, head_dim=D, block_size=bs, gate_hidden_dim=hidden, is_causal=causal)
+
+
+def _params(gate):
+    return (gate.gate_proj_in.weight.detach().numpy(), gate.gate_proj_in.bias.detach().numpy(),
+            gate.gate_proj_out.weight.detach().numpy())
+
+
+def _check(gate, q, k, tau, causal, force_diagonal=False):
+    dev = require_gpu()
+    gd = gate.to(dev)
+    with torch.no_grad():
+        out = gd(q.to(dev), k.to(dev), threshold=tau, return_logits=True, force_diagonal=force_diagonal)
+    torch.cuda.synchronize()
+    gate.cpu()
+    w_in, b_in, w_out = _params(gate)
+    ref_logits = orc.gate_logits(to_np(q), to_np(k), w_in, b_in, w_out, gate.block_size, dtype=np.float64)
+    logits = to_np(out.logits)
+    np.testing.assert_allclose(logits, ref_logits, rtol=LOGIT_RTOL, atol=LOGIT_ATOL)
+    taus = tau.cpu().numpy() if isinstance(tau, torch.Tensor) else tau
+    soft_ref, hard_ref = orc.threshold_mask(logits, taus, causal)
+    if force_diagonal:
+        hard_ref = hard_ref | np.eye(hard_ref.shape[-1], dtype=bool)
+    soft = to_np(out.soft_scores)
+    np.testing.assert_allclose(soft, soft_ref, rtol=0, atol=2e-7)
+    hard = out.hard_mask.cpu().numpy()
+    t = np.asarray(taus, dtype=np.float32)
+    t = t.reshape(1, -1, 1, 1) if t.ndim == 1 else t
+    decisive = np.abs(soft_ref - t) > TAU_BAND
+    if force_diagonal:
+        decisive |= np.eye(hard.shape[-1], dtype=bool)
+    assert np.array_equal(hard[decisive], hard_ref[decisive]), "hard mask differs from identical logits"
+    if causal:
+        up = np.triu(np.ones(soft.shape[-2:], bool), 1)
+        assert (soft[..., up] == 0.0).all()
+    assert out.sparsity_ratio == pytest.approx(1.0 - hard.mean(), abs=1e-9)
+    return out
+
+
+CASES = [
+    # B, Hq, Hkv, S, D, bs, hidden, causal
+    (2, 4, 4, 512, 128, 64, 32, True),
+    (1, 8, 2, 1000, 128, 64, 128, True),   # GQA, ragged (padded last block)
+    (2, 4, 4, 64, 32, 8, 32, True),        # reference test geometry (small_gate)
+    (1, 4, 4, 30, 16, 8, 32, False),       # non-causal, ragged
+    (1, 8, 8, 256, 64, 16, 48, True),      # odd hidden size
+    (1, 2, 1, 777, 128, 48, 64, True),     # block size outside {32,64,128}
+]
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "hidden", "causal"), CASES)
+def test_gate_matches_oracle(B, Hq, Hkv, S, D, bs, hidden, causal):
+    gate = _gate(Hq, D, bs, hidden, causal, seed=S)
+    q = wl.randn_bf16((B, Hq, S, D), S, scale=1.0)
+    k = wl.randn_bf16((B, Hkv, S, D), S + 1, scale=1.0)
+    _check(gate, q, k, 0.5, causal)
+
+
+def test_threshold_edges_and_per_head_tau():
+    gate = _gate(4, 32, 8, 32)
+    q = wl.randn_bf16((2, 4, 32, 32), 1, scale=1.0)
+    k = wl.randn_bf16((2, 4, 32, 32), 2, scale=1.0)
+    out0 = _check(gate, q, k, 0.0, True)
+    assert out0.hard_mask.all()  # 0 >= 0 holds in the zeroed upper triangle too
+    out1 = _check(gate, q, k, 1.0 + 1e-7, True)
+    assert not out1.hard_mask.any()
+    assert out1.sparsity_ratio == pytest.approx(1.0)
+    taus = torch.tensor([0.0, 0.49, 0.5, 0.51])
+    _check(gate, q, k, taus, True)
+    _check(gate, q, k, 0.6, True, force_diagonal=True)
+
+
+def test_gqa_equals_expanded_k():
+    dev = require_gpu()
+    gate = _gate(8, 128, 64, 64).to(dev)
+    q = wl.randn_bf16((1, 8, 512, 128), 3).to(dev)
+    k = wl.randn_bf16((1, 2, 512, 128), 4).to(dev)
+    with torch.no_grad():
+        a = gate(q, k, return_logits=True)
+        b = gate(q, k.repeat_interleave(4, dim=1), return_logits=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a.logits, b.logits) and torch.equal(a.hard_mask, b.hard_mask)
+
+
+def test_autograd_path_matches_kernel_and_has_gradients():
+    dev = require_gpu()
+    gate = _gate(4, 64, 16, 32).to(dev)
+    q = wl.randn_bf16((1, 4, 128, 64), 5, scale=1.0).to(dev)
+    k = wl.randn_bf16((1, 4, 128, 64), 6, scale=1.0).to(dev)
+    with torch.no_grad():
+        ref = gate(q, k, return_logits=True)
+    out = gate(q, k, return_logits=True)  # parameters require grad -> differentiable path
+    torch.testing.assert_close(out.logits.detach(), ref.logits, rtol=1e-4, atol=1e-5)
+    out.soft_scores.sum().backward()
+    for name, p in gate.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all() and p.grad.abs().sum() > 0, name
+
+
+def test_config2_gate_full_size_sampled_heads():
+    """Config 2 geometry: B=4, S=8192, 32/8 heads, hidden 128; heads sampled for the oracle."""
+    dev = require_gpu()
+    shape = wl.CONFIG_SHAPES[2]
+    q, k, _ = wl.qkv(shape, 1002)
+    gate = AttnGate(num_heads=32, head_dim=128, gate_hidden_dim=128)
+    gate.load_state_dict(wl.gate_params(128, 128, 3002))
+    gd = gate.to(dev)
+    with torch.no_grad():
+        out = gd(q.to(dev), k.to(dev), threshold=0.5, return_logits=True)
+    torch.cuda.synchronize()
+    gate.cpu()
+    w_in, b_in, w_out = _params(gate)
+    logits = to_np(out.logits)
+    for b, h in [(0, 0), (2, 17), (3, 31)]:
+        ref = orc.gate_logits(to_np(q[b : b + 1, h : h + 1]), to_np(k[b : b + 1, h // 4 : h // 4 + 1]),
+                              w_in, b_in, w_out, 64, dtype=np.float64)[0, 0]
+        np.testing.assert_allclose(logits[b, h], ref, rtol=LOGIT_RTOL, atol=LOGIT_ATOL)
+    soft_ref, hard_ref = orc.threshold_mask(logits, 0.5, True)
+    decisive = np.abs(soft_ref - 0.5) > TAU_BAND
+    hard = out.hard_mask.cpu().numpy()
+    assert np.array_equal(hard[decisive], hard_ref[decisive])

@@ -1,0 +1,86 @@
+"""Gate-target kernel parity: block maxima and softmax targets vs the CPU oracle."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close_bf16, require_gpu, to_np
+from oracle import tasft_oracle as orc
+from tasft_amd import workloads as wl
+from tasft_amd.training import TASFTObjective, gate_target_from_qk
+
+pytestmark = pytest.mark.gpu
+
+RAW_RTOL = 1e-4
+RAW_ATOL = 1e-6
+
+
+def _gt(q, k, bs, **kw):
+    out = gate_target_from_qk(q, k, bs, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+CASES = [
+    # B, Hq, Hkv, S, D, bs, causal
+    (1, 4, 4, 512, 128, 64, True),
+    (2, 8, 2, 1000, 128, 64, True),   # GQA, ragged
+    (1, 4, 1, 300, 64, 32, False),    # non-causal, D=64
+    (1, 2, 2, 384, 128, 128, True),   # bs=128
+]
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "causal"), CASES)
+def test_block_max_and_targets_match_oracle(B, Hq, Hkv, S, D, bs, causal):
+    dev = require_gpu()
+    q, k, _ = wl.qkv(wl.Shape(B, Hq, Hkv, S, D), 300 + S)
+    qd, kd = q.to(dev), k.to(dev)
+    raw_ref = orc.block_max(to_np(q), to_np(k), bs, causal, dtype=np.float64)
+    raw = to_np(_gt(qd, kd, bs, causal=causal, normalize="none"))
+    assert np.array_equal(np.isneginf(raw), np.isneginf(raw_ref))
+    fin = np.isfinite(raw_ref)
+    np.testing.assert_allclose(raw[fin], raw_ref[fin], rtol=RAW_RTOL, atol=RAW_ATOL)
+    for norm in ("flat", "row"):
+        got = _gt(qd, kd, bs, causal=causal, normalize=norm)
+        ref = orc.normalize_block_max(raw_ref, norm)
+        assert_close_bf16(got, ref, f"gate target {norm}")
+        np.testing.assert_allclose(to_np(got), ref, rtol=1e-3, atol=1e-7)
+
+
+def test_clamp_temperature_variant():
+    dev = require_gpu()
+    q, k, _ = wl.qkv(wl.Shape(1, 4, 4, 256, 128), 77)
+    # Scale the queries so some block maxima exceed the clamp.
+    q = (q.float() * 400).to(torch.bfloat16)
+    got = _gt(q.to(dev), k.to(dev), 64, normalize="flat", temperature=2.0, clamp=50.0)
+    raw_ref = orc.block_max(to_np(q), to_np(k), 64, True, dtype=np.float64)
+    assert np.nanmax(raw_ref[np.isfinite(raw_ref)]) > 50.0
+    ref = orc.normalize_block_max(raw_ref, "flat", temperature=2.0, clamp=50.0)
+    np.testing.assert_allclose(to_np(got), ref, rtol=1e-3, atol=1e-7)
+
+
+def test_matches_reference_dense_path_on_explicit_scores():
+    """gate_target_from_qk == compute_gate_target(Q K^T * scale + triu(-inf))."""
+    dev = require_gpu()
+    q, k, _ = wl.qkv(wl.Shape(1, 4, 2, 256, 128), 88)
+    got = _gt(q.to(dev), k.to(dev), 64)
+    kk = k.float().repeat_interleave(2, 1)
+    scores = (q.float() @ kk.transpose(-1, -2)) / math.sqrt(128)
+    scores = scores + torch.full((256, 256), float("-inf")).triu(1)
+    ref = TASFTObjective.compute_gate_target(scores, 64)
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-3, atol=1e-7)
+
+
+def test_config5_full_size_sampled_heads():
+    dev = require_gpu()
+    shape = wl.CONFIG_SHAPES[5]
+    q, k, _ = wl.qkv(shape, 1005)
+    got = to_np(_gt(q.to(dev), k.to(dev), 64))
+    np.testing.assert_allclose(got.reshape(4, 32, -1).sum(-1), 1.0, rtol=1e-4)
+    assert (got[..., np.triu(np.ones((64, 64), bool), 1)] == 0).all()
+    for b, h in [(0, 0), (3, 31)]:
+        ref = orc.gate_target_from_qk(to_np(q[b : b + 1, h : h + 1]), to_np(k[b : b + 1, h // 4 : h // 4 + 1]), 64)
+        np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)

@@ -1,0 +1,160 @@
+"""Prefill kernel parity: HIP (through the C ABI) vs the CPU oracle on identical inputs.
+
+Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32 oracle on the same bf16
+inputs (tests/helpers.py). Rows with no active key must be exactly 0.
+"""
+from __future__ import annotations
+
+import math
+import warnings
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import assert_close_bf16, require_gpu, to_np
+from oracle import tasft_oracle as orc
+from tasft_amd import workloads as wl
+from tasft_amd.kernels import BlockSparseFlashAttention
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, mask, bs, causal):
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward(q, k, v, mask, causal=causal)
+    torch.cuda.synchronize()
+    return out
+
+
+def _inputs(B, Hq, Hkv, S, D, seed):
+    shape = wl.Shape(B, Hq, Hkv, S, D)
+    return wl.qkv(shape, seed)
+
+
+def test_config1_matches_oracle():
+    dev = require_gpu()
+    shape = wl.CONFIG_SHAPES[1]
+    q, k, v = wl.qkv(shape, 1001)
+    mask = wl.bernoulli_causal_mask(shape, 0.2, 2001)
+    out = _run(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), shape.block, True)
+    ref = orc.attention_block_gather(to_np(q), to_np(k), to_np(v), mask.numpy(), shape.block, True)
+    assert_close_bf16(out, ref, "config 1 prefill")
+
+
+CASES = [
+    # B, Hq, Hkv, S, D, bs, causal, density
+    (2, 4, 4, 256, 128, 64, True, 0.5),     # MHA (reference layout)
+    (1, 8, 2, 1000, 128, 64, True, 0.4),    # GQA, ragged S
+    (1, 4, 1, 300, 64, 32, False, 0.5),     # non-causal, D=64, bs=32
+    (1, 2, 2, 384, 128, 128, True, 0.6),    # bs=128
+    (1, 7, 1, 520, 128, 64, True, 0.3),     # G=7 (Qwen grouping), ragged
+    (2, 4, 2, 192, 64, 128, False, 0.5),    # non-causal, bs=128, D=64, partial last block
+    (1, 4, 2, 100, 128, 32, True, 1.0),     # all-true causal
+]
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "causal", "density"), CASES)
+def test_prefill_shapes_match_oracle(B, Hq, Hkv, S, D, bs, causal, density):
+    dev = require_gpu()
+    seed = 17 + S + Hq
+    q, k, v = _inputs(B, Hq, Hkv, S, D, seed)
+    nb = math.ceil(S / bs)
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.rand((B, Hq, nb, nb), generator=g) < density
+    out = _run(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), bs, causal)
+    ref = orc.attention_dense_masked(to_np(q), to_np(k), to_np(v), mask.numpy(), bs, causal)
+    assert_close_bf16(out, ref, f"prefill {B}x{Hq}/{Hkv}x{S}x{D} bs={bs} causal={causal}")
+
+
+def test_empty_rows_are_exact_zero():
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs = 1, 4, 2, 512, 128, 64
+    q, k, v = _inputs(B, Hq, Hkv, S, D, 5)
+    nb = S // bs
+    mask = torch.ones((B, Hq, nb, nb), dtype=torch.bool)
+    mask[0, 1, 3, :] = False          # fully empty row
+    mask[0, 2, 5, :6] = False         # only blocks above the diagonal remain -> empty under causal
+    out = _run(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), bs, True)
+    o = out.cpu()
+    assert (o[0, 1, 3 * bs : 4 * bs] == 0).all()
+    assert (o[0, 2, 5 * bs : 6 * bs] == 0).all()
+    ref = orc.attention_dense_masked(to_np(q), to_np(k), to_np(v), mask.numpy(), bs, True)
+    assert_close_bf16(out, ref, "empty rows")
+
+
+def test_all_true_mask_equals_sdpa_fp32():
+    dev = require_gpu()
+    q, k, v = _inputs(2, 8, 2, 320, 128, 9)
+    mask = torch.ones((2, 8, 5, 5), dtype=torch.bool)
+    out = _run(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 64, True)
+    kk, vv = k.float().repeat_interleave(4, 1), v.float().repeat_interleave(4, 1)
+    ref = F.scaled_dot_product_attention(q.float(), kk, vv, is_causal=True).numpy()
+    assert_close_bf16(out, ref, "all-true mask vs SDPA")
+
+
+def test_strided_hf_layout_inputs():
+    """Q/K/V as transposed views of [B, S, H, D] (the HF projection layout), no copies."""
+    dev = require_gpu()
+    B, S, Hq, Hkv, D = 2, 256, 8, 2, 128
+    g = torch.Generator().manual_seed(21)
+    base_q = (torch.randn((B, S, Hq, D), generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    base_k = (torch.randn((B, S, Hkv, D), generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    base_v = (torch.randn((B, S, Hkv, D), generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    q, k, v = (t.to(dev).transpose(1, 2) for t in (base_q, base_k, base_v))
+    assert not q.is_contiguous()
+    mask = torch.rand((B, Hq, 4, 4), generator=g) < 0.5
+    out = _run(q, k, v, mask.to(dev), 64, True)
+    ref = orc.attention_dense_masked(to_np(q), to_np(k), to_np(v), mask.numpy(), 64, True)
+    assert_close_bf16(out, ref, "strided inputs")
+
+
+@pytest.mark.parametrize("dtype", [torch.bool, torch.uint8, torch.int32])
+def test_mask_dtypes(dtype):
+    dev = require_gpu()
+    q, k, v = _inputs(1, 4, 4, 192, 128, 31)
+    g = torch.Generator().manual_seed(31)
+    mask = torch.rand((1, 4, 3, 3), generator=g) < 0.6
+    out = _run(q.to(dev), k.to(dev), v.to(dev), mask.to(dtype).to(dev), 64, True)
+    ref = orc.attention_dense_masked(to_np(q), to_np(k), to_np(v), mask.numpy(), 64, True)
+    assert_close_bf16(out, ref, f"mask dtype {dtype}")
+
+
+def test_low_sparsity_policy_falls_back_to_dense_with_warning():
+    dev = require_gpu()
+    q, k, v = (t.to(dev) for t in _inputs(1, 4, 4, 128, 128, 3))
+    mask = torch.ones((1, 4, 2, 2), dtype=torch.bool, device=dev)
+    bsfa = BlockSparseFlashAttention(block_size=64, min_sparsity_for_speedup=0.5)
+    with pytest.warns(UserWarning, match="dense fallback"):
+        out = bsfa.forward(q, k, v, mask, causal=True)
+    ref = F.scaled_dot_product_attention(q.float().cpu(), k.float().cpu(), v.float().cpu(), is_causal=True)
+    assert_close_bf16(out, ref.numpy(), "dense fallback")
+
+
+def _sampled_parity(cfg, mask, seed, heads, rows=None):
+    dev = require_gpu()
+    shape = wl.CONFIG_SHAPES[cfg]
+    q, k, v = wl.qkv(shape, seed)
+    out = _run(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), shape.block, True).cpu()
+    qn, kn, vn = to_np(q), to_np(k), to_np(v)
+    ref = orc.attention_block_gather(qn, kn, vn, mask.numpy(), shape.block, True, heads=heads)
+    for b, h in heads:
+        assert_close_bf16(out[b, h], ref[b, h], f"config {cfg} head ({b},{h})")
+    assert torch.isfinite(out.float()).all()
+
+
+def test_config2_full_size_sampled_heads():
+    shape = wl.CONFIG_SHAPES[2]
+    g = torch.Generator().manual_seed(2002)
+    nb = shape.nb
+    # 80% causal sparsity with the diagonal on (the mask the gate produces at config 2).
+    keep = torch.rand((shape.batch, shape.q_heads, nb, nb), generator=g) < 0.187
+    mask = (keep & torch.ones(nb, nb, dtype=torch.bool).tril(-1)) | torch.eye(nb, dtype=torch.bool)
+    _sampled_parity(2, mask, 1002, heads=[(0, 0), (1, 13), (3, 31)])
+
+
+def test_config4_full_size_sampled_heads():
+    shape = wl.CONFIG_SHAPES[4]
+    mask, _ = wl.qwen_mask(shape, 2004)
+    _sampled_parity(4, mask, 1004, heads=[(0, 0), (1, 27)])

@@ -1,0 +1,201 @@
+"""Host-side API of the drop-in modules (no GPU): constructors, validation, statistics.
+
+Mirrors the reference's CPU unit tests for the same API (tests/unit/test_kernel.py,
+tests/unit/test_attn_gate.py, tests/unit/test_edge_cases.py) where they apply.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import pytest
+import torch
+
+from tasft_amd.exceptions import KernelError, NaNDetectedError, TASFTError, ValidationError
+from tasft_amd.kernels import (
+    BlockSparseFlashAttention,
+    KernelBackend,
+    KernelConfig,
+    LayerKernelConfig,
+    detect_kernels,
+)
+from tasft_amd.modules import AttnGate, GateOutput
+from tasft_amd.training import TASFTObjective
+
+
+class TestBlockSparseInit:
+    def test_invalid_block_size_raises(self):
+        with pytest.raises(ValueError, match="block_size"):
+            BlockSparseFlashAttention(block_size=16)
+
+    @pytest.mark.parametrize("bs", [32, 64, 128])
+    def test_valid_block_sizes(self, bs):
+        assert BlockSparseFlashAttention(block_size=bs).block_size == bs
+
+    def test_min_sparsity_range(self):
+        with pytest.raises(ValueError, match="min_sparsity_for_speedup"):
+            BlockSparseFlashAttention(min_sparsity_for_speedup=1.5)
+
+    def test_auto_selects_hip_backend(self):
+        assert BlockSparseFlashAttention().backend == KernelBackend.HIP_GFX950
+
+    @pytest.mark.parametrize("backend", [KernelBackend.TRITON, KernelBackend.FLASH_ATTN_SPARSE])
+    def test_unavailable_backend_raises(self, backend):
+        with pytest.raises(KernelError, match="not available"):
+            BlockSparseFlashAttention(backend=backend)
+
+    def test_detect_kernels_dense_fallback_last(self):
+        avail = detect_kernels()
+        assert avail[-1] == KernelBackend.DENSE_FALLBACK
+        assert KernelBackend.HIP_GFX950 in avail  # the library is built in-tree
+
+    def test_sparsity_stats(self):
+        bsfa = BlockSparseFlashAttention(block_size=64)
+        mask = torch.zeros(1, 4, 8, 8, dtype=torch.bool)
+        mask[:, :, :4, :] = True
+        st = bsfa.compute_sparsity_stats(mask)
+        assert (st.total_blocks, st.active_blocks) == (256, 128)
+        assert st.sparsity_ratio == pytest.approx(0.5)
+        assert st.estimated_speedup == pytest.approx(1.0 / (1.0 - 0.5 * 0.98))
+
+    def test_speedup_model(self):
+        assert abs(BlockSparseFlashAttention.estimate_speedup(0.0) - 1.0) < 0.05
+        assert BlockSparseFlashAttention.estimate_speedup(0.9) > 3.0
+        prev = 0.0
+        for pct in range(0, 100, 5):
+            s = BlockSparseFlashAttention.estimate_speedup(pct / 100)
+            assert s >= prev
+            prev = s
+
+
+class TestBlockSparseValidation:
+    def _bsfa(self):
+        return BlockSparseFlashAttention(block_size=32, min_sparsity_for_speedup=0.0)
+
+    def test_ndim(self):
+        x = torch.zeros(2, 64, 32)
+        with pytest.raises(KernelError, match="Expected 4D tensors"):
+            self._bsfa().forward(x, x, x, torch.ones(1, 1, 2, 2, dtype=torch.bool))
+
+    def test_shape_mismatch(self):
+        q = torch.zeros(1, 4, 64, 32)
+        k = torch.zeros(1, 3, 64, 32)  # 4 % 3 != 0: not a GQA layout
+        with pytest.raises(KernelError, match="Q, K, V shapes must match"):
+            self._bsfa().forward(q, k, k, torch.ones(1, 4, 2, 2, dtype=torch.bool))
+
+    def test_cpu_tensors_rejected(self):
+        q = torch.zeros(1, 4, 64, 32)
+        kv = torch.zeros(1, 2, 64, 32)  # GQA layout passes the shape check
+        with pytest.raises(KernelError, match="Tensors must be on CUDA device"):
+            self._bsfa().forward(q, kv, kv, torch.ones(1, 4, 2, 2, dtype=torch.bool))
+
+    def test_decode_shape_checks(self):
+        q = torch.zeros(1, 4, 2, 32)
+        kv = torch.zeros(1, 2, 64, 32)
+        with pytest.raises(KernelError, match=r"\[B, H, 1, D\]"):
+            self._bsfa().forward_decode(q, kv, kv, torch.ones(1, 4, 1, 2, dtype=torch.bool))
+
+
+class TestKernelConfig:
+    def test_defaults_and_lookup(self):
+        lc = LayerKernelConfig(layer_idx=3, threshold_tau=0.7, target_sparsity=0.8,
+                               achieved_sparsity_validation=0.79)
+        kc = KernelConfig(per_layer_config={3: lc})
+        assert kc.get_layer_threshold(3) == 0.7
+        assert kc.get_layer_threshold(0) == 0.5
+        assert kc.get_layer_block_size(3) == 64
+
+    def test_validation(self):
+        with pytest.raises(ValueError, match="threshold_tau"):
+            LayerKernelConfig(layer_idx=0, threshold_tau=1.0, target_sparsity=0.5,
+                              achieved_sparsity_validation=0.5)
+        with pytest.raises(ValueError, match="block_size"):
+            KernelConfig(block_size=48)
+        lc = LayerKernelConfig(layer_idx=1, threshold_tau=0.5, target_sparsity=0.5,
+                               achieved_sparsity_validation=0.5)
+        with pytest.raises(ValueError, match="doesn't match"):
+            KernelConfig(per_layer_config={2: lc})
+        with pytest.raises(ValueError):
+            KernelConfig(unknown_field=1)
+
+
+class TestAttnGateHost:
+    def test_defaults(self):
+        g = AttnGate(num_heads=4, head_dim=32)
+        assert (g.block_size, g.default_threshold, g.gate_hidden_dim) == (64, 0.5, 32)
+        assert AttnGate(num_heads=4, head_dim=256).gate_hidden_dim == 64
+
+    @pytest.mark.parametrize(("kwargs", "msg"), [
+        ({"num_heads": 0, "head_dim": 32}, "num_heads must be positive"),
+        ({"num_heads": 4, "head_dim": 0}, "head_dim must be positive"),
+        ({"num_heads": 4, "head_dim": 32, "block_size": 0}, "block_size must be positive"),
+        ({"num_heads": 4, "head_dim": 32, "default_threshold": 1.5}, "default_threshold must be in"),
+    ])
+    def test_constructor_errors(self, kwargs, msg):
+        with pytest.raises(ValidationError, match=msg):
+            AttnGate(**kwargs)
+
+    def test_state_dict_keys_and_param_count(self):
+        g = AttnGate(num_heads=32, head_dim=128, gate_hidden_dim=128)
+        assert set(g.state_dict()) == {"gate_proj_in.weight", "gate_proj_in.bias", "gate_proj_out.weight"}
+        assert g.num_parameters == 256 * 128 + 128 + 128
+        r = g.extra_repr()
+        assert "num_heads=32" in r and "head_dim=128" in r and "block_size=64" in r
+
+    def test_seeded_init_matches_reference_order(self):
+        """Same RNG consumption as the reference: Linear default init, then xavier/zeros/normal."""
+        torch.manual_seed(0)
+        g = AttnGate(num_heads=2, head_dim=16, gate_hidden_dim=8)
+        torch.manual_seed(0)
+        a = torch.nn.Linear(32, 8)
+        b = torch.nn.Linear(8, 1, bias=False)
+        torch.nn.init.xavier_uniform_(a.weight)
+        torch.nn.init.zeros_(a.bias)
+        torch.nn.init.normal_(b.weight, std=0.01)
+        assert torch.equal(g.gate_proj_in.weight, a.weight)
+        assert torch.equal(g.gate_proj_out.weight, b.weight)
+
+    @pytest.mark.parametrize(("q", "k", "msg"), [
+        ((4, 64, 32), (1, 4, 64, 32), "Expected 4D Q tensor"),
+        ((1, 4, 64, 32), (4, 64, 32), "Expected 4D K tensor"),
+        ((1, 4, 64, 32), (1, 4, 128, 32), "Q and K must have same shape"),
+        ((1, 8, 64, 32), (1, 8, 64, 32), "Expected 4 heads"),
+        ((1, 4, 64, 64), (1, 4, 64, 64), "Expected head_dim=32"),
+        ((1, 4, 0, 32), (1, 4, 0, 32), "Sequence length must be > 0"),
+    ])
+    def test_forward_validation_messages(self, q, k, msg):
+        g = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        with pytest.raises(ValidationError, match=msg):
+            g(torch.randn(q), torch.randn(k))
+
+    def test_cpu_tensors_rejected(self):
+        g = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        with pytest.raises(KernelError, match="ROCm device"):
+            g(torch.randn(1, 4, 64, 32), torch.randn(1, 4, 64, 32))
+
+    def test_gate_output_frozen_and_lazy(self):
+        out = GateOutput(soft_scores=torch.zeros(1, 1, 2, 2), hard_mask=torch.zeros(1, 1, 2, 2, dtype=torch.bool),
+                         num_blocks_q=2, num_blocks_k=2, active_count=torch.tensor([1]))
+        assert out.sparsity_ratio == pytest.approx(0.75)
+        with pytest.raises(AttributeError):
+            out.sparsity_ratio = 0.5
+        with pytest.raises(dataclasses.FrozenInstanceError):
+            out.hard_mask = None
+
+
+class TestGateTargetDense:
+    def test_reference_dense_path_on_scores(self):
+        attn = torch.arange(1, 17, dtype=torch.float32).reshape(1, 1, 4, 4)
+        t = TASFTObjective.compute_gate_target(attn, block_size=2)
+        ref = torch.softmax(torch.tensor([6.0, 8.0, 14.0, 16.0]), 0).reshape(1, 1, 2, 2)
+        torch.testing.assert_close(t, ref)
+
+    def test_nan_raises_with_context(self):
+        attn = torch.tensor([[[[float("nan"), 1.0], [1.0, 1.0]]]])
+        with pytest.raises(NaNDetectedError) as ei:
+            TASFTObjective.compute_gate_target(attn, block_size=1)
+        assert ei.value.context["has_nan"] is True
+        assert isinstance(ei.value, TASFTError)
+
+    def test_block_size_zero(self):
+        with pytest.raises(ValueError, match="block_size must be > 0"):
+            TASFTObjective.compute_gate_target(torch.randn(1, 1, 4, 4), block_size=0)

@@ -1,0 +1,71 @@
+"""The C-ABI library loads on the CPU and exports every symbol the header declares.
+
+Only host-side entry points are called here (version, workspace sizes, argument
+validation that returns before any device work); no kernel is launched.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tasft_amd import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "tasft_amd.h"
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(tasft_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load_library()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed from the header"
+    assert declared == set(_native.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} missing from {_native.LIB_PATH}"
+
+
+def test_abi_version_and_workspace_sizes():
+    lib = _native.load_library()
+    assert lib.tasft_abi_version() == 1
+    assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
+    assert lib.tasft_bsfa_decode_workspace_bytes(0, 32, 128, 4) == 0
+    nb = 8192 // 64
+    assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 64, 128) == 4 * 40 * nb * 128 * 4 + 256
+
+
+def _i64(vals):
+    return (ctypes.c_int64 * 4)(*vals)
+
+
+def test_invalid_arguments_return_errors_without_launch():
+    lib = _native.load_library()
+    st = _i64([0, 0, 0, 1])
+    rc = lib.tasft_bsfa_prefill_fwd(None, None, None, None, None, 1, 32, 8, 128, 128, 64,
+                                    st, st, st, st, st, 1.0, 1, None)
+    assert rc == -1 and b"null pointer" in lib.tasft_last_error()
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, 1, 32, 8, 128, 96, 64,
+                                    st, st, st, st, st, 1.0, 1, None)
+    assert rc == -2 and b"head_dim" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, 1, 30, 8, 128, 128, 64,
+                                    st, st, st, st, st, 1.0, 1, None)
+    assert rc == -1 and b"multiple" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_decode_fwd(fake, fake, fake, fake, fake, None, fake, 0, 1, 32, 8, 1024, 128,
+                                   64, 4, st, st, st, st, st, 1.0, None)
+    assert rc == -4 and b"workspace" in lib.tasft_last_error()
+
+
+def test_check_raises_kernel_error_with_message():
+    from tasft_amd.exceptions import KernelError
+    lib = _native.load_library()
+    st = _i64([0, 0, 0, 1])
+    rc = lib.tasft_gate_target_fwd(None, None, None, 1, 1, 1, 64, 128, 64, st, st, 1.0, 1, 0, 1.0, 0.0, None)
+    with pytest.raises(KernelError, match="null pointer"):
+        _native.check(rc, "tasft_gate_target_fwd")

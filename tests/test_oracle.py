@@ -1,0 +1,266 @@
+"""Pins the CPU oracle against the reference's known answers, library routines and brute force.
+
+None of these checks retypes the oracle's own formula: each compares it with literal
+vectors from the reference tests (tests/golden/reference_vectors.json), with a torch
+library routine, with an independent pure-Python loop, or with a second formulation.
+"""
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import tasft_oracle as orc
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+# ----------------------------------------------------------------------------- golden vectors
+@pytest.mark.parametrize("case", ["pool_block4", "pool_padding", "pool_single_block"])
+def test_pool_matches_reference_vectors(case):
+    c = GOLDEN[case]
+    got = orc.pool_to_blocks(np.array(c["x"], dtype=np.float32), c["block_size"])
+    np.testing.assert_allclose(got, np.array(c["expected"]), atol=1e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("case", ["gate_target_4x4", "gate_target_8x8", "gate_target_uniform"])
+def test_gate_target_matches_reference_vectors(case):
+    c = GOLDEN[case]
+    got = orc.gate_target_from_scores(np.array(c["scores"], dtype=np.float64), c["block_size"])
+    np.testing.assert_allclose(got, np.array(c["expected"]), atol=1e-6, rtol=1e-6)
+    assert got.sum() == pytest.approx(1.0, abs=1e-9)
+
+
+def test_gate_target_rejects_nan_and_pos_inf_allows_neg_inf():
+    x = np.zeros((1, 1, 4, 4))
+    x[0, 0, 0, 1] = np.nan
+    with pytest.raises(ValueError):
+        orc.gate_target_from_scores(x, 2)
+    x[0, 0, 0, 1] = np.inf
+    with pytest.raises(ValueError):
+        orc.gate_target_from_scores(x, 2)
+    # Causal -inf (test_numerical_correctness.py:173-184) is allowed and gives a distribution.
+    y = np.random.default_rng(0).standard_normal((1, 1, 8, 8))
+    y[0, 0][np.triu(np.ones((8, 8), bool), 1)] = -np.inf
+    t = orc.gate_target_from_scores(y, 4)
+    assert np.isfinite(t).all() and t.sum() == pytest.approx(1.0)
+
+
+def test_gate_target_matches_torch_maxpool_softmax():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 3, 37, 37))  # ragged: pads to 40 with -inf
+    got = orc.gate_target_from_scores(x, 8)
+    t = torch.from_numpy(x)
+    t = F.pad(t, (0, 3, 0, 3), value=-math.inf)
+    pooled = F.max_pool2d(t, 8, 8)
+    ref = F.softmax(pooled.reshape(2, 3, -1), dim=-1).reshape(pooled.shape).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-15)
+
+
+def test_stats_and_speedup_match_reference_vectors():
+    c = GOLDEN["sparsity_stats"]
+    m = np.zeros(c["mask_shape"], dtype=bool)
+    m[:, :, : c["active_rows"], :] = True
+    assert orc.sparsity_stats(m) == (c["total"], c["active"], c["sparsity"])
+    for s, v in GOLDEN["speedup"]["points"]:
+        assert orc.estimate_speedup(s) == pytest.approx(v, rel=1e-12)
+    lo, hi = GOLDEN["speedup"]["bounds"]["at_0"]
+    assert lo <= orc.estimate_speedup(0.0) <= hi
+    assert orc.estimate_speedup(0.9) > GOLDEN["speedup"]["bounds"]["at_0.9_min"]
+
+
+# ----------------------------------------------------------------------------- gate
+def _torch_gate_reference(q, k, lin_in, lin_out, bs):
+    """Gate logits through torch.nn.Linear / relu on the materialised concat."""
+    qt, kt = torch.from_numpy(q).float(), torch.from_numpy(k).float()
+    B, H, S, D = qt.shape
+    pad = (bs - S % bs) % bs
+    qt, kt = F.pad(qt, (0, 0, 0, pad)), F.pad(kt, (0, 0, 0, pad))
+    nb = qt.shape[2] // bs
+    qb = qt.view(B, H, nb, bs, D).mean(3)
+    kb = kt.view(B, H, nb, bs, D).mean(3)
+    cat = torch.cat([qb.unsqueeze(3).expand(B, H, nb, nb, D), kb.unsqueeze(2).expand(B, H, nb, nb, D)], -1)
+    with torch.no_grad():
+        return lin_out(F.relu(lin_in(cat))).squeeze(-1).numpy()
+
+
+def test_gate_logits_match_torch_linear_and_concat_form():
+    torch.manual_seed(3)
+    D, hid, bs = 16, 24, 8
+    lin_in = torch.nn.Linear(2 * D, hid)
+    lin_out = torch.nn.Linear(hid, 1, bias=False)
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((2, 4, 30, D)).astype(np.float32)
+    k = rng.standard_normal((2, 4, 30, D)).astype(np.float32)
+    w_in, b_in = lin_in.weight.detach().numpy(), lin_in.bias.detach().numpy()
+    w_out = lin_out.weight.detach().numpy()
+    ref = _torch_gate_reference(q, k, lin_in, lin_out, bs)
+    dec = orc.gate_logits(q, k, w_in, b_in, w_out, bs, dtype=np.float64)
+    cat = orc.gate_logits_concat(orc.pool_to_blocks(q, bs), orc.pool_to_blocks(k, bs), w_in, b_in, w_out)
+    np.testing.assert_allclose(dec, ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(cat, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_gate_logits_gqa_equals_expanded_k():
+    rng = np.random.default_rng(4)
+    D, hid, bs = 16, 32, 4
+    w_in = rng.standard_normal((hid, 2 * D)).astype(np.float32)
+    b_in = rng.standard_normal(hid).astype(np.float32)
+    w_out = rng.standard_normal((1, hid)).astype(np.float32)
+    q = rng.standard_normal((1, 8, 16, D)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 16, D)).astype(np.float32)
+    a = orc.gate_logits(q, k, w_in, b_in, w_out, bs)
+    b = orc.gate_logits(q, np.repeat(k, 4, axis=1), w_in, b_in, w_out, bs)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_threshold_mask_invariants():
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((2, 3, 6, 6)).astype(np.float32)
+    soft, hard = orc.threshold_mask(logits, 0.5, causal=True)
+    up = np.triu(np.ones((6, 6), bool), 1)
+    assert (soft[..., up] == 0.0).all() and not hard[..., up].any()
+    lo = ~up
+    ref = torch.sigmoid(torch.from_numpy(logits)).numpy()
+    np.testing.assert_allclose(soft[..., lo], ref[..., lo], rtol=1e-6)
+    _, hard0 = orc.threshold_mask(logits, 0.0, causal=True)
+    assert hard0.all()  # tau=0: 0 >= 0 in the upper triangle (test_edge_cases.py:210-218)
+    _, hard1 = orc.threshold_mask(logits, 1.0 + 1e-7, causal=True)
+    assert not hard1.any()
+    soft_nc, _ = orc.threshold_mask(logits, 0.5, causal=False)
+    assert (soft_nc[..., up] > 0).all()
+    taus = np.array([0.2, 0.5, 0.9], dtype=np.float32)
+    _, hh = orc.threshold_mask(logits, taus, causal=False)
+    for h in range(3):
+        np.testing.assert_array_equal(hh[:, h], soft_nc[:, h] >= taus[h])
+
+
+# ----------------------------------------------------------------------------- attention
+def _brute_attention(q, k, v, mask, bs, causal, scale):
+    """Pure-Python loops: one query at a time, explicit max/exp/sum."""
+    B, H, S, D = q.shape
+    Sk = k.shape[2]
+    g = H // k.shape[1]
+    out = np.zeros_like(q, dtype=np.float64)
+    for b in range(B):
+        for h in range(H):
+            for i in range(S):
+                allowed = []
+                for j in range(Sk):
+                    if not mask[b, h, i // bs, j // bs]:
+                        continue
+                    if causal and (j // bs > i // bs or j > i):
+                        continue
+                    s = sum(float(q[b, h, i, d]) * float(k[b, h // g, j, d]) for d in range(D)) * scale
+                    allowed.append((j, s))
+                if not allowed:
+                    continue
+                m = max(s for _, s in allowed)
+                w = [(j, math.exp(s - m)) for j, s in allowed]
+                tot = sum(x for _, x in w)
+                for d in range(D):
+                    out[b, h, i, d] = sum(x * float(v[b, h // g, j, d]) for j, x in w) / tot
+    return out
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_matches_brute_force(causal):
+    rng = np.random.default_rng(6)
+    B, H, Hkv, S, D, bs = 1, 4, 2, 11, 3, 4
+    q = rng.standard_normal((B, H, S, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    nb = math.ceil(S / bs)
+    mask = rng.random((B, H, nb, nb)) < 0.6
+    mask[0, 1, 1, :] = False  # an empty block row -> zeros
+    ref = _brute_attention(q, k, v, mask, bs, causal, 0.7)
+    for fn in (orc.attention_dense_masked, orc.attention_block_gather):
+        got = fn(q, k, v, mask, bs, causal=causal, scale=0.7, dtype=np.float64)
+        np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+    assert (orc.attention_dense_masked(q, k, v, mask, bs, causal, 0.7)[0, 1, 4:8] == 0).all()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_all_true_mask_equals_sdpa(causal):
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((2, 4, 70, 16)).astype(np.float32)
+    k = rng.standard_normal((2, 4, 70, 16)).astype(np.float32)
+    v = rng.standard_normal((2, 4, 70, 16)).astype(np.float32)
+    mask = np.ones((2, 4, 3, 3), dtype=bool)
+    got = orc.attention_block_gather(q, k, v, mask, 32, causal=causal, dtype=np.float64)
+    ref = F.scaled_dot_product_attention(torch.from_numpy(q).double(), torch.from_numpy(k).double(),
+                                         torch.from_numpy(v).double(), is_causal=causal).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_attention_gather_equals_dense_masked_gqa():
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((1, 8, 200, 32)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 200, 32)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 200, 32)).astype(np.float32)
+    mask = rng.random((1, 8, 4, 4)) < 0.5
+    a = orc.attention_dense_masked(q, k, v, mask, 64, True, dtype=np.float64)
+    b = orc.attention_block_gather(q, k, v, mask, 64, True, dtype=np.float64)
+    np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------- decode
+def test_decode_equals_last_prefill_row_and_brute_force():
+    rng = np.random.default_rng(9)
+    B, H, Hkv, S, D, bs = 2, 4, 2, 100, 8, 16
+    q_all = rng.standard_normal((B, H, S, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    nb = math.ceil(S / bs)
+    row = rng.random((B, H, 1, nb)) < 0.5
+    row[0, 0, 0, :] = False  # head with nothing selected -> 0
+    full = np.zeros((B, H, nb, nb), dtype=bool)
+    full[:, :, nb - 1, :] = row[:, :, 0, :]
+    pre = orc.attention_block_gather(q_all, k, v, full, bs, causal=True, dtype=np.float64)
+    dec = orc.sparse_decode(q_all[:, :, S - 1 : S], k, v, row, bs, dtype=np.float64)
+    np.testing.assert_allclose(dec[:, :, 0], pre[:, :, S - 1], rtol=1e-10, atol=1e-12)
+    assert (dec[0, 0] == 0).all()
+    brute = _brute_attention(q_all[:, :, S - 1 : S], k[:, :, :S], v, np.repeat(row, 1, axis=2), bs,
+                             False, 1 / math.sqrt(D))
+    np.testing.assert_allclose(dec, brute, rtol=1e-10, atol=1e-12)
+
+
+def test_decode_kv_lens_equals_truncated_cache():
+    rng = np.random.default_rng(10)
+    q = rng.standard_normal((2, 2, 1, 8)).astype(np.float32)
+    k = rng.standard_normal((2, 1, 64, 8)).astype(np.float32)
+    v = rng.standard_normal((2, 1, 64, 8)).astype(np.float32)
+    m = np.ones((2, 2, 1, 4), dtype=bool)
+    got = orc.sparse_decode(q, k, v, m, 16, kv_lens=[37, 64], dtype=np.float64)
+    ref0 = orc.sparse_decode(q[:1], k[:1, :, :37], v[:1, :, :37], m[:1, :, :, :3], 16, dtype=np.float64)
+    np.testing.assert_allclose(got[:1], ref0, rtol=1e-12)
+
+
+# ----------------------------------------------------------------------------- gate target from q, k
+@pytest.mark.parametrize("causal", [True, False])
+def test_block_max_equals_explicit_scores(causal):
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((1, 4, 45, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 45, 8)).astype(np.float32)
+    sc = 0.3
+    kk = np.repeat(k, 2, axis=1)
+    scores = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), kk.astype(np.float64)) * sc
+    if causal:
+        scores = scores + np.triu(np.full((45, 45), -np.inf), 1)
+    ref = orc.gate_target_from_scores(scores, 16)
+    got = orc.gate_target_from_qk(q, k, 16, causal=causal, scale=sc)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-9)
+    row = orc.gate_target_from_qk(q, k, 16, causal=causal, scale=sc, normalize="row")
+    np.testing.assert_allclose(row.sum(-1), 1.0, rtol=1e-12)
+
+
+def test_gate_target_clamp_temperature_variant():
+    pooled = np.array([[[[100.0, -np.inf], [3.0, -70.0]]]])
+    got = orc.normalize_block_max(pooled, "flat", temperature=2.0, clamp=50.0)
+    ref = torch.softmax(torch.tensor([50.0, -math.inf, 3.0, -50.0], dtype=torch.float64) / 2.0, 0)
+    np.testing.assert_allclose(got.reshape(-1), ref.numpy(), rtol=1e-12)
