@@ -1,0 +1,333 @@
+"""Benchmark of the MI355X block-sparse attention hot path (one GPU).
+
+A step is one pass of the hot path over one batch: the fused AttnGate followed by the
+causal GQA block-sparse prefill at the Llama-3-8B geometry (config 2: B=4, S=8192, 32/8
+heads, D=128, block 64, gate hidden 128, per-head tau for 80% causal sparsity with the
+diagonal forced on). Inputs are resident in HBM before timing. ``value`` is tokens/s of
+the step. The same run also measures, as extra figures, the split-K decode (config 3:
+B=64, S_kv=32768, 51 of 512 blocks per KV head) in HBM GB/s, the Qwen-2.5-7B prefill
+(config 4) and the gate target (config 5), plus a CPU baseline of the oracle on a bounded
+sample of config 2.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-extras] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sparse-attn prefill ms + decode HBM GB/s @80% sparsity, Llama-3-8B shape"
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+FLOP_PER_BLOCK = 4 * 64 * 64 * 128  # QK^T + PV of one 64x64 tile at D=128
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class LaunchTimer:
+    """Sums HIP-event durations of launches on torch's current stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def __enter__(self):
+        self.s = self.torch.cuda.Event(enable_timing=True)
+        self.e = self.torch.cuda.Event(enable_timing=True)
+        self.s.record()
+        return self
+
+    def __exit__(self, *exc):
+        self.e.record()
+        self.pairs.append((self.s, self.e))
+
+    def total_ms(self) -> float:
+        return sum(s.elapsed_time(e) for s, e in self.pairs)
+
+    def reset(self):
+        self.pairs = []
+
+
+class _Span:
+    def __init__(self, timer):
+        self.timer = timer
+
+    def __enter__(self):
+        return self.timer.__enter__()
+
+    def __exit__(self, *exc):
+        return self.timer.__exit__(*exc)
+
+
+def setup_config2(torch, dev):
+    from tasft_amd import workloads as wl
+    from tasft_amd.modules import AttnGate
+
+    shape = wl.CONFIG_SHAPES[2]
+    q, k, v = wl.qkv(shape, 1002)
+    gate = AttnGate(num_heads=shape.q_heads, head_dim=shape.head_dim, block_size=shape.block,
+                    gate_hidden_dim=128)
+    gate.load_state_dict(wl.gate_params(128, shape.head_dim, 3002))
+    gate = gate.to(dev).requires_grad_(False)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    with torch.no_grad():
+        probe = gate(qd, kd, threshold=0.5)
+    taus = wl.per_head_threshold(probe.soft_scores, keep_causal=0.20)
+    return shape, (q, k, v), (qd, kd, vd), gate, taus
+
+
+def bench_config2(torch, dev, steps, warmup):
+    from tasft_amd.kernels import BlockSparseFlashAttention, executed_blocks
+
+    shape, host, (qd, kd, vd), gate, taus = setup_config2(torch, dev)
+    bsfa = BlockSparseFlashAttention(block_size=shape.block, min_sparsity_for_speedup=0.0)
+    t_gate, t_pref = LaunchTimer(torch), LaunchTimer(torch)
+
+    def step():
+        with torch.no_grad():
+            with _Span(t_gate):
+                g = gate(qd, kd, threshold=taus, force_diagonal=True)
+            with _Span(t_pref):
+                out = bsfa.forward(qd, kd, vd, g.hard_mask, causal=True)
+        return g, out
+
+    for _ in range(warmup):
+        g, _out = step()
+    torch.cuda.synchronize()
+    n_exec = int(executed_blocks(g.hard_mask, causal=True).item())
+    nb = shape.nb
+    n_causal = shape.batch * shape.q_heads * nb * (nb + 1) // 2
+    t_gate.reset()
+    t_pref.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    gate_ms = t_gate.total_ms() / steps
+    pref_ms = t_pref.total_ms() / steps
+    flop = n_exec * FLOP_PER_BLOCK
+    gate_bytes = (qd.numel() + kd.numel()) * 2
+    return {
+        "shape": shape,
+        "host": host,
+        "mask": g.hard_mask,
+        "taus": taus,
+        "gate": gate,
+        "ms_per_step": wall_ms / steps,
+        "gate_ms": gate_ms,
+        "prefill_ms": pref_ms,
+        "executed_blocks": n_exec,
+        "causal_sparsity": 1.0 - n_exec / n_causal,
+        "prefill_tflops": flop / (pref_ms * 1e-3) / 1e12,
+        "gate_gbps": gate_bytes / (gate_ms * 1e-3) / 1e9,
+        "tokens": shape.batch * shape.seq,
+    }
+
+
+def bench_decode(torch, dev, steps, warmup):
+    from tasft_amd import workloads as wl
+    from tasft_amd.kernels import BlockSparseFlashAttention
+
+    shape = wl.CONFIG_SHAPES[3]
+    gen = torch.Generator(device=dev).manual_seed(1003)
+    scale = 1.0 / math.sqrt(shape.head_dim)
+    kv_shape = (shape.batch, shape.kv_heads, shape.seq, shape.head_dim)
+    kc = (torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16) * scale)
+    vc = (torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16) * scale)
+    q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1003).to(dev)
+    mask = wl.decode_mask(shape, 51, 2003).to(dev)
+    bsfa = BlockSparseFlashAttention(block_size=shape.block, min_sparsity_for_speedup=0.0)
+    t = LaunchTimer(torch)
+    for _ in range(warmup):
+        bsfa.forward_decode(q, kc, vc, mask)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        with _Span(t):
+            bsfa.forward_decode(q, kc, vc, mask)
+    torch.cuda.synchronize()
+    ms = t.total_ms() / steps
+    grp = shape.q_heads // shape.kv_heads
+    union = mask[:, :, 0, :].reshape(shape.batch, shape.kv_heads, grp, -1).any(dim=2)
+    blocks = int(union.sum().item())
+    kv_bytes = blocks * shape.block * shape.head_dim * 2 * 2
+    small = q.numel() * 2 * 2 + mask.numel()
+    total = kv_bytes + small
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"decode_ms": ms, "decode_hbm_gbps": total / (ms * 1e-3) / 1e9,
+            "decode_bytes": total, "decode_kv_blocks": blocks}
+
+
+def bench_qwen(torch, dev, steps, warmup):
+    from tasft_amd import workloads as wl
+    from tasft_amd.kernels import BlockSparseFlashAttention, executed_blocks
+
+    shape = wl.CONFIG_SHAPES[4]
+    q, k, v = (t.to(dev) for t in wl.qkv(shape, 1004))
+    mask, _ = wl.qwen_mask(shape, 2004)
+    mask = mask.to(dev)
+    bsfa = BlockSparseFlashAttention(block_size=shape.block, min_sparsity_for_speedup=0.0)
+    t = LaunchTimer(torch)
+    for _ in range(warmup):
+        bsfa.forward(q, k, v, mask, causal=True)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        with _Span(t):
+            bsfa.forward(q, k, v, mask, causal=True)
+    torch.cuda.synchronize()
+    ms = t.total_ms() / steps
+    n_exec = int(executed_blocks(mask, True).item())
+    return {"qwen_prefill_ms": ms, "qwen_prefill_tflops": n_exec * FLOP_PER_BLOCK / (ms * 1e-3) / 1e12,
+            "qwen_executed_blocks": n_exec}
+
+
+def bench_gate_target(torch, dev, steps, warmup):
+    from tasft_amd import workloads as wl
+    from tasft_amd.training import gate_target_from_qk
+
+    shape = wl.CONFIG_SHAPES[5]
+    q, k, _ = (t.to(dev) for t in wl.qkv(shape, 1005))
+    t = LaunchTimer(torch)
+    for _ in range(warmup):
+        gate_target_from_qk(q, k, shape.block)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        with _Span(t):
+            gate_target_from_qk(q, k, shape.block)
+    torch.cuda.synchronize()
+    ms = t.total_ms() / steps
+    nb = shape.nb
+    flop = shape.batch * shape.q_heads * nb * (nb + 1) // 2 * 2 * 64 * 64 * 128
+    return {"gate_target_ms": ms, "gate_target_tflops": flop / (ms * 1e-3) / 1e12}
+
+
+def cpu_baseline(res, budget_s: float = 20.0):
+    """Oracle (numpy) gate + block-sparse attention on a sample of config-2 heads."""
+    import numpy as np
+
+    from oracle import tasft_oracle as orc
+
+    try:
+        import threadpoolctl
+        threads = max((i.get("num_threads", 1) for i in threadpoolctl.threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    shape = res["shape"]
+    q, k, v = (t.float().numpy() for t in res["host"])
+    gate = res["gate"]
+    w_in = gate.gate_proj_in.weight.detach().float().cpu().numpy()
+    b_in = gate.gate_proj_in.bias.detach().float().cpu().numpy()
+    w_out = gate.gate_proj_out.weight.detach().float().cpu().numpy()
+    taus = res["taus"].cpu().numpy()
+    grp = shape.q_heads // shape.kv_heads
+    order = [(b, h) for b in range(shape.batch) for h in range(shape.q_heads)]
+    rng = np.random.default_rng(0)
+    rng.shuffle(order)
+    done, t0 = 0, time.perf_counter()
+    for b, h in order:
+        qh, kh, vh = q[b : b + 1, h : h + 1], k[b : b + 1, h // grp : h // grp + 1], v[b : b + 1, h // grp : h // grp + 1]
+        logits = orc.gate_logits(qh, kh, w_in, b_in, w_out, shape.block)
+        _, hard = orc.threshold_mask(logits, float(taus[h]), True)
+        hard = hard | np.eye(shape.nb, dtype=bool)
+        orc.attention_block_gather(qh, kh, vh, hard, shape.block, True)
+        done += 1
+        if time.perf_counter() - t0 > budget_s or done >= 32:
+            break
+    per_head = (time.perf_counter() - t0) / done
+    total_s = per_head * len(order)
+    return {"value": shape.batch * shape.seq / total_s, "unit": "tokens/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"oracle gate + block-gather attention (numpy fp32) on {done} of {len(order)} "
+                      f"(batch, head) pairs of config 2, scaled linearly to all heads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extras", action="store_true", help="skip decode / Qwen / gate-target figures")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU layout is "
+              "described in DESIGN.md and is not run here", file=sys.stderr)
+        return 2
+    import torch
+
+    dev = torch.device("cuda:0")
+    log("bench: config 2 gate + prefill")
+    res = bench_config2(torch, dev, args.steps, args.warmup)
+    extra = {
+        "gate_ms": round(res["gate_ms"], 4),
+        "prefill_ms": round(res["prefill_ms"], 4),
+        "prefill_tflops_executed": round(res["prefill_tflops"], 1),
+        "gate_hbm_gbps": round(res["gate_gbps"], 1),
+        "executed_blocks": res["executed_blocks"],
+        "causal_sparsity": round(res["causal_sparsity"], 4),
+    }
+    if not args.no_extras:
+        log("bench: config 3 decode")
+        d = bench_decode(torch, dev, max(10, args.steps), args.warmup)
+        extra.update({"decode_ms": round(d["decode_ms"], 4), "decode_hbm_gbps": round(d["decode_hbm_gbps"], 1),
+                      "decode_hbm_frac": round(d["decode_hbm_gbps"] / PEAK_HBM_GBPS, 4),
+                      "decode_bytes": d["decode_bytes"]})
+        log("bench: config 4 Qwen prefill")
+        qw = bench_qwen(torch, dev, max(5, args.steps // 2), min(3, args.warmup))
+        extra.update({"qwen_prefill_ms": round(qw["qwen_prefill_ms"], 4),
+                      "qwen_prefill_tflops_executed": round(qw["qwen_prefill_tflops"], 1)})
+        log("bench: config 5 gate target")
+        gt = bench_gate_target(torch, dev, max(5, args.steps // 2), min(3, args.warmup))
+        extra.update({"gate_target_ms": round(gt["gate_target_ms"], 4),
+                      "gate_target_tflops": round(gt["gate_target_tflops"], 1)})
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline")
+        cpu = cpu_baseline(res)
+    achieved = res["prefill_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": round(res["tokens"] / (res["ms_per_step"] * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "config 2: fused AttnGate + causal GQA block-sparse prefill, Llama-3-8B geometry",
+            "batch": res["shape"].batch, "seq_len": res["shape"].seq, "q_heads": res["shape"].q_heads,
+            "kv_heads": res["shape"].kv_heads, "head_dim": res["shape"].head_dim,
+            "block": res["shape"].block, "gate_hidden": 128, "target_causal_sparsity": 0.8,
+        },
+        "roofline": {
+            "kernel": "bsfa_prefill_kernel<64,128>",
+            "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "algorithmic": f"{res['executed_blocks']} executed 64x64 blocks x {FLOP_PER_BLOCK} flop",
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
