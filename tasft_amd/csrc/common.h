@@ -16,6 +16,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+#define TASFT_LDS __attribute__((address_space(3)))
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -63,6 +66,16 @@ __device__ __forceinline__ f32x16_t mfma_32x32x16_bf16(const bf16x8_t& a, const 
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each group of 16 lanes,
+// lane t receives element t%4 of the 8-byte chunks addressed by lanes t/4, t/4+4,
+// t/4+8 and t/4+12 of its group. If source lane s addresses row R0 + s/4, columns
+// C0 + 4*(s%4) .. +3 of a row-major 16-bit matrix, lane t receives rows R0..R0+3 of
+// column C0 + t: a 4x16 tile read transposed.
+__device__ __forceinline__ u32x2_t ds_read_tr16_b64(const void* lds_byte_addr) {
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TASFT_LDS i16x4_t*)lds_byte_addr);
+  return __builtin_bit_cast(u32x2_t, v);
 }
 
 // Exchange a value with the lane 32 positions away (lane l <-> lane l^32).

@@ -245,6 +245,282 @@ static hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------------------
+// Block size 64: the tuned kernel.
+//
+// Four waves per (batch, query head, query block): wave w owns query rows 32*(w&1)..+31
+// and the key half 32*(w>>1)..+31 of every key block, so each wave issues 8 + D/16 MFMAs
+// per block and two waves share a SIMD. The two key-half partial results of a row are
+// merged once at the end. K and V of the next active block are loaded into registers
+// while the current block is computed, then written to LDS row-major with a 16-byte XOR
+// swizzle (conflict-free without padding). V^T operands come from ds_read_b64_tr_b16, so
+// V is never transposed by VALU. The softmax rescale is lazy: the running maximum used
+// for exp2 is only moved when a new score exceeds it by more than kRescaleLog2 (so P
+// stays <= 2^8); numerator and denominator share the same reference, so the normalised
+// output is unchanged.
+// ---------------------------------------------------------------------------------------
+constexpr float kRescaleLog2 = 8.f;
+
+// 16-byte chunk position of chunk `cc` of K row `r` in LDS.
+template <int D>
+__device__ __forceinline__ int swz_k(int r, int cc) {
+  return cc ^ (D == 128 ? (r & 15) : ((r >> 1) & 7));
+}
+// Same for V rows (read through ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes).
+template <int D>
+__device__ __forceinline__ int swz_v(int r, int cc) {
+  return cc ^ (D == 128 ? ((r & 3) << 1) : (((r >> 1) & 1) << 1));
+}
+
+// Next active key block of a mask row, scanning 64 mask bytes per ballot. Returns -1 at
+// the end. All lanes of all waves see the same sequence.
+__device__ __forceinline__ int next_active_block(const uint8_t* mrow, int64_t stride, int kb_end,
+                                                 int lane, int& chunk, uint64_t& bits) {
+  while (bits == 0) {
+    chunk += kWave;
+    if (chunk >= kb_end) return -1;
+    const int kbl = chunk + lane;
+    bits = __ballot(kbl < kb_end && mrow[(int64_t)kbl * stride] != 0);
+  }
+  const int kb = chunk + __builtin_ctzll(bits);
+  bits &= bits - 1;
+  return kb;
+}
+
+template <int D>
+__global__ void __launch_bounds__(256, 2)
+bsfa_prefill_bs64_kernel(const PrefillParams p) {
+  constexpr int BS = 64;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DTILES = D / 32;
+  constexpr int ROWB = D * 2;            // bytes per K/V row in LDS
+  constexpr int CPR = D / 8;             // 16-byte chunks per row
+  constexpr int CHUNKS = BS * CPR / 256; // chunks per thread per tensor
+
+  // K and V stages are one buffer so the final merge can reuse all of it (2*BS*ROWB
+  // bytes = 2 waves x DTILES*16 floats x 64 lanes).
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2 * BS * ROWB];
+  __shared__ float xch_ml[2][2][kWave];
+  uint8_t* const k_lds = kv_lds;
+  uint8_t* const v_lds = kv_lds + BS * ROWB;
+  static_assert(2 * DTILES * 16 * kWave * 4 == 2 * BS * ROWB, "merge buffer size");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rh = wave & 1;   // row half
+  const int kh = wave >> 1;  // key half
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // Work item: each XCD walks one KV group at a time (all its query heads and query
+  // blocks, longest causal rows first) so the group's K/V stays in that XCD's L2.
+  const int64_t idx = blockIdx.x;
+  const int64_t groups = (int64_t)p.B * p.Hkv;
+  const int64_t per_group = (int64_t)p.G * p.NB;
+  int64_t grp, r;
+  if ((groups & 7) == 0) {
+    const int64_t j = idx >> 3;
+    grp = (idx & 7) + 8 * (j / per_group);
+    r = j % per_group;
+  } else {
+    grp = idx / per_group;
+    r = idx % per_group;
+  }
+  const int qslot = (int)(r / p.G);
+  const int g = (int)(r % p.G);
+  const int qb = p.causal ? (p.NB - 1 - qslot) : qslot;
+  const int b = (int)(grp / p.Hkv);
+  const int kvh = (int)(grp % p.Hkv);
+  const int h = kvh * p.G + g;
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
+  uint16_t* obase = p.o + b * p.so[0] + h * p.so[1];
+  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
+
+  const int qrow = qb * BS + rh * 32 + col;
+  const bool qvalid = qrow < p.S;
+  bf16x8_t qf[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    u32x4_t val = {0u, 0u, 0u, 0u};
+    if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
+    qf[ks] = as_bf16x8(val);
+  }
+
+  // Register staging of one K/V block: thread tid owns chunks tid + 256*i.
+  u32x4_t kreg[CHUNKS], vreg[CHUNKS];
+  auto load_block = [&](int kb) {
+    const int key0 = kb * BS;
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, cc = c % CPR;
+      const bool ok = key0 + row < p.S;
+      const int64_t krow = ok ? (int64_t)(key0 + row) : 0;
+      kreg[i] = *(const u32x4_t*)(kbase + krow * p.sk[2] + cc * 8);
+      vreg[i] = *(const u32x4_t*)(vbase + krow * p.sv[2] + cc * 8);
+      if (!ok) {
+        kreg[i] = (u32x4_t){0u, 0u, 0u, 0u};
+        vreg[i] = (u32x4_t){0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto store_block = [&]() {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, cc = c % CPR;
+      *(u32x4_t*)(k_lds + row * ROWB + swz_k<D>(row, cc) * 16) = kreg[i];
+      *(u32x4_t*)(v_lds + row * ROWB + swz_v<D>(row, cc) * 16) = vreg[i];
+    }
+  };
+
+  f32x16_t oacc[DTILES];
+#pragma unroll
+  for (int dt = 0; dt < DTILES; ++dt) oacc[dt] = (f32x16_t){};
+  float m_ref = -INFINITY;  // exp2 reference of this lane's query row (log2 domain)
+  float l_run = 0.f;
+
+  // Per-lane constant parts of the LDS addresses.
+  const int krow_l = kh * 32 + col;                 // K row read by this lane
+  const int grp16 = lane >> 4, t16 = lane & 15;      // ds_read_tr group and lane in group
+  const int tr_row = t16 >> 2;                       // source row offset within a 4-row run
+  const int tr_cb = (t16 & 3);                       // source 8-byte column block
+
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  int chunk = -kWave;
+  uint64_t bits = 0;
+  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+  if (kb >= 0) load_block(kb);
+  while (kb >= 0) {
+    __syncthreads();  // every wave finished reading the previous block
+    store_block();
+    __syncthreads();
+    const int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    if (kb_next >= 0) load_block(kb_next);  // in flight while this block is computed
+
+    const int key0 = kb * BS;
+    // S^T tile: 32 keys (this wave's half) x 32 query rows.
+    f32x16_t s = (f32x16_t){};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cc = ks * 2 + half;
+      const u32x4_t a = *(const u32x4_t*)(k_lds + krow_l * ROWB + swz_k<D>(krow_l, cc) * 16);
+      s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
+    }
+    const bool need_mask = (p.causal && kb == qb) || (key0 + BS > p.S);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      float x = s[rr] * p.scale_log2;
+      if (need_mask) {
+        const int key = key0 + kh * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+        if (key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
+      }
+      s[rr] = x;
+      mloc = fmaxf(mloc, x);
+    }
+    mloc = fmaxf(mloc, xor32(mloc));
+    // Lazy rescale: move the reference only when a score exceeds it by kRescaleLog2.
+    const bool move = mloc > m_ref + kRescaleLog2;
+    if (__ballot(move)) {
+      // exp2(-inf) = 0 clears the (empty) accumulators on a row's first finite score.
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - mloc) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) oacc[dt] *= alpha;
+      m_ref = move ? mloc : m_ref;
+    }
+    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+    float lsum = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const float e = __builtin_amdgcn_exp2f(s[rr] - m_use);
+      s[rr] = e;
+      lsum += e;
+    }
+    l_run += lsum;
+
+    // O^T += V^T P^T over this wave's 32 keys: two k-steps of 16 keys.
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const u32x4_t w = {pack_bf16x2(s[8 * pp + 0], s[8 * pp + 1]),
+                         pack_bf16x2(s[8 * pp + 2], s[8 * pp + 3]),
+                         pack_bf16x2(s[8 * pp + 4], s[8 * pp + 5]),
+                         pack_bf16x2(s[8 * pp + 6], s[8 * pp + 7])};
+      const bf16x8_t pb = as_bf16x8(w);
+      const int kbase_k = kh * 32 + 16 * pp + 4 * (grp16 >> 1);  // first key of run 1
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+        const int d0 = dt * 32 + 16 * (grp16 & 1) + 4 * tr_cb;  // source column of this lane
+        const int cc = d0 >> 3, sub = (d0 & 7) * 2;
+        const int r1 = kbase_k + tr_row, r2 = r1 + 8;
+        const u32x2_t lo = ds_read_tr16_b64(v_lds + r1 * ROWB + swz_v<D>(r1, cc) * 16 + sub);
+        const u32x2_t hi = ds_read_tr16_b64(v_lds + r2 * ROWB + swz_v<D>(r2, cc) * 16 + sub);
+        const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
+        oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb, oacc[dt]);
+      }
+    }
+    kb = kb_next;
+  }
+
+  // Merge the two key halves of each row: waves 2,3 hand (m, l, O^T) to waves 0,1.
+  const float l_tot = l_run + xor32(l_run);
+  __syncthreads();
+  float* xo = (float*)kv_lds;
+  if (kh == 1) {
+    if (half == 0) {
+      xch_ml[rh][0][col] = m_ref;
+      xch_ml[rh][1][col] = l_tot;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) xo[((rh * DTILES + dt) * 16 + rr) * kWave + lane] = oacc[dt][rr];
+  }
+  __syncthreads();
+  if (kh == 0) {
+    const float m2 = xch_ml[rh][0][col];
+    const float l2 = xch_ml[rh][1][col];
+    const float M = fmaxf(m_ref, m2);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    const float f1 = __builtin_amdgcn_exp2f(m_ref - Mu);  // 0 for an empty half
+    const float f2 = __builtin_amdgcn_exp2f(m2 - Mu);
+    const float L = l_tot * f1 + l2 * f2;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    if (qvalid) {
+      uint16_t* orow = obase + (int64_t)qrow * p.so[2];
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          float o4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int rr = 4 * gq + e;
+            const float o2 = xo[((rh * DTILES + dt) * 16 + rr) * kWave + lane];
+            o4[e] = (oacc[dt][rr] * f1 + o2 * f2) * inv;
+          }
+          const int d0 = dt * 32 + 8 * gq + 4 * half;
+          const u32x2_t w = {pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
+          *(u32x2_t*)(orow + d0) = w;
+        }
+      }
+    }
+  }
+}
+
+template <int D>
+static hipError_t launch_prefill_bs64(const PrefillParams& p, hipStream_t stream) {
+  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
+  hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace tasft
@@ -313,8 +589,8 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_prefill<64, 128>(p, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_prefill<64, 64>(p, s);
+  if (block_size == 64 && head_dim == 128) err = launch_prefill_bs64<128>(p, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_prefill_bs64<64>(p, s);
   else if (block_size == 32 && head_dim == 128) err = launch_prefill<32, 128>(p, s);
   else if (block_size == 32 && head_dim == 64) err = launch_prefill<32, 64>(p, s);
   else if (block_size == 128 && head_dim == 128) err = launch_prefill<128, 128>(p, s);
