@@ -49,14 +49,14 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4_t& v, float* out) {
   }
 }
 
-// Round-to-nearest-even fp32 -> bf16 of two values packed in one dword.
-// gfx950 lowers this conversion to v_cvt_pk_bf16_f32.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 -> bf16 of two values packed in one dword
+// (one v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = (__bf16)lo;
-  __bf16 b = (__bf16)hi;
-  uint16_t ua = __builtin_bit_cast(uint16_t, a);
-  uint16_t ub = __builtin_bit_cast(uint16_t, b);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
+  const bf16x2_t v = __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ f32x16_t mfma_32x32x16_bf16(const bf16x8_t& a, const bf16x8_t& b,
@@ -80,6 +80,20 @@ __device__ __forceinline__ u32x2_t ds_read_tr16_b64(const void* lds_byte_addr) {
 
 // Exchange a value with the lane 32 positions away (lane l <-> lane l^32).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// max / sum of a value over the lane pair (l, l^32) with v_permlane32_swap (gfx950):
+// swapping the upper half of one copy with the lower half of another leaves the pair's
+// two values in the two results, in the same order on both lanes.
+__device__ __forceinline__ float pair_max32(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -267,10 +267,11 @@ template <int D>
 __device__ __forceinline__ int swz_k(int r, int cc) {
   return cc ^ (D == 128 ? (r & 15) : ((r >> 1) & 7));
 }
-// Same for V rows (read through ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes).
+// Same for V rows. ds_read_b64_tr_b16 serves 32 lanes (256 bytes) per LDS cycle: 4 rows
+// x 4 chunks, which this swizzle spreads over all 64 banks.
 template <int D>
 __device__ __forceinline__ int swz_v(int r, int cc) {
-  return cc ^ (D == 128 ? ((r & 3) << 1) : (((r >> 1) & 1) << 1));
+  return cc ^ (D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2));
 }
 
 // Next active key block of a mask row, scanning 64 mask bytes per ballot. Returns -1 at
@@ -351,31 +352,48 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     qf[ks] = as_bf16x8(val);
   }
 
-  // Register staging of one K/V block: thread tid owns chunks tid + 256*i.
+  // Register staging of one K/V block: thread tid owns chunks tid + 256*i. Element
+  // offsets inside a block and LDS byte offsets are loop invariant. Rows past the end
+  // of the sequence (only in a partial last block) are clamped to the last row: their
+  // scores are masked to -inf and their P is exactly 0, so no zero fill is needed and
+  // nothing waits on the loads before the next block's LDS store.
   u32x4_t kreg[CHUNKS], vreg[CHUNKS];
+  int krow_of[CHUNKS], kelt[CHUNKS], velt[CHUNKS], klds[CHUNKS], vlds[CHUNKS];
+#pragma unroll
+  for (int i = 0; i < CHUNKS; ++i) {
+    const int c = tid + 256 * i;
+    const int row = c / CPR, cc = c % CPR;
+    krow_of[i] = row;
+    kelt[i] = row * (int)p.sk[2] + cc * 8;
+    velt[i] = row * (int)p.sv[2] + cc * 8;
+    klds[i] = row * ROWB + swz_k<D>(row, cc) * 16;
+    vlds[i] = row * ROWB + swz_v<D>(row, cc) * 16;
+  }
   auto load_block = [&](int kb) {
     const int key0 = kb * BS;
+    const uint16_t* kb_ptr = kbase + (int64_t)key0 * p.sk[2];
+    const uint16_t* vb_ptr = vbase + (int64_t)key0 * p.sv[2];
+    if (key0 + BS <= p.S) {
 #pragma unroll
-    for (int i = 0; i < CHUNKS; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / CPR, cc = c % CPR;
-      const bool ok = key0 + row < p.S;
-      const int64_t krow = ok ? (int64_t)(key0 + row) : 0;
-      kreg[i] = *(const u32x4_t*)(kbase + krow * p.sk[2] + cc * 8);
-      vreg[i] = *(const u32x4_t*)(vbase + krow * p.sv[2] + cc * 8);
-      if (!ok) {
-        kreg[i] = (u32x4_t){0u, 0u, 0u, 0u};
-        vreg[i] = (u32x4_t){0u, 0u, 0u, 0u};
+      for (int i = 0; i < CHUNKS; ++i) {
+        kreg[i] = *(const u32x4_t*)(kb_ptr + kelt[i]);
+        vreg[i] = *(const u32x4_t*)(vb_ptr + velt[i]);
+      }
+    } else {
+      const int last = p.S - 1 - key0;
+#pragma unroll
+      for (int i = 0; i < CHUNKS; ++i) {
+        const int shift = krow_of[i] > last ? (krow_of[i] - last) : 0;
+        kreg[i] = *(const u32x4_t*)(kb_ptr + kelt[i] - shift * (int)p.sk[2]);
+        vreg[i] = *(const u32x4_t*)(vb_ptr + velt[i] - shift * (int)p.sv[2]);
       }
     }
   };
   auto store_block = [&]() {
 #pragma unroll
     for (int i = 0; i < CHUNKS; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c / CPR, cc = c % CPR;
-      *(u32x4_t*)(k_lds + row * ROWB + swz_k<D>(row, cc) * 16) = kreg[i];
-      *(u32x4_t*)(v_lds + row * ROWB + swz_v<D>(row, cc) * 16) = vreg[i];
+      *(u32x4_t*)(k_lds + klds[i]) = kreg[i];
+      *(u32x4_t*)(v_lds + vlds[i]) = vreg[i];
     }
   };
 
@@ -412,19 +430,19 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
       const u32x4_t a = *(const u32x4_t*)(k_lds + krow_l * ROWB + swz_k<D>(krow_l, cc) * 16);
       s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
     }
-    const bool need_mask = (p.causal && kb == qb) || (key0 + BS > p.S);
-    float mloc = -INFINITY;
+    // Causal diagonal block or partial last block: mask in one uniform branch.
+    if ((p.causal && kb == qb) || (key0 + BS > p.S)) {
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      float x = s[rr] * p.scale_log2;
-      if (need_mask) {
+      for (int rr = 0; rr < 16; ++rr) {
         const int key = key0 + kh * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-        if (key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
+        s[rr] = (key >= p.S || (p.causal && key > qrow)) ? -INFINITY : s[rr];
       }
-      s[rr] = x;
-      mloc = fmaxf(mloc, x);
     }
-    mloc = fmaxf(mloc, xor32(mloc));
+    // Scores stay unscaled: scale > 0 commutes with max, and exp2 takes one FMA.
+    float mraw = s[0];
+#pragma unroll
+    for (int rr = 1; rr < 16; ++rr) mraw = fmaxf(mraw, s[rr]);
+    const float mloc = pair_max32(mraw) * p.scale_log2;
     // Lazy rescale: move the reference only when a score exceeds it by kRescaleLog2.
     const bool move = mloc > m_ref + kRescaleLog2;
     if (__ballot(move)) {
@@ -439,7 +457,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     float lsum = 0.f;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
-      const float e = __builtin_amdgcn_exp2f(s[rr] - m_use);
+      const float e = __builtin_amdgcn_exp2f(fmaf(s[rr], p.scale_log2, -m_use));
       s[rr] = e;
       lsum += e;
     }
@@ -469,7 +487,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   }
 
   // Merge the two key halves of each row: waves 2,3 hand (m, l, O^T) to waves 0,1.
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = pair_sum32(l_run);
   __syncthreads();
   float* xo = (float*)kv_lds;
   if (kh == 1) {
