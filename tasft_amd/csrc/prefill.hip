@@ -289,23 +289,41 @@ __device__ __forceinline__ int next_active_block(const uint8_t* mrow, int64_t st
   return kb;
 }
 
+// One 64 x D bf16 tile in LDS, written by global_load_lds_dwordx4 (DMA, no VGPRs).
+// Unit u (1 KB, one instruction of one wave) covers bytes u*1024 .. +1023 of the tile;
+// lane l of that instruction lands at byte u*1024 + 16*l, i.e. row (u*1024+16l)/ROWB,
+// 16-byte position ((u*1024+16l)%ROWB)/16. The lane therefore loads the global chunk
+// that the swizzle maps to that position (the XOR swizzles are involutions).
+template <int D>
+__device__ __forceinline__ void dma_tile(uint8_t* tile, const uint16_t* src, const int* elt,
+                                         int wave) {
+  constexpr int UNITS_PER_WAVE = (64 * D * 2 / 1024) / 4;
+#pragma unroll
+  for (int i = 0; i < UNITS_PER_WAVE; ++i) {
+    const int u = wave * UNITS_PER_WAVE + i;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + elt[i]),
+                                     (TASFT_LDS void*)(tile + u * 1024), 16, 0, 0);
+  }
+}
+
 template <int D>
 __global__ void __launch_bounds__(256, 2)
 bsfa_prefill_bs64_kernel(const PrefillParams p) {
   constexpr int BS = 64;
   constexpr int KSTEPS = D / 16;
   constexpr int DTILES = D / 32;
-  constexpr int ROWB = D * 2;            // bytes per K/V row in LDS
-  constexpr int CPR = D / 8;             // 16-byte chunks per row
-  constexpr int CHUNKS = BS * CPR / 256; // chunks per thread per tensor
+  constexpr int ROWB = D * 2;                        // bytes per K/V row in LDS
+  constexpr int TILE = BS * ROWB;                    // one K or V tile
+  constexpr int UNITS_PER_WAVE = (TILE / 1024) / 4;  // DMA instructions per wave per tile
 
-  // K and V stages are one buffer so the final merge can reuse all of it (2*BS*ROWB
-  // bytes = 2 waves x DTILES*16 floats x 64 lanes).
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2 * BS * ROWB];
+  // Two stages (A, B) of K and V tiles, each its own LDS object so that reads of one
+  // stage are not ordered behind DMA into the other.
+  __shared__ __attribute__((aligned(1024))) uint8_t kA[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t vA[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t kB[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t vB[TILE];
   __shared__ float xch_ml[2][2][kWave];
-  uint8_t* const k_lds = kv_lds;
-  uint8_t* const v_lds = kv_lds + BS * ROWB;
-  static_assert(2 * DTILES * 16 * kWave * 4 == 2 * BS * ROWB, "merge buffer size");
+  static_assert(DTILES * 16 * kWave * 4 == TILE, "merge buffer size");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -352,49 +370,33 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     qf[ks] = as_bf16x8(val);
   }
 
-  // Register staging of one K/V block: thread tid owns chunks tid + 256*i. Element
-  // offsets inside a block and LDS byte offsets are loop invariant. Rows past the end
-  // of the sequence (only in a partial last block) are clamped to the last row: their
-  // scores are masked to -inf and their P is exactly 0, so no zero fill is needed and
-  // nothing waits on the loads before the next block's LDS store.
-  u32x4_t kreg[CHUNKS], vreg[CHUNKS];
-  int krow_of[CHUNKS], kelt[CHUNKS], velt[CHUNKS], klds[CHUNKS], vlds[CHUNKS];
+  // Per-lane source rows and element offsets of this wave's DMA units.
+  int urow[UNITS_PER_WAVE], kelt[UNITS_PER_WAVE], velt[UNITS_PER_WAVE];
 #pragma unroll
-  for (int i = 0; i < CHUNKS; ++i) {
-    const int c = tid + 256 * i;
-    const int row = c / CPR, cc = c % CPR;
-    krow_of[i] = row;
-    kelt[i] = row * (int)p.sk[2] + cc * 8;
-    velt[i] = row * (int)p.sv[2] + cc * 8;
-    klds[i] = row * ROWB + swz_k<D>(row, cc) * 16;
-    vlds[i] = row * ROWB + swz_v<D>(row, cc) * 16;
+  for (int i = 0; i < UNITS_PER_WAVE; ++i) {
+    const int byte = (wave * UNITS_PER_WAVE + i) * 1024 + lane * 16;
+    const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+    urow[i] = row;
+    kelt[i] = row * (int)p.sk[2] + swz_k<D>(row, pos) * 8;
+    velt[i] = row * (int)p.sv[2] + swz_v<D>(row, pos) * 8;
   }
-  auto load_block = [&](int kb) {
+  // Start the DMA of key block kb into one stage. Rows past the end of the sequence
+  // (partial last block) are clamped to the last row: their scores are masked to -inf
+  // and their P is exactly 0.
+  auto issue = [&](uint8_t* kt, uint8_t* vt, int kb) {
     const int key0 = kb * BS;
-    const uint16_t* kb_ptr = kbase + (int64_t)key0 * p.sk[2];
-    const uint16_t* vb_ptr = vbase + (int64_t)key0 * p.sv[2];
-    if (key0 + BS <= p.S) {
+    const uint16_t* kp = kbase + (int64_t)key0 * p.sk[2];
+    const uint16_t* vp = vbase + (int64_t)key0 * p.sv[2];
+    int ke[UNITS_PER_WAVE], ve[UNITS_PER_WAVE];
+    const int last = p.S - 1 - key0;
 #pragma unroll
-      for (int i = 0; i < CHUNKS; ++i) {
-        kreg[i] = *(const u32x4_t*)(kb_ptr + kelt[i]);
-        vreg[i] = *(const u32x4_t*)(vb_ptr + velt[i]);
-      }
-    } else {
-      const int last = p.S - 1 - key0;
-#pragma unroll
-      for (int i = 0; i < CHUNKS; ++i) {
-        const int shift = krow_of[i] > last ? (krow_of[i] - last) : 0;
-        kreg[i] = *(const u32x4_t*)(kb_ptr + kelt[i] - shift * (int)p.sk[2]);
-        vreg[i] = *(const u32x4_t*)(vb_ptr + velt[i] - shift * (int)p.sv[2]);
-      }
+    for (int i = 0; i < UNITS_PER_WAVE; ++i) {
+      const int shift = urow[i] > last ? (urow[i] - last) : 0;
+      ke[i] = kelt[i] - shift * (int)p.sk[2];
+      ve[i] = velt[i] - shift * (int)p.sv[2];
     }
-  };
-  auto store_block = [&]() {
-#pragma unroll
-    for (int i = 0; i < CHUNKS; ++i) {
-      *(u32x4_t*)(k_lds + klds[i]) = kreg[i];
-      *(u32x4_t*)(v_lds + vlds[i]) = vreg[i];
-    }
+    dma_tile<D>(kt, kp, ke, wave);
+    dma_tile<D>(vt, vp, ve, wave);
   };
 
   f32x16_t oacc[DTILES];
@@ -403,33 +405,21 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   float m_ref = -INFINITY;  // exp2 reference of this lane's query row (log2 domain)
   float l_run = 0.f;
 
-  // Per-lane constant parts of the LDS addresses.
-  const int krow_l = kh * 32 + col;                 // K row read by this lane
-  const int grp16 = lane >> 4, t16 = lane & 15;      // ds_read_tr group and lane in group
-  const int tr_row = t16 >> 2;                       // source row offset within a 4-row run
-  const int tr_cb = (t16 & 3);                       // source 8-byte column block
+  const int krow_l = kh * 32 + col;
+  const int grp16 = lane >> 4, t16 = lane & 15;  // ds_read_tr group and lane in group
+  const int tr_row = t16 >> 2;                   // source row offset within a 4-row run
+  const int tr_cb = t16 & 3;                     // source 8-byte column block
 
-  const int kb_end = p.causal ? qb + 1 : p.NB;
-  int chunk = -kWave;
-  uint64_t bits = 0;
-  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
-  if (kb >= 0) load_block(kb);
-  while (kb >= 0) {
-    __syncthreads();  // every wave finished reading the previous block
-    store_block();
-    __syncthreads();
-    const int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
-    if (kb_next >= 0) load_block(kb_next);  // in flight while this block is computed
-
-    const int key0 = kb * BS;
-    // S^T tile: 32 keys (this wave's half) x 32 query rows.
+  // One key block from stage (kt, vt): S^T MFMAs, online softmax, PV MFMAs.
+  auto compute = [&](const uint8_t* kt, const uint8_t* vt, int kb) {
     f32x16_t s = (f32x16_t){};
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cc = ks * 2 + half;
-      const u32x4_t a = *(const u32x4_t*)(k_lds + krow_l * ROWB + swz_k<D>(krow_l, cc) * 16);
+      const u32x4_t a = *(const u32x4_t*)(kt + krow_l * ROWB + swz_k<D>(krow_l, cc) * 16);
       s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
     }
+    const int key0 = kb * BS;
     // Causal diagonal block or partial last block: mask in one uniform branch.
     if ((p.causal && kb == qb) || (key0 + BS > p.S)) {
 #pragma unroll
@@ -462,7 +452,6 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
       lsum += e;
     }
     l_run += lsum;
-
     // O^T += V^T P^T over this wave's 32 keys: two k-steps of 16 keys.
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
@@ -477,19 +466,40 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
         const int d0 = dt * 32 + 16 * (grp16 & 1) + 4 * tr_cb;  // source column of this lane
         const int cc = d0 >> 3, sub = (d0 & 7) * 2;
         const int r1 = kbase_k + tr_row, r2 = r1 + 8;
-        const u32x2_t lo = ds_read_tr16_b64(v_lds + r1 * ROWB + swz_v<D>(r1, cc) * 16 + sub);
-        const u32x2_t hi = ds_read_tr16_b64(v_lds + r2 * ROWB + swz_v<D>(r2, cc) * 16 + sub);
+        const u32x2_t lo = ds_read_tr16_b64((const void*)(vt + r1 * ROWB + swz_v<D>(r1, cc) * 16 + sub));
+        const u32x2_t hi = ds_read_tr16_b64((const void*)(vt + r2 * ROWB + swz_v<D>(r2, cc) * 16 + sub));
         const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
         oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb, oacc[dt]);
       }
     }
+  };
+
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  int chunk = -kWave;
+  uint64_t bits = 0;
+  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+  if (kb >= 0) issue(kA, vA, kb);
+  // Unrolled by two so each stage is a fixed LDS object.
+  while (kb >= 0) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's DMA of block kb landed
+    __syncthreads();                      // every wave's DMA landed; stage B is free
+    int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    if (kb_next >= 0) issue(kB, vB, kb_next);
+    compute(kA, vA, kb);
+    kb = kb_next;
+    if (kb < 0) break;
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    if (kb_next >= 0) issue(kA, vA, kb_next);
+    compute(kB, vB, kb);
     kb = kb_next;
   }
 
   // Merge the two key halves of each row: waves 2,3 hand (m, l, O^T) to waves 0,1.
   const float l_tot = pair_sum32(l_run);
   __syncthreads();
-  float* xo = (float*)kv_lds;
+  float* xo = (float*)(rh == 0 ? kA : vA);
   if (kh == 1) {
     if (half == 0) {
       xch_ml[rh][0][col] = m_ref;
@@ -498,7 +508,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt)
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) xo[((rh * DTILES + dt) * 16 + rr) * kWave + lane] = oacc[dt][rr];
+      for (int rr = 0; rr < 16; ++rr) xo[(dt * 16 + rr) * kWave + lane] = oacc[dt][rr];
   }
   __syncthreads();
   if (kh == 0) {
@@ -520,8 +530,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int rr = 4 * gq + e;
-            const float o2 = xo[((rh * DTILES + dt) * 16 + rr) * kWave + lane];
-            o4[e] = (oacc[dt][rr] * f1 + o2 * f2) * inv;
+            o4[e] = (oacc[dt][rr] * f1 + xo[(dt * 16 + rr) * kWave + lane] * f2) * inv;
           }
           const int d0 = dt * 32 + 8 * gq + 4 * half;
           const u32x2_t w = {pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
