@@ -289,21 +289,29 @@ __device__ __forceinline__ int next_active_block(const uint8_t* mrow, int64_t st
   return kb;
 }
 
-// One 64 x D bf16 tile in LDS, written by global_load_lds_dwordx4 (DMA, no VGPRs).
+// One 64 x D bf16 tile in LDS, written by buffer_load_dwordx4 ... lds (DMA, no VGPRs).
 // Unit u (1 KB, one instruction of one wave) covers bytes u*1024 .. +1023 of the tile;
 // lane l of that instruction lands at byte u*1024 + 16*l, i.e. row (u*1024+16l)/ROWB,
 // 16-byte position ((u*1024+16l)%ROWB)/16. The lane therefore loads the global chunk
-// that the swizzle maps to that position (the XOR swizzles are involutions).
+// that the swizzle maps to that position (the XOR swizzles are involutions). The
+// buffer resource starts at the tile's first row and ends after row S-1, so rows past
+// the end of the sequence are out of range and land in LDS as zeros.
 template <int D>
-__device__ __forceinline__ void dma_tile(uint8_t* tile, const uint16_t* src, const int* elt,
-                                         int wave) {
+__device__ __forceinline__ void dma_tile(uint8_t* tile, __amdgpu_buffer_rsrc_t rsrc,
+                                         const int* voff, int wave) {
   constexpr int UNITS_PER_WAVE = (64 * D * 2 / 1024) / 4;
 #pragma unroll
   for (int i = 0; i < UNITS_PER_WAVE; ++i) {
     const int u = wave * UNITS_PER_WAVE + i;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + elt[i]),
-                                     (TASFT_LDS void*)(tile + u * 1024), 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (TASFT_LDS void*)(tile + u * 1024), 16, voff[i], 0,
+                                             0, 0);
   }
+}
+
+// Raw buffer resource (stride 0) over `bytes` bytes starting at `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
 template <int D>
@@ -370,33 +378,21 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     qf[ks] = as_bf16x8(val);
   }
 
-  // Per-lane source rows and element offsets of this wave's DMA units.
-  int urow[UNITS_PER_WAVE], kelt[UNITS_PER_WAVE], velt[UNITS_PER_WAVE];
+  // Per-lane byte offsets (within a tile's rows) of this wave's DMA units.
+  int kvoff[UNITS_PER_WAVE], vvoff[UNITS_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < UNITS_PER_WAVE; ++i) {
     const int byte = (wave * UNITS_PER_WAVE + i) * 1024 + lane * 16;
     const int row = byte / ROWB, pos = (byte % ROWB) / 16;
-    urow[i] = row;
-    kelt[i] = row * (int)p.sk[2] + swz_k<D>(row, pos) * 8;
-    velt[i] = row * (int)p.sv[2] + swz_v<D>(row, pos) * 8;
+    kvoff[i] = (row * (int)p.sk[2] + swz_k<D>(row, pos) * 8) * 2;
+    vvoff[i] = (row * (int)p.sv[2] + swz_v<D>(row, pos) * 8) * 2;
   }
-  // Start the DMA of key block kb into one stage. Rows past the end of the sequence
-  // (partial last block) are clamped to the last row: their scores are masked to -inf
-  // and their P is exactly 0.
+  // Start the DMA of key block kb into one stage (rows >= S arrive as zeros).
   auto issue = [&](uint8_t* kt, uint8_t* vt, int kb) {
     const int key0 = kb * BS;
-    const uint16_t* kp = kbase + (int64_t)key0 * p.sk[2];
-    const uint16_t* vp = vbase + (int64_t)key0 * p.sv[2];
-    int ke[UNITS_PER_WAVE], ve[UNITS_PER_WAVE];
-    const int last = p.S - 1 - key0;
-#pragma unroll
-    for (int i = 0; i < UNITS_PER_WAVE; ++i) {
-      const int shift = urow[i] > last ? (urow[i] - last) : 0;
-      ke[i] = kelt[i] - shift * (int)p.sk[2];
-      ve[i] = velt[i] - shift * (int)p.sv[2];
-    }
-    dma_tile<D>(kt, kp, ke, wave);
-    dma_tile<D>(vt, vp, ve, wave);
+    const int64_t rows_left = (int64_t)(p.S - key0);
+    dma_tile<D>(kt, tile_rsrc(kbase + (int64_t)key0 * p.sk[2], rows_left * p.sk[2] * 2), kvoff, wave);
+    dma_tile<D>(vt, tile_rsrc(vbase + (int64_t)key0 * p.sv[2], rows_left * p.sv[2] * 2), vvoff, wave);
   };
 
   f32x16_t oacc[DTILES];
