@@ -9,19 +9,22 @@
 // over the tokens < kv_len of the key blocks selected for query head h; a head with no
 // selected block outputs 0.
 //
-// Data path. A workgroup owns (batch b, KV head kvh, split s). It walks the union of the
-// key blocks selected by the G query heads of kvh, takes every P-th entry (P = number of
-// splits) and hands those to its 4 waves round-robin. Each selected KV block is read from
-// HBM exactly once per KV head (16-byte loads), whatever the number of query heads that
-// chose it; every head that chose it is updated from the same registers. Partial
+// Data path. A workgroup owns (batch b, KV head kvh, split s): the contiguous range of
+// key blocks [s*NB/P, (s+1)*NB/P). It reads the mask bytes of its range for the G query
+// heads of kvh in one round trip into LDS, then its 4 waves take the blocks selected by
+// any of those heads round-robin. Each selected KV block is read from HBM once per KV
+// head, however many query heads chose it; all its K and V loads are issued together.
+// QK^T runs on MFMA (v_mfma_f32_32x32x16_bf16; K is loaded straight into the A-operand
+// layout, the G query heads are the N columns), PV on the VALU. Partial
 // (max, sum, output) triples per (b, h, split) go to a caller-provided workspace and a
 // second kernel merges them.
 #include "common.h"
 
 namespace tasft {
 
-constexpr int kDecodeMaxG = 8;  // query heads per KV head handled by one workgroup
+constexpr int kDecodeMaxG = 8;    // query heads per KV head handled by one workgroup
 constexpr int kDecodeWaves = 4;
+constexpr int kDecodeMaxRange = 256;  // key blocks per split (mask bytes staged in LDS)
 
 struct DecodeParams {
   const uint16_t* q;
@@ -37,21 +40,30 @@ struct DecodeParams {
   float scale_log2;
 };
 
+// SUB keys (<= 64) of one KV block are processed at a time; a block of BS keys is
+// BS/SUB sub-blocks.
 template <int BS, int D>
-__global__ void __launch_bounds__(kDecodeWaves * kWave)
+__global__ void __launch_bounds__(kDecodeWaves * kWave, 2)
 bsfa_decode_split_kernel(const DecodeParams p) {
+  constexpr int SUB = BS < 64 ? BS : 64;
+  constexpr int NSUB = BS / SUB;
+  constexpr int KT = SUB / 32;        // 32-key MFMA tiles per sub-block
+  constexpr int KSTEPS = D / 16;      // MFMA k-steps over the head dim
   constexpr int DOCT = D / 8;         // 16-byte chunks per row
   constexpr int KG = kWave / DOCT;    // key groups in the PV phase
-  constexpr int KPL = (BS + kWave - 1) / kWave;  // keys per lane in the QK phase
+  constexpr int VPL = SUB / KG;       // V rows per lane per sub-block
 
-  __shared__ float q_lds[kDecodeMaxG][D];
-  __shared__ float p_lds[kDecodeWaves][BS][kDecodeMaxG];
+  __shared__ uint8_t hb[kDecodeMaxRange];                 // head bits per block of the range
+  __shared__ float p_lds[kDecodeWaves][SUB][kDecodeMaxG]; // probabilities of one sub-block
+  __shared__ float a_lds[kDecodeWaves][kDecodeMaxG];      // rescale factor per head
   __shared__ float comb_ml[kDecodeWaves][kDecodeMaxG][2];
   __shared__ float comb_o[kDecodeWaves][kDecodeMaxG][D];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int col = lane & 31;   // QK layout: query head of this lane
+  const int half = lane >> 5;
   const int G = p.G;
 
   const int64_t item = blockIdx.x;
@@ -63,132 +75,159 @@ bsfa_decode_split_kernel(const DecodeParams p) {
 
   const int kv_len = p.kv_lens ? min(max(p.kv_lens[b], 0), p.S_kv) : p.S_kv;
   const int nb_valid = (kv_len + BS - 1) / BS;
+  const int lo = (int)(((int64_t)s * p.NB) / p.P);
+  const int hi = min((int)(((int64_t)(s + 1) * p.NB) / p.P), nb_valid);
+  const int range = max(hi - lo, 0);
 
-  // Queries of the group, pre-scaled by scale*log2(e), in fp32.
-  for (int i = tid; i < G * D; i += kDecodeWaves * kWave) {
-    const int gg = i / D, d = i % D;
-    const uint16_t qv = p.q[b * p.sq[0] + (int64_t)(h0 + gg) * p.sq[1] + d];
-    q_lds[gg][d] = bf16_bits_to_f32(qv) * p.scale_log2;
+  // Mask bytes of the range for the group's heads, one round trip.
+  const uint8_t* mbase = p.mask + b * p.sm[0] + (int64_t)h0 * p.sm[1];
+  for (int t = tid; t < range; t += kDecodeWaves * kWave) {
+    uint32_t bitsv = 0;
+    for (int gg = 0; gg < G; ++gg)
+      if (mbase[(int64_t)gg * p.sm[1] + (int64_t)(lo + t) * p.sm[2]]) bitsv |= 1u << gg;
+    hb[t] = (uint8_t)bitsv;
+  }
+
+  // Q^T as the MFMA B operand: lane (col, half) holds head h0+col, head dims
+  // ks*16 + half*8 .. +7. Columns >= G are zero.
+  bf16x8_t qf[KSTEPS];
+  {
+    const bool hv = col < G;
+    const uint16_t* qrow = p.q + b * p.sq[0] + (int64_t)(h0 + (hv ? col : 0)) * p.sq[1];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      u32x4_t val = {0u, 0u, 0u, 0u};
+      if (hv) val = *(const u32x4_t*)(qrow + ks * 16 + half * 8);
+      qf[ks] = as_bf16x8(val);
+    }
   }
   __syncthreads();
 
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
   const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
-  const uint8_t* mbase = p.mask + b * p.sm[0] + (int64_t)h0 * p.sm[1];
 
-  float m_run[kDecodeMaxG], l_run[kDecodeMaxG], oacc[kDecodeMaxG][8];
+  // QK-layout state of this lane's head (identical in lanes l and l^32).
+  float m_run = -INFINITY, l_run = 0.f;
+  // PV-layout accumulators: lane (kg, dc) holds head dims dc*8..+7 of every head.
+  const int dc = lane % DOCT;
+  const int kg = lane / DOCT;
+  float oacc[kDecodeMaxG][8];
 #pragma unroll
-  for (int gg = 0; gg < kDecodeMaxG; ++gg) {
-    m_run[gg] = -INFINITY;
-    l_run[gg] = 0.f;
+  for (int gg = 0; gg < kDecodeMaxG; ++gg)
 #pragma unroll
     for (int i = 0; i < 8; ++i) oacc[gg][i] = 0.f;
-  }
 
-  const int dc = lane % DOCT;  // PV phase: head-dim chunk of this lane
-  const int kg = lane / DOCT;  // PV phase: key group of this lane
-  int entry = 0;               // rank of the next union entry (uniform)
-  for (int chunk = 0; chunk < nb_valid; chunk += kWave) {
-    const int kbl = chunk + lane;
-    uint32_t heads = 0;
-    if (kbl < nb_valid) {
-      for (int gg = 0; gg < G; ++gg)
-        if (mbase[(int64_t)gg * p.sm[1] + (int64_t)kbl * p.sm[2]]) heads |= 1u << gg;
-    }
-    uint64_t bits = __ballot(heads != 0);
+  int rank = 0;  // union rank of the next entry in this range (uniform)
+  for (int c0 = 0; c0 < range; c0 += kWave) {
+    const int t = c0 + lane;
+    const uint32_t mybits = t < range ? hb[t] : 0u;
+    uint64_t bits = __ballot(mybits != 0);
     while (bits) {
       const int pos = __builtin_ctzll(bits);
       bits &= bits - 1;
-      const int e = entry++;
-      if (e % p.P != s || (e / p.P) % kDecodeWaves != wave) continue;
-      const int kb = chunk + pos;
-      const uint32_t hsel = __builtin_amdgcn_readlane(heads, pos);
-      const int key0 = kb * BS;
-
-      // QK: lane owns keys key0 + lane + 64*i.
-      float x[KPL][kDecodeMaxG];
+      const int e = rank++;
+      if ((e & (kDecodeWaves - 1)) != wave) continue;
+      const int kb = lo + c0 + pos;
+      const uint32_t hsel = __builtin_amdgcn_readlane(mybits, pos);
+      const bool head_on = col < G && ((hsel >> col) & 1u);
+#pragma unroll 1
+      for (int sb = 0; sb < NSUB; ++sb) {
+        const int key0 = kb * BS + sb * SUB;
+        if (key0 >= kv_len) break;
+        // Issue every K (A-operand layout) and V (PV layout) load of the sub-block.
+        u32x4_t ka[KT][KSTEPS];
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) {
-        const int kk = lane + i * kWave;
-        const int token = key0 + kk;
-        const bool valid = kk < BS && token < kv_len;
-        float acc[kDecodeMaxG];
+        for (int t2 = 0; t2 < KT; ++t2) {
+          const int tok = min(key0 + t2 * 32 + col, kv_len - 1);
+          const uint16_t* krow = kbase + (int64_t)tok * p.sk[2] + half * 8;
 #pragma unroll
-        for (int gg = 0; gg < kDecodeMaxG; ++gg) acc[gg] = 0.f;
-        if (valid) {
-          const uint16_t* krow = kbase + (int64_t)token * p.sk[2];
+          for (int ks = 0; ks < KSTEPS; ++ks) ka[t2][ks] = *(const u32x4_t*)(krow + ks * 16);
+        }
+        u32x4_t va[VPL];
 #pragma unroll
-          for (int c = 0; c < DOCT; ++c) {
-            const u32x4_t kv = *(const u32x4_t*)(krow + c * 8);
-            float kf[8];
-            unpack_bf16x8(kv, kf);
+        for (int i = 0; i < VPL; ++i) {
+          const int tok = min(key0 + kg + KG * i, kv_len - 1);
+          va[i] = *(const u32x4_t*)(vbase + (int64_t)tok * p.sv[2] + dc * 8);
+        }
+        // S^T = K Q^T: rows = keys, cols = heads.
+        f32x16_t sacc[KT];
 #pragma unroll
-            for (int gg = 0; gg < kDecodeMaxG; ++gg) {
-              if (gg < G) {
+        for (int t2 = 0; t2 < KT; ++t2) {
+          sacc[t2] = (f32x16_t){};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[gg] = fmaf(kf[j], q_lds[gg][c * 8 + j], acc[gg]);
-              }
-            }
+          for (int ks = 0; ks < KSTEPS; ++ks)
+            sacc[t2] = mfma_32x32x16_bf16(as_bf16x8(ka[t2][ks]), qf[ks], sacc[t2]);
+        }
+        // Register r of tile t2 holds key t2*32 + 8*(r/4) + 4*half + r%4 of head `col`.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t2 = 0; t2 < KT; ++t2) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = key0 + t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const float x = (head_on && key < kv_len) ? sacc[t2][r] * p.scale_log2 : -INFINITY;
+            sacc[t2][r] = x;
+            mx = fmaxf(mx, x);
           }
         }
-#pragma unroll
-        for (int gg = 0; gg < kDecodeMaxG; ++gg)
-          x[i][gg] = (valid && ((hsel >> gg) & 1u)) ? acc[gg] : -INFINITY;
-      }
-
-      float alpha[kDecodeMaxG];
-#pragma unroll
-      for (int gg = 0; gg < kDecodeMaxG; ++gg) {
-        if (gg >= G) { alpha[gg] = 1.f; continue; }
-        float bm = x[0][gg];
-#pragma unroll
-        for (int i = 1; i < KPL; ++i) bm = fmaxf(bm, x[i][gg]);
-        bm = wave_max(bm);
-        const float m_new = fmaxf(m_run[gg], bm);
+        mx = pair_max32(mx);
+        const float m_new = fmaxf(m_run, mx);
         const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        alpha[gg] = __builtin_amdgcn_exp2f(m_run[gg] - m_use);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
         float ls = 0.f;
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(x[i][gg] - m_use);
-          ls += pv;
-          const int kk = lane + i * kWave;
-          if (kk < BS) p_lds[wave][kk][gg] = pv;
+        for (int t2 = 0; t2 < KT; ++t2) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float e2 = __builtin_amdgcn_exp2f(sacc[t2][r] - m_use);
+            ls += e2;
+            if (col < G) p_lds[wave][t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)][col] = e2;
+          }
         }
-        l_run[gg] = l_run[gg] * alpha[gg] + ls;
-        m_run[gg] = m_new;
-      }
-      // p_lds is private to this wave: a wave-level barrier orders its writes and reads.
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-      // PV: lane owns head dims dc*8..+7 for keys kg, kg+KG, ...
-#pragma unroll
-      for (int gg = 0; gg < kDecodeMaxG; ++gg)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) oacc[gg][i] *= alpha[gg];
-      const int kmax = min(BS, kv_len - key0);
-      for (int kk = kg; kk < kmax; kk += KG) {
-        const u32x4_t vv = *(const u32x4_t*)(vbase + (int64_t)(key0 + kk) * p.sv[2] + dc * 8);
-        float vf[8];
-        unpack_bf16x8(vv, vf);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+        if (half == 0 && col < G) a_lds[wave][col] = alpha;
+        // p_lds / a_lds are private to this wave: a wave barrier orders writes and reads.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // PV: oacc[g] = alpha_g * oacc[g] + sum_key p[key][g] * V[key][dc*8..+7].
 #pragma unroll
         for (int gg = 0; gg < kDecodeMaxG; ++gg) {
           if (gg < G) {
-            const float pw = p_lds[wave][kk][gg];
+            const float a = a_lds[wave][gg];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pw, vf[j], oacc[gg][j]);
+            for (int j = 0; j < 8; ++j) oacc[gg][j] *= a;
           }
         }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+          const int kk = kg + KG * i;
+          float vf[8];
+          unpack_bf16x8(va[i], vf);
+#pragma unroll
+          for (int gg = 0; gg < kDecodeMaxG; ++gg) {
+            if (gg < G) {
+              const float pw = p_lds[wave][kk][gg];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pw, vf[j], oacc[gg][j]);
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 
-  // Reduce each wave's PV partials over its key groups, then merge the 4 waves.
+  // Per wave: reduce the PV partials over key groups and the denominators over the lane
+  // pair, then merge the 4 waves.
+  const float l_tot = pair_sum32(l_run);
+  if (half == 0 && col < G) {
+    comb_ml[wave][col][0] = m_run;
+    comb_ml[wave][col][1] = l_tot;
+  }
 #pragma unroll
   for (int gg = 0; gg < kDecodeMaxG; ++gg) {
     if (gg >= G) continue;
@@ -196,14 +235,9 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     for (int off = DOCT; off < kWave; off <<= 1)
 #pragma unroll
       for (int j = 0; j < 8; ++j) oacc[gg][j] += __shfl_xor(oacc[gg][j], off, 64);
-    const float lt = wave_sum(l_run[gg]);
     if (lane < DOCT) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) comb_o[wave][gg][lane * 8 + j] = oacc[gg][j];
-    }
-    if (lane == 0) {
-      comb_ml[wave][gg][0] = m_run[gg];
-      comb_ml[wave][gg][1] = lt;
     }
   }
   __syncthreads();
@@ -300,6 +334,11 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
   if (block_size != 32 && block_size != 64 && block_size != 128)
     return set_error(kErrUnsupported, "decode: block_size must be 32, 64 or 128, got %lld",
                      (long long)block_size);
+  const int64_t nb = (kv_len_max + block_size - 1) / block_size;
+  if ((nb + num_splits - 1) / num_splits > kDecodeMaxRange)
+    return set_error(kErrInvalidArgument,
+                     "decode: num_splits must be >= ceil(num_blocks / %d) (got %lld for %lld blocks)",
+                     kDecodeMaxRange, (long long)num_splits, (long long)nb);
   const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
   if (workspace_bytes < need)
     return set_error(kErrWorkspace, "decode: workspace too small: need %zu bytes, got %zu", need,
@@ -309,9 +348,11 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
   for (int j = 0; j < 3; ++j)
     if (k_strides[j] % 8 != 0 || v_strides[j] % 8 != 0)
       return set_error(kErrInvalidArgument, "decode: K/V strides must be multiples of 8 elements");
-  if ((((uintptr_t)k_cache) & 15u) || (((uintptr_t)v_cache) & 15u) || (((uintptr_t)workspace) & 15u))
-    return set_error(kErrInvalidArgument, "decode: K/V cache and workspace must be 16-byte aligned");
-  const int64_t nb = (kv_len_max + block_size - 1) / block_size;
+  if (q_strides[0] % 8 != 0 || q_strides[1] % 8 != 0)
+    return set_error(kErrInvalidArgument, "decode: q strides must be multiples of 8 elements");
+  if ((((uintptr_t)q) & 15u) || (((uintptr_t)k_cache) & 15u) || (((uintptr_t)v_cache) & 15u) ||
+      (((uintptr_t)workspace) & 15u))
+    return set_error(kErrInvalidArgument, "decode: q, K/V cache and workspace must be 16-byte aligned");
   if (batch * num_kv_heads * num_splits > 0x7fffffffLL || kv_len_max > 0x3fffffffLL)
     return set_error(kErrUnsupported, "decode: problem too large for one launch");
 
