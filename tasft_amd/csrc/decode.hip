@@ -40,9 +40,25 @@ struct DecodeParams {
   float scale_log2;
 };
 
+// Raw buffer resource (stride 0) over `bytes` bytes starting at `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t decode_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
+}
+
+// One 16-byte-per-lane DMA (buffer_load ... lds) of 1 KB into LDS at `dst`.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TASFT_LDS void*)dst, 16, voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 // SUB keys (<= 64) of one KV block are processed at a time; a block of BS keys is
-// BS/SUB sub-blocks.
-template <int BS, int D>
+// BS/SUB sub-blocks. MG >= G is the head count the loops are unrolled for (padding heads
+// carry zero probability).
+template <int BS, int D, int MG>
 __global__ void __launch_bounds__(kDecodeWaves * kWave, 2)
 bsfa_decode_split_kernel(const DecodeParams p) {
   constexpr int SUB = BS < 64 ? BS : 64;
@@ -53,11 +69,12 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   constexpr int KG = kWave / DOCT;    // key groups in the PV phase
   constexpr int VPL = SUB / KG;       // V rows per lane per sub-block
 
-  __shared__ uint8_t hb[kDecodeMaxRange];                 // head bits per block of the range
-  __shared__ float p_lds[kDecodeWaves][SUB][kDecodeMaxG]; // probabilities of one sub-block
-  __shared__ float a_lds[kDecodeWaves][kDecodeMaxG];      // rescale factor per head
-  __shared__ float comb_ml[kDecodeWaves][kDecodeMaxG][2];
-  __shared__ float comb_o[kDecodeWaves][kDecodeMaxG][D];
+  constexpr int VTILE = SUB * D * 2;  // bytes of one sub-block of V
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kDecodeWaves][VTILE];  // per-wave V tile
+  __shared__ uint8_t hb[kDecodeMaxRange];                     // head bits per block of the range
+  __shared__ float p_lds[kDecodeWaves][SUB * MG + kWave];     // probabilities (+ dummy slots)
+  __shared__ float a_lds[kDecodeWaves][MG];                   // rescale factor per head
+  __shared__ float comb_ml[kDecodeWaves][MG][2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,8 +100,9 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   const uint8_t* mbase = p.mask + b * p.sm[0] + (int64_t)h0 * p.sm[1];
   for (int t = tid; t < range; t += kDecodeWaves * kWave) {
     uint32_t bitsv = 0;
-    for (int gg = 0; gg < G; ++gg)
-      if (mbase[(int64_t)gg * p.sm[1] + (int64_t)(lo + t) * p.sm[2]]) bitsv |= 1u << gg;
+#pragma unroll
+    for (int gg = 0; gg < MG; ++gg)
+      if (gg < G && mbase[(int64_t)gg * p.sm[1] + (int64_t)(lo + t) * p.sm[2]]) bitsv |= 1u << gg;
     hb[t] = (uint8_t)bitsv;
   }
 
@@ -105,17 +123,29 @@ bsfa_decode_split_kernel(const DecodeParams p) {
 
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
   const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
+  const int ks2 = (int)p.sk[2], vs2 = (int)p.sv[2];  // row strides (elements)
 
   // QK-layout state of this lane's head (identical in lanes l and l^32).
   float m_run = -INFINITY, l_run = 0.f;
   // PV-layout accumulators: lane (kg, dc) holds head dims dc*8..+7 of every head.
   const int dc = lane % DOCT;
   const int kg = lane / DOCT;
-  float oacc[kDecodeMaxG][8];
+  float oacc[MG][8];
 #pragma unroll
-  for (int gg = 0; gg < kDecodeMaxG; ++gg)
+  for (int gg = 0; gg < MG; ++gg)
 #pragma unroll
     for (int i = 0; i < 8; ++i) oacc[gg][i] = 0.f;
+  // Per-lane byte offsets inside a sub-block: K row `col` (A-operand layout); for the V
+  // DMA, lane l of unit u fetches byte u*1024 + 16*l of the row-major tile.
+  const int k_voff = (col * ks2 + half * 8) * 2;
+  int v_dma_off[VTILE / 1024];
+#pragma unroll
+  for (int u = 0; u < VTILE / 1024; ++u) {
+    const int byte = u * 1024 + lane * 16;
+    v_dma_off[u] = (byte / (D * 2)) * vs2 * 2 + byte % (D * 2);
+  }
+  // Where this lane's probabilities go in p_lds (lanes of padding heads: a dummy slot).
+  const bool pcol = col < MG;
 
   int rank = 0;  // union rank of the next entry in this range (uniform)
   for (int c0 = 0; c0 < range; c0 += kWave) {
@@ -135,19 +165,32 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         const int key0 = kb * BS + sb * SUB;
         if (key0 >= kv_len) break;
         // Issue every K (A-operand layout) and V (PV layout) load of the sub-block.
+        const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)SUB * ks2 * 2);
+        // V: DMA into this wave's LDS tile. The resource ends at row kv_len-1, so rows
+        // past kv_len (possibly never written) arrive as zeros.
+        const __amdgpu_buffer_rsrc_t vr =
+            decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(SUB, kv_len - key0) * vs2 * 2);
+#pragma unroll
+        for (int u = 0; u < VTILE / 1024; ++u)
+          dma16(vr, v_lds[wave] + u * 1024, v_dma_off[u]);
         u32x4_t ka[KT][KSTEPS];
+        if (key0 + SUB <= kv_len) {
 #pragma unroll
-        for (int t2 = 0; t2 < KT; ++t2) {
-          const int tok = min(key0 + t2 * 32 + col, kv_len - 1);
-          const uint16_t* krow = kbase + (int64_t)tok * p.sk[2] + half * 8;
+          for (int t2 = 0; t2 < KT; ++t2)
 #pragma unroll
-          for (int ks = 0; ks < KSTEPS; ++ks) ka[t2][ks] = *(const u32x4_t*)(krow + ks * 16);
-        }
-        u32x4_t va[VPL];
+            for (int ks = 0; ks < KSTEPS; ++ks)
+              ka[t2][ks] = buf_load16(kr, k_voff + ks * 32, t2 * 32 * ks2 * 2);
+        } else {
+          // Partial last sub-block: K rows past kv_len are replaced by row kv_len-1; their
+          // scores are masked to -inf.
+          const int last = kv_len - 1 - key0;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-          const int tok = min(key0 + kg + KG * i, kv_len - 1);
-          va[i] = *(const u32x4_t*)(vbase + (int64_t)tok * p.sv[2] + dc * 8);
+          for (int t2 = 0; t2 < KT; ++t2) {
+            const int row = min(t2 * 32 + col, last);
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks)
+              ka[t2][ks] = buf_load16(kr, (row * ks2 + half * 8) * 2 + ks * 32, 0);
+          }
         }
         // S^T = K Q^T: rows = keys, cols = heads.
         f32x16_t sacc[KT];
@@ -175,43 +218,43 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
         float ls = 0.f;
+        float* pw = p_lds[wave];
 #pragma unroll
         for (int t2 = 0; t2 < KT; ++t2) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const float e2 = __builtin_amdgcn_exp2f(sacc[t2][r] - m_use);
             ls += e2;
-            if (col < G) p_lds[wave][t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)][col] = e2;
+            const int key = t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            pw[pcol ? key * MG + col : SUB * MG + lane] = e2;
           }
         }
         l_run = l_run * alpha + ls;
         m_run = m_new;
-        if (half == 0 && col < G) a_lds[wave][col] = alpha;
-        // p_lds / a_lds are private to this wave: a wave barrier orders writes and reads.
+        if (half == 0 && col < MG) a_lds[wave][col] = alpha;
+        // p_lds / a_lds / v_lds are private to this wave: wait for the V DMA, then a wave
+        // barrier orders the LDS writes and reads.
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // PV: oacc[g] = alpha_g * oacc[g] + sum_key p[key][g] * V[key][dc*8..+7].
 #pragma unroll
-        for (int gg = 0; gg < kDecodeMaxG; ++gg) {
-          if (gg < G) {
-            const float a = a_lds[wave][gg];
+        for (int gg = 0; gg < MG; ++gg) {
+          const float a = a_lds[wave][gg];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) oacc[gg][j] *= a;
-          }
+          for (int j = 0; j < 8; ++j) oacc[gg][j] *= a;
         }
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
           const int kk = kg + KG * i;
           float vf[8];
-          unpack_bf16x8(va[i], vf);
+          unpack_bf16x8(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
 #pragma unroll
-          for (int gg = 0; gg < kDecodeMaxG; ++gg) {
-            if (gg < G) {
-              const float pw = p_lds[wave][kk][gg];
+          for (int gg = 0; gg < MG; ++gg) {
+            const float pv = pw[kk * MG + gg];
 #pragma unroll
-              for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pw, vf[j], oacc[gg][j]);
-            }
+            for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pv, vf[j], oacc[gg][j]);
           }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -222,22 +265,23 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   }
 
   // Per wave: reduce the PV partials over key groups and the denominators over the lane
-  // pair, then merge the 4 waves.
+  // pair, then merge the 4 waves. Each wave's partial output goes to its own V tile.
+  static_assert(MG * D * 4 <= VTILE, "merge buffer size");
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // no V DMA may still target the tile
   const float l_tot = pair_sum32(l_run);
-  if (half == 0 && col < G) {
+  if (half == 0 && col < MG) {
     comb_ml[wave][col][0] = m_run;
     comb_ml[wave][col][1] = l_tot;
   }
 #pragma unroll
-  for (int gg = 0; gg < kDecodeMaxG; ++gg) {
-    if (gg >= G) continue;
+  for (int gg = 0; gg < MG; ++gg) {
 #pragma unroll
     for (int off = DOCT; off < kWave; off <<= 1)
 #pragma unroll
       for (int j = 0; j < 8; ++j) oacc[gg][j] += __shfl_xor(oacc[gg][j], off, 64);
     if (lane < DOCT) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) comb_o[wave][gg][lane * 8 + j] = oacc[gg][j];
+      for (int j = 0; j < 8; ++j) ((float*)v_lds[wave])[gg * D + lane * 8 + j] = oacc[gg][j];
     }
   }
   __syncthreads();
@@ -252,7 +296,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     for (int w = 0; w < kDecodeWaves; ++w) {
       const float f = __builtin_amdgcn_exp2f(comb_ml[w][gg][0] - Mu);
       L += comb_ml[w][gg][1] * f;
-      O += comb_o[w][gg][d] * f;
+      O += ((const float*)v_lds[w])[gg * D + d] * f;
     }
     const int64_t row = ((int64_t)b * p.Hq + h0 + gg) * p.P + s;
     p.ws_o[row * D + d] = O;
@@ -287,16 +331,24 @@ bsfa_decode_combine_kernel(const DecodeParams p) {
   p.o[b * p.so[0] + h * p.so[1] + d] = __builtin_bit_cast(uint16_t, rb);
 }
 
-template <int BS, int D>
-static hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+template <int BS, int D, int MG>
+static hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.B * p.Hkv * p.P;
-  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG>), dim3((unsigned)grid),
                      dim3(kDecodeWaves * kWave), 0, stream, p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((bsfa_decode_combine_kernel<D>), dim3((unsigned)((int64_t)p.B * p.Hq)), dim3(D),
                      0, stream, p);
   return hipGetLastError();
+}
+
+template <int BS, int D>
+static hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+  if (p.G <= 1) return launch_decode_g<BS, D, 1>(p, stream);
+  if (p.G <= 2) return launch_decode_g<BS, D, 2>(p, stream);
+  if (p.G <= 4) return launch_decode_g<BS, D, 4>(p, stream);
+  return launch_decode_g<BS, D, 8>(p, stream);
 }
 
 }  // namespace tasft
