@@ -10,20 +10,22 @@
 // this computes u_i = W_q qbar_i + b_in once per query block and v_j = W_k kbar_j once
 // per key block, so each pair costs hidden x (add, max, fma) instead of a 2D-wide GEMV.
 //
-// Kernel 1 (pool + project) streams Q and K from HBM exactly once (GQA-native: K is
-// pooled per KV head, never expanded). Kernel 2 (pairwise) evaluates the MLP for the
-// causal pairs in fp32, applies sigmoid, the causal zero and the per-head threshold, and
-// writes soft scores (fp32), optional logits, the uint8 hard mask and the active count.
-// Flag bit 1 forces the diagonal blocks on in the hard mask (soft scores unchanged).
+// Pooling streams Q and K from HBM exactly once (GQA-native: K is pooled per KV head,
+// never expanded); for block size 64 and D in {64, 128} it is a pure streaming kernel
+// followed by an LDS-tiled fp32 projection GEMM, otherwise one fused pool + project
+// kernel. The pairwise kernel evaluates the MLP for the causal pairs in fp32, applies
+// sigmoid, the causal zero and the per-head threshold, and writes soft scores (fp32),
+// optional logits, the uint8 hard mask and the active count. Flag bit 1 forces the
+// diagonal blocks on in the hard mask (soft scores unchanged).
+#include <algorithm>
+
 #include "common.h"
 
 namespace tasft {
 
 constexpr int kPoolBlocks = 8;    // blocks pooled per workgroup (amortises the W_in read)
 constexpr int kGateMaxD = 256;
-constexpr int kPairRows = 32;     // query-block rows per pairwise workgroup
-constexpr int kPairCols = 64;     // key-block columns per inner tile
-constexpr int kPairHid = 64;      // hidden units staged per LDS round
+constexpr int kPairHid = 128;     // hidden units staged per LDS round (pairwise)
 
 struct GatePoolParams {
   const uint16_t* q;
@@ -32,6 +34,8 @@ struct GatePoolParams {
   const float* b_in;  // [hidden]
   float* uq;          // [B, Hq, NB, hidden]
   float* uk;          // [B, Hkv, NB, hidden]
+  float* pq;          // [B, Hq, NB, D] block means (fast path)
+  float* pk;          // [B, Hkv, NB, D]
   unsigned long long* counter;
   int64_t sq[3], sk[3];
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
@@ -108,6 +112,178 @@ gate_pool_project_kernel(const GatePoolParams p) {
   }
 }
 
+
+// Fast path for block size 64 and D in {64, 128}: pooling and projection are two
+// kernels. gate_pool64_kernel is a pure stream: a workgroup pools kFastPB blocks of one
+// (batch, head), issuing every row load of all its blocks up front through a buffer
+// resource that ends at row S-1, so rows of a partial last block arrive as zeros, which
+// is exactly the reference's zero padding (the mean still divides by the block size).
+// The means go to an fp32 [rows, D] buffer that gate_project_kernel multiplies by the
+// W_in halves as an LDS-tiled fp32 GEMM (coalesced W_in reads, 16 outputs per thread).
+constexpr int kFastPB = 4;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
+}
+
+template <int D>
+__global__ void __launch_bounds__(256)
+gate_pool64_kernel(const GatePoolParams p) {
+  constexpr int BSZ = 64;
+  constexpr int DOCT = D / 8;        // 16-byte chunks per row
+  constexpr int RG = 256 / DOCT;     // row groups in the workgroup
+  constexpr int RPT = BSZ / RG;      // rows per thread per block
+  constexpr int WRG = kWave / DOCT;  // row groups per wave
+  static_assert(WRG == 4 || WRG == 8, "row groups per wave");
+  __shared__ float red[4][kFastPB][D];
+
+  const int tid = threadIdx.x;
+  if (blockIdx.x == 0 && tid == 0 && p.counter) *p.counter = 0ull;
+  const int chunks = (p.NB + kFastPB - 1) / kFastPB;
+  const int64_t nq = (int64_t)p.B * p.Hq * chunks;
+  const bool is_q = blockIdx.x < nq;
+  const int64_t local = is_q ? blockIdx.x : blockIdx.x - nq;
+  const int heads = is_q ? p.Hq : p.Hkv;
+  const int64_t bh = local / chunks;
+  const int chunk = (int)(local % chunks);
+  const int b = (int)(bh / heads);
+  const int h = (int)(bh % heads);
+  const uint16_t* src = is_q ? p.q + b * p.sq[0] + h * p.sq[1] : p.k + b * p.sk[0] + h * p.sk[1];
+  const int srow = (int)(is_q ? p.sq[2] : p.sk[2]);
+  const int blk0 = chunk * kFastPB;
+  const int row0 = blk0 * BSZ;
+  const __amdgpu_buffer_rsrc_t r =
+      gate_rsrc(src + (int64_t)row0 * srow, (int64_t)(p.S - row0) * srow * 2);
+
+  const int dc = tid % DOCT, rg = tid / DOCT;
+  u32x4_t v[kFastPB][RPT];
+#pragma unroll
+  for (int bi = 0; bi < kFastPB; ++bi)
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int row = bi * BSZ + rg + RG * i;
+      v[bi][i] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (row * srow + dc * 8) * 2, 0, 0));
+    }
+  const int wave = tid / kWave;
+#pragma unroll
+  for (int bi = 0; bi < kFastPB; ++bi) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      float f[8];
+      unpack_bf16x8(v[bi][i], f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += f[j];
+    }
+    // Lanes l, l + DOCT, ... of a wave hold the same columns of different rows.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float x = pair_sum32(acc[j]);
+      x += __shfl_xor(x, 16, 64);
+      if (WRG == 8) x += __shfl_xor(x, 8, 64);
+      acc[j] = x;
+    }
+    if ((tid % kWave) < DOCT) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[wave][bi][dc * 8 + j] = acc[j];
+    }
+  }
+  __syncthreads();
+  const int nblk = min(kFastPB, p.NB - blk0);
+  float* dst = (is_q ? p.pq : p.pk) + (bh * p.NB + blk0) * (int64_t)D;
+  const float inv_bs = 1.f / (float)BSZ;
+  for (int e = tid; e < nblk * D; e += 256) {
+    const int bi = e / D, d = e % D;
+    dst[e] = ((red[0][bi][d] + red[1][bi][d]) + (red[2][bi][d] + red[3][bi][d])) * inv_bs;
+  }
+}
+
+// u[row][c] = sum_d pooled[row][d] * W_in[c][off + d] (+ b_in[c] for query rows).
+// Workgroup: 64 rows x 64 hidden units, d staged 32 at a time (transposed in LDS);
+// thread (tr, tc) accumulates rows 4tr..4tr+3 x units 4tc..4tc+3.
+constexpr int kProjTile = 64;
+constexpr int kProjK = 32;
+constexpr int kProjLd = kProjTile + 4;
+
+__global__ void __launch_bounds__(256)
+gate_project_kernel(const GatePoolParams p) {
+  __shared__ __attribute__((aligned(16))) float a_t[kProjK][kProjLd];
+  __shared__ __attribute__((aligned(16))) float w_t[kProjK][kProjLd];
+  const int tid = threadIdx.x;
+  const int tr = tid / 16, tc = tid % 16;
+  const int64_t rq = (int64_t)p.B * p.Hq * p.NB, rk = (int64_t)p.B * p.Hkv * p.NB;
+  const int64_t qtiles = (rq + kProjTile - 1) / kProjTile;
+  const int col_tiles = (p.hidden + kProjTile - 1) / kProjTile;
+  const int64_t rt = blockIdx.x / col_tiles;
+  const int c0 = (int)(blockIdx.x % col_tiles) * kProjTile;
+  const bool is_q = rt < qtiles;
+  const int64_t r0 = (is_q ? rt : rt - qtiles) * kProjTile;
+  const int64_t rows = is_q ? rq : rk;
+  const float* src = is_q ? p.pq : p.pk;
+  float* dst = is_q ? p.uq : p.uk;
+  const int off = is_q ? 0 : p.D;
+
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+
+  // Staging: thread t loads 8 consecutive d of row / unit t / 4; the loads of the next
+  // d chunk are in flight while the current one is multiplied.
+  const int sr = tid / 4, sd = (tid % 4) * 8;
+  const int64_t arow = r0 + sr;
+  const int wc = c0 + sr;
+  const float* asrc = src + arow * p.D + sd;
+  const float* wsrc = p.w_in + (int64_t)wc * 2 * p.D + off + sd;
+  f32x4_t xa0 = {}, xa1 = {}, xw0 = {}, xw1 = {};
+  auto load = [&](int d0) {
+    if (arow < rows) {
+      xa0 = *(const f32x4_t*)(asrc + d0);
+      xa1 = *(const f32x4_t*)(asrc + d0 + 4);
+    }
+    if (wc < p.hidden) {
+      xw0 = *(const f32x4_t*)(wsrc + d0);
+      xw1 = *(const f32x4_t*)(wsrc + d0 + 4);
+    }
+  };
+  load(0);
+  for (int d0 = 0; d0 < p.D; d0 += kProjK) {
+    if (d0 > 0) __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a_t[sd + j][sr] = xa0[j];
+      a_t[sd + 4 + j][sr] = xa1[j];
+      w_t[sd + j][sr] = xw0[j];
+      w_t[sd + 4 + j][sr] = xw1[j];
+    }
+    __syncthreads();
+    if (d0 + kProjK < p.D) load(d0 + kProjK);
+#pragma unroll 8
+    for (int d = 0; d < kProjK; ++d) {
+      const f32x4_t av = *(const f32x4_t*)&a_t[d][4 * tr];
+      const f32x4_t wv = *(const f32x4_t*)&w_t[d][4 * tc];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], wv[j], acc[i][j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = c0 + 4 * tc + j;
+    if (c >= p.hidden) continue;
+    const float bias = is_q ? p.b_in[c] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = r0 + 4 * tr + i;
+      if (row < rows) dst[row * p.hidden + c] = acc[i][j] + bias;
+    }
+  }
+}
+
 struct GatePairParams {
   const float* uq;
   const float* uk;
@@ -117,87 +293,140 @@ struct GatePairParams {
   float* logits;       // [B, Hq, NB, NB] or null
   uint8_t* mask;       // [B, Hq, NB, NB]
   unsigned long long* counter;
-  int B, Hq, Hkv, G, NB, hidden, causal, force_diag, row_tiles;
+  int B, Hq, Hkv, G, NB, hidden, causal, force_diag, tiles;
 };
+
+// Pairwise MLP: a workgroup evaluates a kPairTile x kPairTile tile of (query block,
+// key block) pairs of one (batch, head). The hidden units are staged kPairHid at a time
+// (transposed) and split over the four waves, 32 each; lane (tr, tc) of a wave
+// accumulates the 4 x 4 pairs rows 4tr.., cols 4tc.. (three LDS reads per 16 pairs and
+// hidden unit). The four partial sums meet in LDS; the epilogue applies sigmoid, the
+// causal zero and the threshold with coalesced stores.
+constexpr int kPairTile = 32;
+constexpr int kPairLd = kPairTile + 4;
 
 __global__ void __launch_bounds__(256)
 gate_pairwise_kernel(const GatePairParams p) {
-  __shared__ __attribute__((aligned(16))) float uq_t[kPairHid][kPairRows + 1];
-  __shared__ __attribute__((aligned(16))) float uk_t[kPairHid][kPairCols + 4];
+  // [kPairHid][kPairLd] query units | [kPairHid][kPairLd] key units; afterwards the four
+  // partial-sum tiles [4][kPairTile][kPairLd] (the same size).
+  __shared__ __attribute__((aligned(16))) float lds[2 * kPairHid * kPairLd];
   __shared__ float wo[kPairHid];
+  static_assert(2 * kPairHid >= 4 * kPairTile, "partial sums alias the staging tiles");
+  __shared__ unsigned int wave_count[4];
+  float* uq_t = lds;
+  float* uk_t = lds + kPairHid * kPairLd;
 
   const int tid = threadIdx.x;
-  const int tr = tid / 16;  // rows 2*tr, 2*tr+1
-  const int tc = tid % 16;  // cols 4*tc .. 4*tc+3
-  const int64_t bh = blockIdx.x / p.row_tiles;
-  const int i0 = (int)(blockIdx.x % p.row_tiles) * kPairRows;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int tr = lane / 8, tc = lane % 8;
+  const int per_head = p.tiles * p.tiles;
+  const int64_t bh = blockIdx.x / per_head;
+  const int t2 = (int)(blockIdx.x % per_head);
+  const int i0 = (t2 / p.tiles) * kPairTile;
+  const int j0 = (t2 % p.tiles) * kPairTile;
   const int b = (int)(bh / p.Hq);
   const int h = (int)(bh % p.Hq);
   const int kvh = h / p.G;
-  const float tau = p.tau[h];
   const float* uq = p.uq + (bh * p.NB) * (int64_t)p.hidden;
   const float* uk = p.uk + (((int64_t)b * p.Hkv + kvh) * p.NB) * (int64_t)p.hidden;
-  const int64_t obase = bh * (int64_t)p.NB * p.NB;
-  const int i_last = min(i0 + kPairRows, p.NB) - 1;
-  // With causal=1 and no logits requested, pairs above the diagonal are never evaluated.
-  const bool skip_upper = p.causal && p.logits == nullptr;
+  // With causal=1 and no logits requested, a tile wholly above the diagonal is never
+  // evaluated (its soft scores are exactly zero).
+  const bool skip = p.causal && p.logits == nullptr && j0 > i0 + kPairTile - 1;
 
-  unsigned int active = 0;
-  for (int j0 = 0; j0 < p.NB; j0 += kPairCols) {
-    float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    const bool compute = !(skip_upper && j0 > i_last);
-    if (compute) {
-      for (int c0 = 0; c0 < p.hidden; c0 += kPairHid) {
-        const int hc = min(kPairHid, p.hidden - c0);
-        __syncthreads();
-        for (int e = tid; e < kPairRows * kPairHid; e += 256) {
-          const int r = e / kPairHid, cc = e % kPairHid;
-          const int i = i0 + r;
-          uq_t[cc][r] = (cc < hc && i < p.NB) ? uq[(int64_t)i * p.hidden + c0 + cc] : 0.f;
-        }
-        for (int e = tid; e < kPairCols * kPairHid; e += 256) {
-          const int r = e / kPairHid, cc = e % kPairHid;
-          const int j = j0 + r;
-          uk_t[cc][r] = (cc < hc && j < p.NB) ? uk[(int64_t)j * p.hidden + c0 + cc] : 0.f;
-        }
-        if (tid < kPairHid) wo[tid] = tid < hc ? p.w_out[c0 + tid] : 0.f;
-        __syncthreads();
-        for (int cc = 0; cc < hc; ++cc) {
-          const float a0 = uq_t[cc][2 * tr];
-          const float a1 = uq_t[cc][2 * tr + 1];
-          const f32x4_t bv = *(const f32x4_t*)&uk_t[cc][4 * tc];
-          const float w = wo[cc];
+  if (!skip) {
+    float acc[4][4];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            acc[0][c] = fmaf(w, fmaxf(a0 + bv[c], 0.f), acc[0][c]);
-            acc[1][c] = fmaf(w, fmaxf(a1 + bv[c], 0.f), acc[1][c]);
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
+    constexpr int SU = kPairHid / 8;              // units staged per thread
+    const int sr = tid / 8, su = (tid % 8) * SU;  // staging: row sr, units su..su+SU-1
+    const bool vec = (p.hidden % 4) == 0;         // rows start 16-byte aligned
+    for (int c0 = 0; c0 < p.hidden; c0 += kPairHid) {
+      const int hc = min(kPairHid, p.hidden - c0);
+      if (c0 > 0) __syncthreads();
+      const int i = i0 + sr, j = j0 + sr;
+      const float* qrow = uq + (int64_t)i * p.hidden + c0;
+      const float* krow = uk + (int64_t)j * p.hidden + c0;
+      if (vec && su + SU <= hc) {
+        // Whole run in range: 16-byte loads (hc is a multiple of 4 here).
+#pragma unroll
+        for (int u = 0; u < SU; u += 4) {
+          const f32x4_t a = i < p.NB ? *(const f32x4_t*)(qrow + su + u) : (f32x4_t){};
+          const f32x4_t c = j < p.NB ? *(const f32x4_t*)(krow + su + u) : (f32x4_t){};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uq_t[(su + u + e) * kPairLd + sr] = a[e];
+            uk_t[(su + u + e) * kPairLd + sr] = c[e];
           }
         }
+      } else {
+#pragma unroll
+        for (int u = 0; u < SU; ++u) {
+          const int cc = su + u;
+          uq_t[cc * kPairLd + sr] = (cc < hc && i < p.NB) ? qrow[cc] : 0.f;
+          uk_t[cc * kPairLd + sr] = (cc < hc && j < p.NB) ? krow[cc] : 0.f;
+        }
+      }
+      if (tid < kPairHid) wo[tid] = tid < hc ? p.w_out[c0 + tid] : 0.f;
+      __syncthreads();
+      // Wave w takes units w, w+4, ...; units past hc (up to the next multiple of 4)
+      // are zero in every operand and contribute nothing.
+      const int nu = (hc + 3) / 4;
+#pragma unroll 8
+      for (int u = 0; u < nu; ++u) {
+        const int cc = 4 * u + wave;
+        const f32x4_t av = *(const f32x4_t*)&uq_t[cc * kPairLd + 4 * tr];
+        const f32x4_t bv = *(const f32x4_t*)&uk_t[cc * kPairLd + 4 * tc];
+        const float w = wo[cc];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(w, fmaxf(av[r] + bv[c], 0.f), acc[r][c]);
       }
     }
+    __syncthreads();
+    float* part = lds + wave * (kPairTile * kPairLd);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int i = i0 + 2 * tr + r;
-      if (i >= p.NB) continue;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int j = j0 + 4 * tc + c;
-        if (j >= p.NB) continue;
-        const float logit = acc[r][c];
-        float soft = 1.f / (1.f + expf(-logit));
-        if (p.causal && j > i) soft = 0.f;
-        const bool on = soft >= tau || (p.force_diag && i == j);
-        active += on ? 1u : 0u;
-        const int64_t o = obase + (int64_t)i * p.NB + j;
-        p.soft[o] = soft;
-        p.mask[o] = on ? 1 : 0;
-        if (p.logits) p.logits[o] = logit;
-      }
-    }
+    for (int r = 0; r < 4; ++r)
+      *(f32x4_t*)&part[(4 * tr + r) * kPairLd + 4 * tc] =
+          (f32x4_t){acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
+    __syncthreads();
   }
-  // One atomic per wave.
+
+  const float tau = p.tau[h];
+  const int64_t obase = bh * (int64_t)p.NB * p.NB;
+  unsigned int active = 0;
+#pragma unroll
+  for (int k = 0; k < (kPairTile * kPairTile) / 256; ++k) {
+    const int idx = tid + 256 * k;
+    const int ii = idx / kPairTile, jj = idx % kPairTile;
+    const int i = i0 + ii, j = j0 + jj;
+    if (i >= p.NB || j >= p.NB) continue;
+    float logit = 0.f;
+    if (!skip) {
+      const int o = ii * kPairLd + jj;
+      const int t = kPairTile * kPairLd;
+      logit = (lds[o] + lds[t + o]) + (lds[2 * t + o] + lds[3 * t + o]);
+    }
+    float soft = 1.f / (1.f + expf(-logit));
+    if (p.causal && j > i) soft = 0.f;
+    const bool on = soft >= tau || (p.force_diag && i == j);
+    active += on ? 1u : 0u;
+    const int64_t o = obase + (int64_t)i * p.NB + j;
+    p.soft[o] = soft;
+    p.mask[o] = on ? 1 : 0;
+    if (p.logits) p.logits[o] = logit;
+  }
+  // One atomic per workgroup: same-address atomics serialise in L2, so a per-wave
+  // atomic costs more than the extra barrier.
   const float tot = wave_sum((float)active);
-  if ((tid & 63) == 0 && tot > 0.f) atomicAdd(p.counter, (unsigned long long)(tot + 0.5f));
+  if (lane == 0) wave_count[wave] = (unsigned int)(tot + 0.5f);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int t = (wave_count[0] + wave_count[1]) + (wave_count[2] + wave_count[3]);
+    if (t) atomicAdd(p.counter, (unsigned long long)t);
+  }
 }
 
 }  // namespace tasft
@@ -206,12 +435,15 @@ using namespace tasft;
 
 extern "C" size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads,
                                              int64_t num_kv_heads, int64_t seq_len,
-                                             int64_t block_size, int64_t hidden) {
-  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0 || block_size <= 0 ||
-      hidden <= 0)
+                                             int64_t head_dim, int64_t block_size,
+                                             int64_t hidden) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0 ||
+      block_size <= 0 || hidden <= 0)
     return 0;
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  return (size_t)(batch * (num_q_heads + num_kv_heads) * nb * hidden) * sizeof(float) + 256;
+  // Projected units (hidden per block) and block means (head_dim per block), fp32.
+  return (size_t)(batch * (num_q_heads + num_kv_heads) * nb * (hidden + head_dim)) *
+             sizeof(float) + 256;
 }
 
 extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float* b_in,
@@ -241,15 +473,15 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   if ((((uintptr_t)q) & 15u) || (((uintptr_t)k) & 15u) || (((uintptr_t)w_in) & 15u))
     return set_error(kErrInvalidArgument, "gate: q, k and w_in must be 16-byte aligned");
   const size_t need = tasft_gate_workspace_bytes(batch, num_q_heads, num_kv_heads, seq_len,
-                                                 block_size, hidden);
+                                                 head_dim, block_size, hidden);
   if (workspace_bytes < need)
     return set_error(kErrWorkspace, "gate: workspace too small: need %zu bytes, got %zu", need,
                      workspace_bytes);
   const int64_t nb = (seq_len + block_size - 1) / block_size;
   const int64_t chunks = (nb + kPoolBlocks - 1) / kPoolBlocks;
-  const int64_t row_tiles = (nb + kPairRows - 1) / kPairRows;
+  const int64_t tiles = (nb + kPairTile - 1) / kPairTile;
   if (batch * (num_q_heads + num_kv_heads) * chunks > 0x7fffffffLL ||
-      batch * num_q_heads * row_tiles > 0x7fffffffLL || seq_len > 0x3fffffffLL)
+      batch * num_q_heads * tiles * tiles > 0x7fffffffLL || seq_len > 0x3fffffffLL)
     return set_error(kErrUnsupported, "gate: problem too large for one launch");
 
   GatePoolParams pp;
@@ -259,6 +491,10 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   pp.b_in = b_in;
   pp.uq = (float*)workspace;
   pp.uk = pp.uq + batch * num_q_heads * nb * hidden;
+  // Block means start on a 256-byte boundary (16-byte vector loads); the slack is part of
+  // the workspace size.
+  pp.pq = (float*)workspace + ((batch * (num_q_heads + num_kv_heads) * nb * hidden + 63) & ~63LL);
+  pp.pk = pp.pq + batch * num_q_heads * nb * head_dim;
   pp.counter = active_count;
   for (int j = 0; j < 3; ++j) {
     pp.sq[j] = q_strides[j];
@@ -275,8 +511,23 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   pp.chunks = (int)chunks;
 
   hipStream_t s = (hipStream_t)stream;
-  const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * chunks;
-  hipLaunchKernelGGL(gate_pool_project_kernel, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+  const bool fast = block_size == 64 && (head_dim == 64 || head_dim == 128) &&
+                    seq_len * std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
+  if (fast) {
+    const int64_t fchunks = (nb + kFastPB - 1) / kFastPB;
+    const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * fchunks;
+    if (head_dim == 128)
+      hipLaunchKernelGGL(gate_pool64_kernel<128>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+    else
+      hipLaunchKernelGGL(gate_pool64_kernel<64>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+    const int64_t rq = batch * num_q_heads * nb, rk = batch * num_kv_heads * nb;
+    const int64_t gridp = ((rq + kProjTile - 1) / kProjTile + (rk + kProjTile - 1) / kProjTile) *
+                          ((hidden + kProjTile - 1) / kProjTile);
+    hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)gridp), dim3(256), 0, s, pp);
+  } else {
+    const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * chunks;
+    hipLaunchKernelGGL(gate_pool_project_kernel, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate: pool launch failed: %s", hipGetErrorString(err));
@@ -298,8 +549,8 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   qp.hidden = pp.hidden;
   qp.causal = (flags & 1) ? 1 : 0;
   qp.force_diag = (flags & 2) ? 1 : 0;
-  qp.row_tiles = (int)row_tiles;
-  const int64_t grid2 = batch * num_q_heads * row_tiles;
+  qp.tiles = (int)tiles;
+  const int64_t grid2 = batch * num_q_heads * tiles * tiles;
   hipLaunchKernelGGL(gate_pairwise_kernel, dim3((unsigned)grid2), dim3(256), 0, s, qp);
   if ((err = hipGetLastError()) != hipSuccess)
     return set_error(kErrLaunch, "gate: pairwise launch failed: %s", hipGetErrorString(err));

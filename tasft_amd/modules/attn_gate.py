@@ -235,7 +235,7 @@ class AttnGate(nn.Module):
         mask = torch.empty((B, H, nb, nb), dtype=torch.uint8, device=dev)
         logits = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev) if return_logits else None
         active = torch.empty((1,), dtype=torch.int64, device=dev)
-        ws_bytes = lib.tasft_gate_workspace_bytes(B, H, Hkv, S, self.block_size, hidden)
+        ws_bytes = lib.tasft_gate_workspace_bytes(B, H, Hkv, S, D, self.block_size, hidden)
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         status = lib.tasft_gate_fwd(
             q.data_ptr(), k.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(),

@@ -72,6 +72,8 @@ CASES = [
     (1, 4, 4, 30, 16, 8, 32, False),       # non-causal, ragged
     (1, 8, 8, 256, 64, 16, 48, True),      # odd hidden size
     (1, 2, 1, 777, 128, 48, 64, True),     # block size outside {32,64,128}
+    (1, 4, 2, 700, 64, 64, 32, True),      # block 64, D=64, 11 blocks (partial pool chunk)
+    (1, 4, 2, 1300, 128, 64, 200, False),  # block 64, 21 blocks, hidden > one staging tile
 ]
 
 
