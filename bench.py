@@ -9,7 +9,11 @@ B=64, S_kv=32768, 51 of 512 blocks per KV head) in HBM GB/s, the Qwen-2.5-7B pre
 (config 4) and the gate target (config 5), plus a CPU baseline of the oracle on a bounded
 sample of config 2.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-extras] [--no-cpu-baseline]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--extras decode,qwen,gate_target|none]
+                       [--no-extras] [--no-cpu-baseline] [--copy-probe MIB]
+
+``--copy-probe MIB`` instead times a plain device-to-device copy of MIB MiB and prints
+one JSON line; it is the calibration workload for the HBM byte counters.
 """
 from __future__ import annotations
 
@@ -28,6 +32,11 @@ METRIC = "sparse-attn prefill ms + decode HBM GB/s @80% sparsity, Llama-3-8B sha
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 FLOP_PER_BLOCK = 4 * 64 * 64 * 128  # QK^T + PV of one 64x64 tile at D=128
+# HBM bytes per launch of the config-2 prefill kernel, measured offline with rocprofv3:
+# FETCH_SIZE (KiB per dispatch, scaled by 2.0, the factor a plain 256 MiB copy shows) plus
+# WRITE_SIZE (scale 1.0), on `bench.py --no-cpu-baseline --steps 3 --warmup 1`. Against the
+# 673.2 MB algorithmic bytes (Q + K + V + O + mask) this is 1.30x.
+PREFILL_TRAFFIC_BYTES = 294671 * 1024 * 2.0 + 262151 * 1024
 
 
 def log(msg: str) -> None:
@@ -253,21 +262,52 @@ def cpu_baseline(res, budget_s: float = 20.0):
                       f"(batch, head) pairs of config 2, scaled linearly to all heads"}
 
 
+def copy_probe(torch, dev, mib: int) -> int:
+    """Time y.copy_(x) for an MIB-MiB fp32 buffer: reads and writes exactly MIB MiB each."""
+    n = mib * 1024 * 1024 // 4
+    x = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    y = torch.empty_like(x)
+    for _ in range(2):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    t = LaunchTimer(torch)
+    for _ in range(3):
+        with _Span(t):
+            y.copy_(x)
+    torch.cuda.synchronize()
+    ms = t.total_ms() / 3
+    print(json.dumps({"copy_probe_mib": mib, "bytes_read": n * 4, "bytes_written": n * 4,
+                      "ms": round(ms, 4), "gbps": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-extras", action="store_true", help="skip decode / Qwen / gate-target figures")
+    ap.add_argument("--extras", default="decode,qwen,gate_target",
+                    help="comma list of extra workloads (decode, qwen, gate_target) or 'none'")
+    ap.add_argument("--no-extras", action="store_true", help="same as --extras none")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="time a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU layout is "
-              "described in DESIGN.md and is not run here", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): every GPU box here has "
+              "one GPU, and sharding across GPUs is a design note, not a measured run",
+              file=sys.stderr)
+        return 2
+    extras = set() if args.no_extras or args.extras == "none" else set(args.extras.split(","))
+    unknown = extras - {"decode", "qwen", "gate_target"}
+    if unknown:
+        print(f"unknown --extras entries: {sorted(unknown)}", file=sys.stderr)
         return 2
     import torch
 
     dev = torch.device("cuda:0")
+    if args.copy_probe:
+        return copy_probe(torch, dev, args.copy_probe)
     log("bench: config 2 gate + prefill")
     res = bench_config2(torch, dev, args.steps, args.warmup)
     extra = {
@@ -278,16 +318,18 @@ def main() -> int:
         "executed_blocks": res["executed_blocks"],
         "causal_sparsity": round(res["causal_sparsity"], 4),
     }
-    if not args.no_extras:
+    if "decode" in extras:
         log("bench: config 3 decode")
         d = bench_decode(torch, dev, max(10, args.steps), args.warmup)
         extra.update({"decode_ms": round(d["decode_ms"], 4), "decode_hbm_gbps": round(d["decode_hbm_gbps"], 1),
                       "decode_hbm_frac": round(d["decode_hbm_gbps"] / PEAK_HBM_GBPS, 4),
                       "decode_bytes": d["decode_bytes"]})
+    if "qwen" in extras:
         log("bench: config 4 Qwen prefill")
         qw = bench_qwen(torch, dev, max(5, args.steps // 2), min(3, args.warmup))
         extra.update({"qwen_prefill_ms": round(qw["qwen_prefill_ms"], 4),
                       "qwen_prefill_tflops_executed": round(qw["qwen_prefill_tflops"], 1)})
+    if "gate_target" in extras:
         log("bench: config 5 gate target")
         gt = bench_gate_target(torch, dev, max(5, args.steps // 2), min(3, args.warmup))
         extra.update({"gate_target_ms": round(gt["gate_target_ms"], 4),
@@ -317,9 +359,11 @@ def main() -> int:
             "block": res["shape"].block, "gate_hidden": 128, "target_causal_sparsity": 0.8,
         },
         "roofline": {
-            "kernel": "bsfa_prefill_kernel<64,128>",
+            "kernel": "bsfa_prefill_bs64_kernel<128>",
             "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": round(PREFILL_TRAFFIC_BYTES),
+            "traffic_note": "HBM bytes per launch from rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE, offline",
             "algorithmic": f"{res['executed_blocks']} executed 64x64 blocks x {FLOP_PER_BLOCK} flop",
         },
         "cpu_baseline": cpu,

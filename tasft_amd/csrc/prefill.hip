@@ -252,10 +252,11 @@ static hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
 // Four waves per (batch, query head, query block): wave w owns query rows 32*(w&1)..+31
 // and the key half 32*(w>>1)..+31 of every key block, so each wave issues 8 + D/16 MFMAs
 // per block and two waves share a SIMD. The two key-half partial results of a row are
-// merged once at the end. K and V of the next active block are loaded into registers
-// while the current block is computed, then written to LDS row-major with a 16-byte XOR
-// swizzle (conflict-free without padding). V^T operands come from ds_read_b64_tr_b16, so
-// V is never transposed by VALU. The softmax rescale is lazy: the running maximum used
+// merged once at the end. K and V of the next active block are copied HBM -> LDS by
+// buffer_load_dwordx4 ... lds (no staging registers) into the other of two LDS stages
+// while the current block is computed (one barrier per block), row-major with a 16-byte
+// XOR swizzle (conflict-free without padding). V^T operands come from
+// ds_read_b64_tr_b16, so V is never transposed by VALU. The softmax rescale is lazy: the running maximum used
 // for exp2 is only moved when a new score exceeds it by more than kRescaleLog2 (so P
 // stays <= 2^8); numerator and denominator share the same reference, so the normalised
 // output is unchanged.
