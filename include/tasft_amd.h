@@ -33,7 +33,7 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (1). */
+/* ABI version of this library (2). */
 int tasft_abi_version(void);
 
 /*
@@ -49,13 +49,27 @@ int tasft_abi_version(void);
  * Rows with no admissible key are 0. P is rounded to bf16 before the PV product.
  * block_mask: [B, Hq, ceil(S/bs), ceil(S/bs)] bytes, strides in mask_strides (bytes).
  * head_dim in {64, 128}; block_size in {32, 64, 128}; strides of b/h/s multiples of 8.
+ * workspace: NULL (one workgroup per query-block row), or >=
+ * tasft_bsfa_prefill_workspace_bytes(...) bytes, 16-byte aligned: then (block size 64)
+ * a persistent launch keeps every CU slot busy, pulling rows from ticket counters kept
+ * in the workspace (zeroed on `stream` by the call itself). The output does not depend
+ * on it. Calls that share one workspace must be ordered on one stream.
  */
 int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* out,
-                           const uint8_t* block_mask, int64_t batch, int64_t num_q_heads,
+                           const uint8_t* block_mask, void* workspace, size_t workspace_bytes,
+                           int64_t batch, int64_t num_q_heads,
                            int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
                            int64_t block_size, const int64_t* q_strides, const int64_t* k_strides,
                            const int64_t* v_strides, const int64_t* o_strides,
                            const int64_t* mask_strides, float scale, int causal, void* stream);
+
+/*
+ * Bytes of the optional workspace of tasft_bsfa_prefill_fwd (work-queue counters).
+ * No reference counterpart: the reference launches one program per query block in
+ * grid order (tasft/kernels/block_sparse_fa.py:517-550).
+ */
+size_t tasft_bsfa_prefill_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t seq_len,
+                                          int64_t block_size);
 
 /*
  * Bytes of workspace tasft_bsfa_decode_fwd needs for `num_splits` splits.

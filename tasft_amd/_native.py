@@ -20,6 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtasft_amd.so"
 EXPORTED_SYMBOLS = (
     "tasft_last_error",
     "tasft_abi_version",
+    "tasft_bsfa_prefill_workspace_bytes",
     "tasft_bsfa_prefill_fwd",
     "tasft_bsfa_decode_workspace_bytes",
     "tasft_bsfa_decode_fwd",
@@ -41,9 +42,10 @@ _SZ = ctypes.c_size_t
 _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_last_error": (ctypes.c_char_p, []),
     "tasft_abi_version": (_I, []),
+    "tasft_bsfa_prefill_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "tasft_bsfa_prefill_fwd": (
         _I,
-        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+        [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
     ),
     "tasft_bsfa_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),

@@ -20,6 +20,8 @@
 // accumulator registers feed the PV product O^T = V^T . P^T directly as the B operand
 // with no shuffle. K (row major) and V^T (transposed while staging) go through LDS
 // rows padded so the MFMA operand reads are bank-conflict free on the 64-bank LDS.
+#include <algorithm>
+
 #include "common.h"
 
 namespace tasft {
@@ -35,7 +37,53 @@ struct PrefillParams {
   int B, Hq, Hkv, G, S, NB;
   float scale_log2;  // softmax scale * log2(e)
   int causal;
+  int* queue;        // per-partition ticket counters of the persistent launch, or null
+  int parts;         // work partitions: 8 (one per XCD) or 1
+  int wg_per_part;   // persistent workgroups per partition
 };
+
+// Static order of the (batch, query head, query block) work items. gfx950 dispatches
+// workgroup i to XCD i % 8; each XCD walks the KV groups congruent to it modulo 8 one at
+// a time (all query heads and query blocks of the group, longest causal rows first) so
+// the group's K/V stays in that XCD's L2. With a number of KV groups that is not a
+// multiple of 8 the order is group-major.
+struct PrefillItem {
+  int b, kvh, h, qb;
+};
+
+__device__ __forceinline__ PrefillItem prefill_item(const PrefillParams& p, int64_t idx) {
+  const int64_t groups = (int64_t)p.B * p.Hkv;
+  const int64_t per_group = (int64_t)p.G * p.NB;
+  int64_t grp, r;
+  if ((groups & 7) == 0) {
+    const int64_t j = idx >> 3;
+    grp = (idx & 7) + 8 * (j / per_group);
+    r = j % per_group;
+  } else {
+    grp = idx / per_group;
+    r = idx % per_group;
+  }
+  const int qslot = (int)(r / p.G);
+  PrefillItem it;
+  it.qb = p.causal ? (p.NB - 1 - qslot) : qslot;
+  it.b = (int)(grp / p.Hkv);
+  it.kvh = (int)(grp % p.Hkv);
+  it.h = it.kvh * p.G + (int)(r % p.G);
+  return it;
+}
+
+// Persistent launch (block size 64). Rows differ widely in cost (a gate can light whole
+// rows), and a grid of one workgroup per row leaves CU slots idle while heavy and light
+// rows are dispatched side by side. Instead, two workgroups per CU stay resident and
+// pull rows from a ticket counter per partition (one partition per XCD: item
+// x + 8j belongs to XCD x, so the static group-major order and its L2 locality are
+// kept). The counters live in the caller's workspace and are zeroed by
+// bsfa_queue_reset_kernel on the same stream before every launch.
+constexpr int kQueueSlots = 8;
+
+__global__ void bsfa_queue_reset_kernel(int* queue) {
+  if (threadIdx.x < kQueueSlots) queue[threadIdx.x] = 0;
+}
 
 template <int BS, int D>
 __global__ void __launch_bounds__(BS / 32 * kWave)
@@ -57,19 +105,8 @@ bsfa_prefill_kernel(const PrefillParams p) {
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  // Work item: query blocks in descending order (causal rows get longer with qb, so the
-  // heaviest rows start first); inside one query-block slab the query heads of a KV
-  // head share an XCD.
-  const int64_t per_slab = (int64_t)p.B * p.Hq;
-  const int64_t idx = blockIdx.x;
-  const int slab = (int)(idx / per_slab);
-  const int qb = p.causal ? (p.NB - 1 - slab) : slab;
-  int64_t grp;
-  int g;
-  xcd_group_map(idx % per_slab, (int64_t)p.B * p.Hkv, p.G, &grp, &g);
-  const int b = (int)(grp / p.Hkv);
-  const int kvh = (int)(grp % p.Hkv);
-  const int h = kvh * p.G + g;
+  const PrefillItem item = prefill_item(p, (int64_t)blockIdx.x);
+  const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
 
   const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
@@ -332,6 +369,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t kB[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t vB[TILE];
   __shared__ float xch_ml[2][2][kWave];
+  __shared__ int next_slot;
   static_assert(DTILES * 16 * kWave * 4 == TILE, "merge buffer size");
 
   const int tid = threadIdx.x;
@@ -342,26 +380,32 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  // Work item: each XCD walks one KV group at a time (all its query heads and query
-  // blocks, longest causal rows first) so the group's K/V stays in that XCD's L2.
-  const int64_t idx = blockIdx.x;
-  const int64_t groups = (int64_t)p.B * p.Hkv;
-  const int64_t per_group = (int64_t)p.G * p.NB;
-  int64_t grp, r;
-  if ((groups & 7) == 0) {
-    const int64_t j = idx >> 3;
-    grp = (idx & 7) + 8 * (j / per_group);
-    r = j % per_group;
-  } else {
-    grp = idx / per_group;
-    r = idx % per_group;
+  // Per-lane byte offsets (within a tile's rows) of this wave's DMA units.
+  int kvoff[UNITS_PER_WAVE], vvoff[UNITS_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < UNITS_PER_WAVE; ++i) {
+    const int byte = (wave * UNITS_PER_WAVE + i) * 1024 + lane * 16;
+    const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+    kvoff[i] = (row * (int)p.sk[2] + swz_k<D>(row, pos) * 8) * 2;
+    vvoff[i] = (row * (int)p.sv[2] + swz_v<D>(row, pos) * 8) * 2;
   }
-  const int qslot = (int)(r / p.G);
-  const int g = (int)(r % p.G);
-  const int qb = p.causal ? (p.NB - 1 - qslot) : qslot;
-  const int b = (int)(grp / p.Hkv);
-  const int kvh = (int)(grp % p.Hkv);
-  const int h = kvh * p.G + g;
+  const int krow_l = kh * 32 + col;
+  const int grp16 = lane >> 4, t16 = lane & 15;  // ds_read_tr group and lane in group
+  const int tr_row = t16 >> 2;                   // source row offset within a 4-row run
+  const int tr_cb = t16 & 3;                     // source 8-byte column block
+
+  // Work distribution: one item per workgroup, or the persistent ticket loop.
+  const bool persistent = p.queue != nullptr;
+  const int part = persistent ? (int)(blockIdx.x % p.parts) : 0;
+  const int64_t per_part = persistent ? (int64_t)p.B * p.Hq * p.NB / p.parts : 1;
+  int64_t slot = persistent ? (int64_t)(blockIdx.x / p.parts) : 0;
+  while (slot < per_part) {
+  const int64_t idx = !persistent ? (int64_t)blockIdx.x : (p.parts == 8 ? part + 8 * slot : slot);
+  // The next ticket is fetched now; its latency hides behind this item.
+  int ticket = 0;
+  if (persistent && tid == 0) ticket = atomicAdd(&p.queue[part], 1);
+  const PrefillItem item = prefill_item(p, idx);
+  const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
 
   const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
@@ -379,15 +423,6 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     qf[ks] = as_bf16x8(val);
   }
 
-  // Per-lane byte offsets (within a tile's rows) of this wave's DMA units.
-  int kvoff[UNITS_PER_WAVE], vvoff[UNITS_PER_WAVE];
-#pragma unroll
-  for (int i = 0; i < UNITS_PER_WAVE; ++i) {
-    const int byte = (wave * UNITS_PER_WAVE + i) * 1024 + lane * 16;
-    const int row = byte / ROWB, pos = (byte % ROWB) / 16;
-    kvoff[i] = (row * (int)p.sk[2] + swz_k<D>(row, pos) * 8) * 2;
-    vvoff[i] = (row * (int)p.sv[2] + swz_v<D>(row, pos) * 8) * 2;
-  }
   // Start the DMA of key block kb into one stage (rows >= S arrive as zeros).
   auto issue = [&](uint8_t* kt, uint8_t* vt, int kb) {
     const int key0 = kb * BS;
@@ -401,11 +436,6 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   for (int dt = 0; dt < DTILES; ++dt) oacc[dt] = (f32x16_t){};
   float m_ref = -INFINITY;  // exp2 reference of this lane's query row (log2 domain)
   float l_run = 0.f;
-
-  const int krow_l = kh * 32 + col;
-  const int grp16 = lane >> 4, t16 = lane & 15;  // ds_read_tr group and lane in group
-  const int tr_row = t16 >> 2;                   // source row offset within a 4-row run
-  const int tr_cb = t16 & 3;                     // source 8-byte column block
 
   // One key block from stage (kt, vt): S^T MFMAs, online softmax, PV MFMAs.
   auto compute = [&](const uint8_t* kt, const uint8_t* vt, int kb) {
@@ -536,11 +566,50 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
       }
     }
   }
+  if (!persistent) break;
+  if (tid == 0) next_slot = p.wg_per_part + ticket;
+  __syncthreads();  // merge buffer, stages and next_slot are free for the next item
+  slot = next_slot;
+  }
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Resident workgroups per CU of a kernel (at least 1).
+template <typename K>
+static int resident_per_cu(K kernel, int threads) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n <= 0) n = 1;
+  return n;
 }
 
 template <int D>
-static hipError_t launch_prefill_bs64(const PrefillParams& p, hipStream_t stream) {
-  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
+static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t stream) {
+  const int64_t total = (int64_t)p.NB * p.B * p.Hq;
+  int64_t grid = total;
+  if (queue) {
+    // Every resident workgroup slot filled once, a whole number per partition.
+    p.parts = (((int64_t)p.B * p.Hkv) % 8 == 0) ? 8 : 1;
+    static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D>, 256);
+    int64_t wg = std::min<int64_t>(total, (int64_t)per_cu * device_cus());
+    wg = std::max<int64_t>(p.parts, wg / p.parts * p.parts);
+    p.wg_per_part = (int)(wg / p.parts);
+    p.queue = queue;
+    grid = wg;
+    hipLaunchKernelGGL(bsfa_queue_reset_kernel, dim3(1), dim3(64), 0, stream, queue);
+  }
   hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
@@ -551,8 +620,15 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 using namespace tasft;
 
+extern "C" size_t tasft_bsfa_prefill_workspace_bytes(int64_t batch, int64_t num_q_heads,
+                                                     int64_t seq_len, int64_t block_size) {
+  if (batch <= 0 || num_q_heads <= 0 || seq_len <= 0 || block_size <= 0) return 0;
+  return 256;  // the persistent launch's ticket counters
+}
+
 extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* out,
-                                      const uint8_t* block_mask, int64_t batch,
+                                      const uint8_t* block_mask, void* workspace,
+                                      size_t workspace_bytes, int64_t batch,
                                       int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
                                       int64_t head_dim, int64_t block_size,
                                       const int64_t* q_strides, const int64_t* k_strides,
@@ -588,6 +664,14 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   const int64_t nb = (seq_len + block_size - 1) / block_size;
   if (nb * batch * num_q_heads > 0x7fffffffLL || seq_len > 0x3fffffffLL)
     return set_error(kErrUnsupported, "prefill: problem too large for one launch");
+  const size_t ws_need = tasft_bsfa_prefill_workspace_bytes(batch, num_q_heads, seq_len, block_size);
+  if (workspace) {
+    if (workspace_bytes < ws_need)
+      return set_error(kErrWorkspace, "prefill: workspace too small: need %zu bytes, got %zu",
+                       ws_need, workspace_bytes);
+    if (((uintptr_t)workspace) & 15u)
+      return set_error(kErrInvalidArgument, "prefill: workspace must be 16-byte aligned");
+  }
 
   PrefillParams p;
   p.q = (const uint16_t*)q;
@@ -610,11 +694,15 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   p.NB = (int)nb;
   p.scale_log2 = scale * kLog2e;
   p.causal = causal ? 1 : 0;
+  p.queue = nullptr;
+  p.parts = 1;
+  p.wg_per_part = 1;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_prefill_bs64<128>(p, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_prefill_bs64<64>(p, s);
+  int* queue = (int*)workspace;  // ticket counters of the persistent launch (block size 64)
+  if (block_size == 64 && head_dim == 128) err = launch_prefill_bs64<128>(p, queue, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_prefill_bs64<64>(p, queue, s);
   else if (block_size == 32 && head_dim == 128) err = launch_prefill<32, 128>(p, s);
   else if (block_size == 32 && head_dim == 64) err = launch_prefill<32, 64>(p, s);
   else if (block_size == 128 && head_dim == 128) err = launch_prefill<128, 128>(p, s);

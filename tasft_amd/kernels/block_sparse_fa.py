@@ -239,9 +239,12 @@ class BlockSparseFlashAttention:
         mask = _mask_bytes(block_mask.to(q.device))
         out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
         scale = 1.0 / math.sqrt(D)
+        # Workspace for the persistent launch's work-queue counters.
+        ws_bytes = lib.tasft_bsfa_prefill_workspace_bytes(B, H, S, self.block_size)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
         status = lib.tasft_bsfa_prefill_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
-            B, H, k.shape[1], S, D, self.block_size,
+            workspace.data_ptr(), ws_bytes, B, H, k.shape[1], S, D, self.block_size,
             _native.strides(q), _native.strides(k), _native.strides(v), _native.strides(out),
             _native.strides(mask), scale, 1 if causal else 0, _native.stream_handle(q.device),
         )

@@ -158,3 +158,38 @@ def test_config4_full_size_sampled_heads():
     shape = wl.CONFIG_SHAPES[4]
     mask, _ = wl.qwen_mask(shape, 2004)
     _sampled_parity(4, mask, 1004, heads=[(0, 0), (1, 27)])
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "bs"), [
+    (2, 16, 4, 2048, 64),   # 8 KV groups: per-XCD partitions
+    (2, 6, 3, 1500, 64),    # 6 KV groups: one partition, ragged
+    (1, 8, 2, 1024, 128),   # generic kernel
+])
+def test_persistent_queue_is_bit_identical(B, Hq, Hkv, S, bs):
+    """The persistent work queue (workspace given) must not change any output bit."""
+    import ctypes
+
+    from tasft_amd import _native
+
+    dev = require_gpu()
+    q, k, v = _inputs(B, Hq, Hkv, S, 128, 4242 + S)
+    shape = wl.Shape(B, Hq, Hkv, S, 128, bs)
+    mask = wl.bernoulli_causal_mask(shape, 0.15, 5151 + S)
+    mask[0, 1, -3:, :] = True   # whole rows lit, as a gate can produce
+    mask[B - 1, Hq - 1, 5, :] = True
+    q, k, v, mask = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    out_ws = _run(q, k, v, mask, bs, True)  # the Python path passes a workspace
+    lib = _native.load_library()
+    out = torch.empty_like(q)
+    m8 = mask.view(torch.uint8)
+    rc = lib.tasft_bsfa_prefill_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), m8.data_ptr(), None, 0,
+        B, Hq, Hkv, S, 128, bs, _native.strides(q), _native.strides(k), _native.strides(v),
+        _native.strides(out), _native.strides(m8), ctypes.c_float(1.0 / math.sqrt(128)), 1,
+        _native.stream_handle(dev))
+    _native.check(rc, "tasft_bsfa_prefill_fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_ws)
+    ref = orc.attention_block_gather(to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu()),
+                                     mask.cpu().numpy(), bs, True)
+    assert_close_bf16(out_ws, ref, "persistent prefill")

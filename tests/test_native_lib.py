@@ -33,7 +33,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace_sizes():
     lib = _native.load_library()
-    assert lib.tasft_abi_version() == 1
+    assert lib.tasft_abi_version() == 2
+    assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 8192, 64) == 256
+    assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 0, 64) == 0
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
     assert lib.tasft_bsfa_decode_workspace_bytes(0, 32, 128, 4) == 0
     nb = 8192 // 64
@@ -48,16 +50,19 @@ def _i64(vals):
 def test_invalid_arguments_return_errors_without_launch():
     lib = _native.load_library()
     st = _i64([0, 0, 0, 1])
-    rc = lib.tasft_bsfa_prefill_fwd(None, None, None, None, None, 1, 32, 8, 128, 128, 64,
+    rc = lib.tasft_bsfa_prefill_fwd(None, None, None, None, None, None, 0, 1, 32, 8, 128, 128, 64,
                                     st, st, st, st, st, 1.0, 1, None)
     assert rc == -1 and b"null pointer" in lib.tasft_last_error()
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, 1, 32, 8, 128, 96, 64,
+    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, None, 0, 1, 32, 8, 128, 96, 64,
                                     st, st, st, st, st, 1.0, 1, None)
     assert rc == -2 and b"head_dim" in lib.tasft_last_error()
-    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, 1, 30, 8, 128, 128, 64,
+    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, None, 0, 1, 30, 8, 128, 128, 64,
                                     st, st, st, st, st, 1.0, 1, None)
     assert rc == -1 and b"multiple" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, fake, 16, 1, 32, 8, 128, 128, 64,
+                                    st, st, st, st, st, 1.0, 1, None)
+    assert rc == -4 and b"workspace" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_fwd(fake, fake, fake, fake, fake, None, fake, 0, 1, 32, 8, 1024, 128,
                                    64, 4, st, st, st, st, st, 1.0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
