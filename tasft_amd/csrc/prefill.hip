@@ -37,6 +37,7 @@ struct PrefillParams {
   int B, Hq, Hkv, G, S, NB;
   float scale_log2;  // softmax scale * log2(e)
   int causal;
+  int small_spans;   // S * row bytes of K and V below 2^31: 32-bit DMA address math
   int* queue;        // per-partition ticket counters of the persistent launch, or null
   int parts;         // work partitions: 8 (one per XCD) or 1
   int wg_per_part;   // persistent workgroups per partition
@@ -423,12 +424,24 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     qf[ks] = as_bf16x8(val);
   }
 
-  // Start the DMA of key block kb into one stage (rows >= S arrive as zeros).
+  // Start the DMA of key block kb into one stage (rows >= S arrive as zeros). With
+  // small spans the resource base and size take 32-bit scalar math only.
+  const uint32_t krb = (uint32_t)p.sk[2] * 2u, vrb = (uint32_t)p.sv[2] * 2u;
   auto issue = [&](uint8_t* kt, uint8_t* vt, int kb) {
-    const int key0 = kb * BS;
-    const int64_t rows_left = (int64_t)(p.S - key0);
-    dma_tile<D>(kt, tile_rsrc(kbase + (int64_t)key0 * p.sk[2], rows_left * p.sk[2] * 2), kvoff, wave);
-    dma_tile<D>(vt, tile_rsrc(vbase + (int64_t)key0 * p.sv[2], rows_left * p.sv[2] * 2), vvoff, wave);
+    if (p.small_spans) {
+      const uint32_t key0 = (uint32_t)kb * BS, left = (uint32_t)p.S - key0;
+      dma_tile<D>(kt, __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)kbase + key0 * krb),
+                                                        (short)0, (int)(left * krb), 0x00020000),
+                  kvoff, wave);
+      dma_tile<D>(vt, __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)vbase + key0 * vrb),
+                                                        (short)0, (int)(left * vrb), 0x00020000),
+                  vvoff, wave);
+    } else {
+      const int key0 = kb * BS;
+      const int64_t rows_left = (int64_t)(p.S - key0);
+      dma_tile<D>(kt, tile_rsrc(kbase + (int64_t)key0 * p.sk[2], rows_left * p.sk[2] * 2), kvoff, wave);
+      dma_tile<D>(vt, tile_rsrc(vbase + (int64_t)key0 * p.sv[2], rows_left * p.sv[2] * 2), vvoff, wave);
+    }
   };
 
   f32x16_t oacc[DTILES];
@@ -694,6 +707,8 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   p.NB = (int)nb;
   p.scale_log2 = scale * kLog2e;
   p.causal = causal ? 1 : 0;
+  p.small_spans = (seq_len * k_strides[2] * 2 < 0x7fffffffLL &&
+                   seq_len * v_strides[2] * 2 < 0x7fffffffLL) ? 1 : 0;
   p.queue = nullptr;
   p.parts = 1;
   p.wg_per_part = 1;
