@@ -46,6 +46,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t decode_rsrc(const void* base, 
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
+// s_waitcnt immediate waiting until at most n vector-memory operations are outstanding
+// (expcnt and lgkmcnt left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // One 16-byte-per-lane DMA (buffer_load ... lds) of 1 KB into LDS at `dst`.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, int voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TASFT_LDS void*)dst, 16, voff, 0, 0, 0);
@@ -72,13 +76,15 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   constexpr int VTILE = SUB * D * 2;  // bytes of one sub-block of V
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kDecodeWaves][VTILE];  // per-wave V tile
   __shared__ uint8_t hb[kDecodeMaxRange];                     // head bits per block of the range
+  __shared__ uint16_t sel[kDecodeMaxRange];                   // selected blocks (range offsets)
+  __shared__ int nsel_lds;
   __shared__ float p_lds[kDecodeWaves][SUB * MG + kWave];     // probabilities (+ dummy slots)
   __shared__ float a_lds[kDecodeWaves][MG];                   // rescale factor per head
   __shared__ float comb_ml[kDecodeWaves][MG][2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop state
   const int col = lane & 31;   // QK layout: query head of this lane
   const int half = lane >> 5;
   const int G = p.G;
@@ -138,15 +144,162 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   // Per-lane byte offsets inside a sub-block: K row `col` (A-operand layout); for the V
   // DMA, lane l of unit u fetches byte u*1024 + 16*l of the row-major tile.
   const int k_voff = (col * ks2 + half * 8) * 2;
-  int v_dma_off[VTILE / 1024];
-#pragma unroll
-  for (int u = 0; u < VTILE / 1024; ++u) {
-    const int byte = u * 1024 + lane * 16;
-    v_dma_off[u] = (byte / (D * 2)) * vs2 * 2 + byte % (D * 2);
-  }
+  // Unit u covers rows u*RPU .. u*RPU+RPU-1 (RPU = 1024 / row bytes): a per-lane base
+  // plus u * v_unit_stride. The whole offset stays in the per-lane (VGPR) offset, which
+  // the buffer range check covers, so rows past kv_len read as zeros.
+  constexpr int RPU = 1024 / (D * 2);
+  const int v_dma_base = (lane / (kWave / RPU)) * vs2 * 2 + (lane % (kWave / RPU)) * 16;
+  const int v_unit_stride = RPU * vs2 * 2;
   // Where this lane's probabilities go in p_lds (lanes of padding heads: a dummy slot).
   const bool pcol = col < MG;
 
+  if constexpr (NSUB == 1) {
+    // Selected blocks of the range, compacted once (wave 0), then taken round-robin by
+    // the waves. Each wave keeps the next block's loads in flight: its K loads are issued
+    // into the K registers as soon as the S MFMAs have read them, and its V DMA into the
+    // wave's V tile as soon as the PV product has read it.
+    if (wave == 0) {
+      int base = 0;
+      for (int c0 = 0; c0 < range; c0 += kWave) {
+        const int t = c0 + lane;
+        const bool on = t < range && hb[t] != 0;
+        const uint64_t bits = __ballot(on);
+        if (on) sel[base + __popcll(bits & ((1ull << lane) - 1ull))] = (uint16_t)t;
+        base += __popcll(bits);
+      }
+      if (lane == 0) nsel_lds = base;
+    }
+    __syncthreads();
+    // Uniform values (scalar registers) keep the buffer resources scalar.
+    const int nsel = __builtin_amdgcn_readfirstlane(nsel_lds);
+    constexpr int NKL = KT * KSTEPS;  // K load instructions per block
+    u32x4_t ka[KT][KSTEPS];
+    auto load_k = [&](int t_off) {
+      const int key0 = (lo + t_off) * BS;
+      const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)SUB * ks2 * 2);
+      if (key0 + SUB <= kv_len) {
+#pragma unroll
+        for (int t2 = 0; t2 < KT; ++t2)
+#pragma unroll
+          for (int ks = 0; ks < KSTEPS; ++ks)
+            ka[t2][ks] = buf_load16(kr, k_voff + ks * 32, t2 * 32 * ks2 * 2);
+      } else {
+        // Partial last block: K rows past kv_len are replaced by row kv_len-1; their
+        // scores are masked to -inf.
+        const int last = kv_len - 1 - key0;
+#pragma unroll
+        for (int t2 = 0; t2 < KT; ++t2) {
+          const int row = min(t2 * 32 + col, last);
+#pragma unroll
+          for (int ks = 0; ks < KSTEPS; ++ks)
+            ka[t2][ks] = buf_load16(kr, (row * ks2 + half * 8) * 2 + ks * 32, 0);
+        }
+      }
+    };
+    auto dma_v = [&](int t_off) {
+      const int key0 = (lo + t_off) * BS;
+      // The resource ends at row kv_len-1, so rows past kv_len arrive as zeros.
+      const __amdgpu_buffer_rsrc_t vr =
+          decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(SUB, kv_len - key0) * vs2 * 2);
+#pragma unroll
+      for (int u = 0; u < VTILE / 1024; ++u) dma16(vr, v_lds[wave] + u * 1024, v_dma_base + u * v_unit_stride);
+    };
+    int e = wave;
+    if (e < nsel) {
+      const int t0 = __builtin_amdgcn_readfirstlane((int)sel[e]);
+      load_k(t0);
+      dma_v(t0);
+    }
+    while (e < nsel) {
+      const int t_off = __builtin_amdgcn_readfirstlane((int)sel[e]);
+      const int kb = lo + t_off;
+      const int key0 = kb * BS;
+      const uint32_t hsel = __builtin_amdgcn_readfirstlane((int)hb[t_off]);
+      const bool head_on = col < G && ((hsel >> col) & 1u);
+      // S^T = K Q^T: rows = keys, cols = heads.
+      f32x16_t sacc[KT];
+#pragma unroll
+      for (int t2 = 0; t2 < KT; ++t2) {
+        sacc[t2] = (f32x16_t){};
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+          sacc[t2] = mfma_32x32x16_bf16(as_bf16x8(ka[t2][ks]), qf[ks], sacc[t2]);
+      }
+      // The next block of this wave: its K loads go out now (the K registers are free).
+      const int en = e + kDecodeWaves;
+      const bool more = en < nsel;
+      const int tn = more ? __builtin_amdgcn_readfirstlane((int)sel[en]) : 0;
+      if (more) load_k(tn);
+      // Register r of tile t2 holds key t2*32 + 8*(r/4) + 4*half + r%4 of head `col`.
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t2 = 0; t2 < KT; ++t2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const float x = (head_on && key < kv_len) ? sacc[t2][r] * p.scale_log2 : -INFINITY;
+          sacc[t2][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = pair_max32(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      float ls = 0.f;
+      float* pw = p_lds[wave];
+#pragma unroll
+      for (int t2 = 0; t2 < KT; ++t2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e2 = __builtin_amdgcn_exp2f(sacc[t2][r] - m_use);
+          ls += e2;
+          const int key = t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          pw[pcol ? key * MG + col : SUB * MG + lane] = e2;
+        }
+      }
+      l_run = l_run * alpha + ls;
+      m_run = m_new;
+      if (half == 0 && col < MG) a_lds[wave][col] = alpha;
+      // p_lds / a_lds / v_lds are private to this wave: wait for this block's V DMA (the
+      // next block's K loads, issued after it, may still be in flight), then a wave
+      // barrier orders the LDS writes and reads.
+      if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NKL));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // PV: oacc[g] = alpha_g * oacc[g] + sum_key p[key][g] * V[key][dc*8..+7].
+#pragma unroll
+      for (int gg = 0; gg < MG; ++gg) {
+        const float a = a_lds[wave][gg];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) oacc[gg][j] *= a;
+      }
+#pragma unroll 2
+      for (int i = 0; i < VPL; ++i) {
+        const int kk = kg + KG * i;
+        float vf[8];
+        unpack_bf16x8(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
+#pragma unroll
+        for (int gg = 0; gg < MG; ++gg) {
+          const float pv = pw[kk * MG + gg];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pv, vf[j], oacc[gg][j]);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (more) {
+        // The DMA writes the V tile through the memory path: every LDS read of it must
+        // have returned first.
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        dma_v(tn);
+      }
+      e = en;
+    }
+  } else {
   int rank = 0;  // union rank of the next entry in this range (uniform)
   for (int c0 = 0; c0 < range; c0 += kWave) {
     const int t = c0 + lane;
@@ -172,7 +325,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
             decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(SUB, kv_len - key0) * vs2 * 2);
 #pragma unroll
         for (int u = 0; u < VTILE / 1024; ++u)
-          dma16(vr, v_lds[wave] + u * 1024, v_dma_off[u]);
+          dma16(vr, v_lds[wave] + u * 1024, v_dma_base + u * v_unit_stride);
         u32x4_t ka[KT][KSTEPS];
         if (key0 + SUB <= kv_len) {
 #pragma unroll
@@ -264,6 +417,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     }
   }
 
+  }
   // Per wave: reduce the PV partials over key groups and the denominators over the lane
   // pair, then merge the 4 waves. Each wave's partial output goes to its own V tile.
   static_assert(MG * D * 4 <= VTILE, "merge buffer size");

@@ -371,9 +371,12 @@ class BlockSparseFlashAttention:
 
 
 def default_decode_splits(batch: int, num_kv_heads: int, num_blocks: int) -> int:
-    """Split-K factor giving about 2048 decode workgroups (8 per CU on 256 CUs)."""
+    """Split-K factor giving about 1024 decode workgroups (4 per CU on 256 CUs: each
+    workgroup streams enough blocks to amortise its prologue), and at least the number
+    of splits that keeps every split within 256 key blocks."""
     groups = max(1, batch * num_kv_heads)
-    return int(max(1, min(max(1, num_blocks // 4), math.ceil(2048 / groups))))
+    want = min(max(1, num_blocks // 4), math.ceil(1024 / groups))
+    return int(max(1, want, math.ceil(num_blocks / 256)))
 
 
 def executed_blocks(block_mask: torch.Tensor, causal: bool = True) -> torch.Tensor:
