@@ -149,6 +149,41 @@ int tasft_gate_target_fwd(const void* q, const void* k, float* target, int64_t b
                           const int64_t* k_strides, float scale, int causal, int normalize,
                           float temperature, float clamp, void* stream);
 
+/*
+ * Block mask -> compressed rows (CSR) of its active blocks.
+ * No reference counterpart: the reference hands its Triton kernel the dense mask and
+ * scans every byte of a row (tasft/kernels/block_sparse_fa.py:192-203); this gives
+ * callers (and index-based selection) the active blocks directly.
+ *
+ * Rows are (b, h, query block) in row-major order, rows = batch*num_heads*num_q_blocks.
+ * row_ptr [rows + 1] int32 receives the exclusive prefix of the per-row counts;
+ * col_idx receives each row's active key-block indices in ascending order, at most
+ * col_capacity of them in total (row_ptr[rows] is the full count, so overflow is
+ * visible). causal != 0 counts only key blocks <= the query block (the AND at
+ * tasft/kernels/block_sparse_fa.py:502-508). workspace: >=
+ * tasft_mask_compact_workspace_bytes(...) bytes.
+ */
+size_t tasft_mask_compact_workspace_bytes(int64_t batch, int64_t num_heads, int64_t num_q_blocks);
+int tasft_mask_compact(const uint8_t* block_mask, int64_t batch, int64_t num_heads,
+                       int64_t num_q_blocks, int64_t num_k_blocks, const int64_t* mask_strides,
+                       int causal, int32_t* row_ptr, int32_t* col_idx, int64_t col_capacity,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Padded index lists -> dense block mask, the input form of tasft_bsfa_decode_fwd for
+ * callers that select KV blocks by index (the decode selection of a serving engine).
+ * No reference counterpart (reference decode is dense:
+ * tasft/inference/vllm_patch.py:189-196).
+ *
+ * indices [rows, k] int32 with row stride index_row_stride (elements), -1 = empty slot;
+ * block_mask [rows, num_k_blocks] bytes, contiguous, receives 1 at every listed index
+ * and 0 elsewhere. *error_flag (device int) becomes non-zero if an index other than -1
+ * lies outside [0, num_k_blocks); such indices are skipped.
+ */
+int tasft_mask_from_indices(const int32_t* indices, int64_t rows, int64_t k,
+                            int64_t index_row_stride, int64_t num_k_blocks, uint8_t* block_mask,
+                            int* error_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

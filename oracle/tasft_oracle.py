@@ -22,6 +22,8 @@ asks for float64. How each function is pinned (checked independently of itself):
 * ``block_max`` / ``gate_target_from_qk``: equal ``gate_target_from_scores`` applied to
   explicitly built scores.
 * ``sparsity_stats`` / ``estimate_speedup``: literal values of tests/unit/test_kernel.py.
+* ``mask_to_csr`` / ``indices_to_mask``: a hand-checked literal example and the round
+  trip dense -> CSR -> dense (numpy ``nonzero`` / fancy-index scatter).
 """
 from __future__ import annotations
 
@@ -320,3 +322,33 @@ def executed_blocks(block_mask: np.ndarray, causal: bool = True) -> int:
         nb = m.shape[-1]
         m = m & np.tril(np.ones((nb, nb), dtype=bool))
     return int(np.count_nonzero(m))
+
+
+# ----------------------------------------------------------------------------- formats
+def mask_to_csr(mask: np.ndarray, causal: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    """Dense block mask ``[B, H, NBq, NBk]`` -> CSR ``(row_ptr, col_idx)`` of the active blocks.
+
+    Rows are ``(b, h, query block)`` row-major; columns ascend within a row. ``causal``
+    keeps only key blocks <= the query block, the AND applied before the reference kernel
+    (tasft/kernels/block_sparse_fa.py:502-508).
+    """
+    m = mask != 0
+    if causal:
+        nbq, nbk = m.shape[-2:]
+        m = m & np.tril(np.ones((nbq, nbk), dtype=bool))
+    rows = m.reshape(-1, m.shape[-1])
+    counts = rows.sum(axis=1).astype(np.int64)
+    row_ptr = np.zeros(rows.shape[0] + 1, dtype=np.int32)
+    row_ptr[1:] = np.cumsum(counts)
+    col_idx = np.nonzero(rows)[1].astype(np.int32)  # row-major order: ascending per row
+    return row_ptr, col_idx
+
+
+def indices_to_mask(indices: np.ndarray, num_blocks: int) -> np.ndarray:
+    """Padded index lists ``[..., K]`` (``-1`` = empty) -> bool mask ``[..., num_blocks]``."""
+    lead = indices.shape[:-1]
+    flat = indices.reshape(-1, indices.shape[-1])
+    out = np.zeros((flat.shape[0], num_blocks), dtype=bool)
+    r, c = np.nonzero(flat >= 0)
+    out[r, flat[r, c]] = True
+    return out.reshape(*lead, num_blocks)

@@ -27,6 +27,9 @@ EXPORTED_SYMBOLS = (
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
     "tasft_gate_target_fwd",
+    "tasft_mask_compact_workspace_bytes",
+    "tasft_mask_compact",
+    "tasft_mask_from_indices",
 )
 
 _lock = threading.Lock()
@@ -64,6 +67,12 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _F, _I, _I, _F, _F, _P],
     ),
+    "tasft_mask_compact_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "tasft_mask_compact": (
+        _I,
+        [_P, _I64, _I64, _I64, _I64, _I64P, _I, _P, _P, _I64, _P, _SZ, _P],
+    ),
+    "tasft_mask_from_indices": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
 }
 
 

@@ -15,7 +15,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 OUT_DIR = HERE.parent / "_lib"
 LIB_NAME = "libtasft_amd.so"
-SOURCES = ["capi.cpp", "prefill.hip", "decode.hip", "gate.hip", "gate_target.hip"]
+SOURCES = ["capi.cpp", "prefill.hip", "decode.hip", "gate.hip", "gate_target.hip", "mask.hip"]
 ARCH = "gfx950"
 
 

@@ -6,6 +6,8 @@ from tasft_amd.kernels.block_sparse_fa import (
     default_decode_splits,
     detect_kernels,
     executed_blocks,
+    indices_to_mask,
+    mask_to_csr,
 )
 from tasft_amd.kernels.kernel_config import KernelConfig, LayerKernelConfig
 
@@ -18,4 +20,6 @@ __all__ = [
     "default_decode_splits",
     "detect_kernels",
     "executed_blocks",
+    "indices_to_mask",
+    "mask_to_csr",
 ]

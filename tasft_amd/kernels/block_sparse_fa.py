@@ -268,8 +268,9 @@ class BlockSparseFlashAttention:
         q: torch.Tensor,
         k_cache: torch.Tensor,
         v_cache: torch.Tensor,
-        block_mask: torch.Tensor,
+        block_mask: torch.Tensor | None = None,
         *,
+        block_indices: torch.Tensor | None = None,
         kv_lens: torch.Tensor | None = None,
         num_splits: int | None = None,
     ) -> torch.Tensor:
@@ -279,6 +280,9 @@ class BlockSparseFlashAttention:
             q: ``[B, Hq, 1, D]`` bf16, the new token's queries.
             k_cache, v_cache: ``[B, Hkv, S_kv, D]`` bf16; the new token's K/V are included.
             block_mask: ``[B, Hq, 1, ceil(S_kv / block_size)]``; non-zero selects a block.
+            block_indices: instead of ``block_mask``, ``[B, Hq, K]`` integer lists of the
+                selected block indices per head, ``-1`` marking empty slots (converted on
+                the GPU by ``tasft_mask_from_indices``; duplicates are harmless).
             kv_lens: optional ``[B]`` int32 valid lengths (default ``S_kv``).
             num_splits: split-K factor (default: sized so the launch fills the GPU).
 
@@ -308,6 +312,17 @@ class BlockSparseFlashAttention:
         B, H, _, D = q.shape
         Hkv, S_kv = k_cache.shape[1], k_cache.shape[2]
         nb = math.ceil(S_kv / self.block_size)
+        if (block_mask is None) == (block_indices is None):
+            raise KernelError("Pass exactly one of block_mask and block_indices",
+                              context={"block_mask": block_mask is not None,
+                                       "block_indices": block_indices is not None})
+        if block_indices is not None:
+            if block_indices.ndim != 3 or tuple(block_indices.shape[:2]) != (B, H):
+                raise KernelError(
+                    f"block_indices must have shape [{B}, {H}, K], got {tuple(block_indices.shape)}",
+                    context={"expected": [B, H, -1], "got": list(block_indices.shape)},
+                )
+            block_mask = indices_to_mask(block_indices.to(q.device), nb).view(B, H, 1, nb)
         if tuple(block_mask.shape) != (B, H, 1, nb):
             raise KernelError(
                 f"block_mask shape mismatch: expected {(B, H, 1, nb)}, got {tuple(block_mask.shape)}",
@@ -370,6 +385,64 @@ class BlockSparseFlashAttention:
         return 1.0 / max(1e-6, denominator)
 
 
+def indices_to_mask(block_indices: torch.Tensor, num_blocks: int) -> torch.Tensor:
+    """Padded block-index lists ``[..., K]`` (``-1`` = empty) -> bool mask ``[..., num_blocks]``.
+
+    Runs ``tasft_mask_from_indices`` on the device; an index outside ``[0, num_blocks)``
+    other than ``-1`` raises ``KernelError`` (this reads one device flag).
+    """
+    if not block_indices.is_cuda:
+        raise KernelError("Tensors must be on CUDA device", context={"device": str(block_indices.device)})
+    if block_indices.dtype not in (torch.int32, torch.int64, torch.int16, torch.uint8):
+        raise KernelError(f"block indices must be integers, got {block_indices.dtype}",
+                          context={"dtype": str(block_indices.dtype)})
+    lead = tuple(block_indices.shape[:-1])
+    k = block_indices.shape[-1]
+    idx = block_indices.reshape(-1, k).to(torch.int32).contiguous()
+    rows = idx.shape[0]
+    mask = torch.empty((rows, num_blocks), dtype=torch.uint8, device=block_indices.device)
+    flag = torch.empty((1,), dtype=torch.int32, device=block_indices.device)
+    lib = _native.load_library()
+    status = lib.tasft_mask_from_indices(idx.data_ptr(), rows, k, k, num_blocks, mask.data_ptr(),
+                                         flag.data_ptr(), _native.stream_handle(idx.device))
+    _native.check(status, "tasft_mask_from_indices", {"rows": rows, "k": k})
+    if int(flag.item()) != 0:
+        raise KernelError(f"block index outside [0, {num_blocks}) (other than -1)",
+                          context={"num_blocks": num_blocks})
+    return mask.view(torch.bool).view(*lead, num_blocks)
+
+
+def mask_to_csr(block_mask: torch.Tensor, causal: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense block mask ``[B, H, NBq, NBk]`` -> CSR ``(row_ptr [B*H*NBq + 1], col_idx [nnz])``.
+
+    Rows are ``(b, h, query block)`` in row-major order; column indices ascend within a
+    row. With ``causal`` only the lower block triangle counts (the kernel-side AND of the
+    reference, ``block_sparse_fa.py:502-508``). Runs ``tasft_mask_compact`` on the device
+    and reads the total once to trim ``col_idx``.
+    """
+    if block_mask.ndim != _EXPECTED_TENSOR_NDIM:
+        raise KernelError(f"Expected a 4D block mask, got {block_mask.ndim}D",
+                          context={"shape": list(block_mask.shape)})
+    if not block_mask.is_cuda:
+        raise KernelError("Tensors must be on CUDA device", context={"device": str(block_mask.device)})
+    B, H, NBq, NBk = block_mask.shape
+    mask = _mask_bytes(block_mask)
+    rows = B * H * NBq
+    lib = _native.load_library()
+    ws_bytes = lib.tasft_mask_compact_workspace_bytes(B, H, NBq)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=mask.device)
+    row_ptr = torch.empty((rows + 1,), dtype=torch.int32, device=mask.device)
+    capacity = rows * (min(NBq, NBk) if causal else NBk)  # a row holds at most this many
+    col_idx = torch.empty((max(capacity, 1),), dtype=torch.int32, device=mask.device)
+    status = lib.tasft_mask_compact(mask.data_ptr(), B, H, NBq, NBk, _native.strides(mask),
+                                    1 if causal else 0, row_ptr.data_ptr(), col_idx.data_ptr(),
+                                    capacity, workspace.data_ptr(), ws_bytes,
+                                    _native.stream_handle(mask.device))
+    _native.check(status, "tasft_mask_compact", {"shape": [B, H, NBq, NBk]})
+    nnz = int(row_ptr[-1].item())
+    return row_ptr, col_idx[:nnz]
+
+
 def default_decode_splits(batch: int, num_kv_heads: int, num_blocks: int) -> int:
     """Split-K factor giving about 1024 decode workgroups (4 per CU on 256 CUs: each
     workgroup streams enough blocks to amortise its prologue), and at least the number
@@ -395,4 +468,6 @@ __all__ = [
     "default_decode_splits",
     "detect_kernels",
     "executed_blocks",
+    "indices_to_mask",
+    "mask_to_csr",
 ]

@@ -41,6 +41,8 @@ def test_abi_version_and_workspace_sizes():
     nb = 8192 // 64
     assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 128, 64, 128) == 4 * 40 * nb * 256 * 4 + 256
     assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 0, 64, 128) == 0
+    assert lib.tasft_mask_compact_workspace_bytes(4, 32, 128) == 4 * 32 * 128 * 4
+    assert lib.tasft_mask_compact_workspace_bytes(0, 32, 128) == 0
 
 
 def _i64(vals):
@@ -66,6 +68,10 @@ def test_invalid_arguments_return_errors_without_launch():
     rc = lib.tasft_bsfa_decode_fwd(fake, fake, fake, fake, fake, None, fake, 0, 1, 32, 8, 1024, 128,
                                    64, 4, st, st, st, st, st, 1.0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
+    rc = lib.tasft_mask_compact(fake, 1, 1, 4, 4, st, 0, fake, fake, 16, fake, 0, None)
+    assert rc == -4 and b"workspace" in lib.tasft_last_error()
+    rc = lib.tasft_mask_from_indices(fake, 4, 3, 2, 10, fake, fake, None)
+    assert rc == -1 and b"invalid sizes" in lib.tasft_last_error()
 
 
 def test_check_raises_kernel_error_with_message():

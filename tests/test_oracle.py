@@ -264,3 +264,29 @@ def test_gate_target_clamp_temperature_variant():
     got = orc.normalize_block_max(pooled, "flat", temperature=2.0, clamp=50.0)
     ref = torch.softmax(torch.tensor([50.0, -math.inf, 3.0, -50.0], dtype=torch.float64) / 2.0, 0)
     np.testing.assert_allclose(got.reshape(-1), ref.numpy(), rtol=1e-12)
+
+
+def test_mask_csr_literal_and_round_trip():
+    # Hand-checked: rows (b=0,h=0,qb=0..2) of a 3x4 mask.
+    mask = np.array([[[[1, 0, 1, 0], [0, 0, 0, 0], [1, 1, 0, 1]]]], dtype=np.uint8)
+    rp, ci = orc.mask_to_csr(mask)
+    assert rp.tolist() == [0, 2, 2, 5]
+    assert ci.tolist() == [0, 2, 0, 1, 3]
+    rp_c, ci_c = orc.mask_to_csr(mask, causal=True)  # keeps kb <= qb
+    assert rp_c.tolist() == [0, 1, 1, 3]
+    assert ci_c.tolist() == [0, 0, 1]
+    rng = np.random.default_rng(5)
+    m = rng.random((2, 3, 7, 9)) < 0.3
+    rp, ci = orc.mask_to_csr(m)
+    back = np.zeros((2 * 3 * 7, 9), dtype=bool)
+    for r in range(back.shape[0]):
+        back[r, ci[rp[r]:rp[r + 1]]] = True
+    assert np.array_equal(back.reshape(m.shape), m)
+
+
+def test_indices_to_mask_literal():
+    idx = np.array([[[3, -1, 0, 3]], [[-1, -1, -1, -1]]], dtype=np.int32)  # [2, 1, 4]
+    m = orc.indices_to_mask(idx, 5)
+    assert m.shape == (2, 1, 5)
+    assert m[0, 0].tolist() == [True, False, False, True, False]
+    assert not m[1].any()
