@@ -26,6 +26,12 @@ struct GateTargetParams {
   int causal;
 };
 
+
+// One 16-byte-per-lane DMA (buffer_load ... lds) of 1 KB into LDS at `dst`.
+__device__ __forceinline__ void gt_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TASFT_LDS void*)dst, 16, voff, 0, 0, 0);
+}
+
 template <int BS, int D>
 __global__ void __launch_bounds__(BS / 32 * kWave)
 gate_target_blockmax_kernel(const GateTargetParams p) {
@@ -153,6 +159,152 @@ gate_target_normalize_kernel(float* data, int64_t group_len, float inv_temp, flo
   for (int64_t i = tid; i < group_len; i += 256) x[i] = expf(xform(x[i]) - mx) * inv;
 }
 
+
+// Block size 64: four waves per (batch, query head, query block); wave w takes query rows
+// 32*(w&1).. and the key half 32*(w>>1).. of every causal key block. K tiles are copied
+// HBM -> LDS by buffer_load_dwordx4 ... lds (16-byte XOR swizzle, rows past S arrive as
+// zeros) into two stages, one barrier per block. Each wave reduces its 32 x 32 sub-tile to
+// one maximum with DPP / permlane swaps (no LDS round trips); the four partial maxima of a
+// block are combined one block later from a double-buffered LDS slot.
+template <int D>
+__device__ __forceinline__ int gt_swz(int r, int cc) {
+  return cc ^ (D == 128 ? (r & 15) : ((r >> 1) & 7));
+}
+
+template <int D>
+__global__ void __launch_bounds__(256)
+gate_target_bs64_kernel(const GateTargetParams p) {
+  constexpr int BS = 64;
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROWB = D * 2;
+  constexpr int TILE = BS * ROWB;
+  constexpr int UNITS_PER_WAVE = (TILE / 1024) / 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t kA[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t kB[TILE];
+  __shared__ float red[2][4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rh = wave & 1, kh = wave >> 1;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // Item order: each XCD walks one KV group at a time, longest causal rows first.
+  const int64_t idx = blockIdx.x;
+  const int64_t groups = (int64_t)p.B * p.Hkv;
+  const int64_t per_group = (int64_t)p.G * p.NB;
+  int64_t grp, r;
+  if ((groups & 7) == 0) {
+    const int64_t j = idx >> 3;
+    grp = (idx & 7) + 8 * (j / per_group);
+    r = j % per_group;
+  } else {
+    grp = idx / per_group;
+    r = idx % per_group;
+  }
+  const int qslot = (int)(r / p.G);
+  const int qb = p.causal ? (p.NB - 1 - qslot) : qslot;
+  const int b = (int)(grp / p.Hkv);
+  const int kvh = (int)(grp % p.Hkv);
+  const int h = kvh * p.G + (int)(r % p.G);
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NB + qb) * p.NB;
+
+  const int qrow = qb * BS + rh * 32 + col;
+  const bool qvalid = qrow < p.S;
+  bf16x8_t qf[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    u32x4_t val = {0u, 0u, 0u, 0u};
+    if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
+    qf[ks] = as_bf16x8(val);
+  }
+  int koff[UNITS_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < UNITS_PER_WAVE; ++i) {
+    const int byte = (wave * UNITS_PER_WAVE + i) * 1024 + lane * 16;
+    const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+    koff[i] = (row * (int)p.sk[2] + gt_swz<D>(row, pos) * 8) * 2;
+  }
+  auto issue = [&](uint8_t* kt, int kb) {
+    const int key0 = kb * BS;
+    const int64_t rows_left = (int64_t)(p.S - key0);
+    const int64_t bytes = rows_left * p.sk[2] * 2;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kbase + (int64_t)key0 * p.sk[2]), (short)0,
+        bytes > 0x7fffffff ? 0x7fffffff : (int)bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < UNITS_PER_WAVE; ++i)
+      gt_dma16(rs, kt + (wave * UNITS_PER_WAVE + i) * 1024, koff[i]);
+  };
+  const int krow_l = kh * 32 + col;
+  // One block from stage kt: this wave's 32 x 32 sub-tile maximum (raw scores).
+  auto block_max = [&](const uint8_t* kt, int kb) {
+    f32x16_t s = (f32x16_t){};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cc = ks * 2 + half;
+      const u32x4_t a = *(const u32x4_t*)(kt + krow_l * ROWB + gt_swz<D>(krow_l, cc) * 16);
+      s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
+    }
+    const int key0 = kb * BS;
+    if ((p.causal && kb == qb) || (key0 + BS > p.S) || qb * BS + BS > p.S) {
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int key = key0 + kh * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+        s[rr] = (!qvalid || key >= p.S || (p.causal && key > qrow)) ? -INFINITY : s[rr];
+      }
+    }
+    float m4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      m4[j] = fmaxf(fmaxf(s[4 * j], s[4 * j + 1]), fmaxf(s[4 * j + 2], s[4 * j + 3]));
+    return wave_max_dpp(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+  };
+  // Combine the four partial maxima of block kb (slot kb & 1) and store it, scaled.
+  auto store = [&](int kb) {
+    if (tid == 0) {
+      const float* rm = red[kb & 1];
+      orow[kb] = fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3])) * p.scale;
+    }
+  };
+
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  for (int kb = kb_end + tid; kb < p.NB; kb += 256) orow[kb] = -INFINITY;
+  if (kb_end > 0) issue(kA, 0);
+  for (int kb = 0; kb < kb_end; kb += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's DMA of block kb landed
+    __syncthreads();                      // every wave's; stage B free; red[(kb-1)&1] final
+    if (kb > 0) store(kb - 1);
+    if (kb + 1 < kb_end) issue(kB, kb + 1);
+    {
+      const float m = block_max(kA, kb);
+      if (lane == 0) red[kb & 1][wave] = m;
+    }
+    if (kb + 1 >= kb_end) break;
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    store(kb);
+    if (kb + 2 < kb_end) issue(kA, kb + 2);
+    {
+      const float m = block_max(kB, kb + 1);
+      if (lane == 0) red[(kb + 1) & 1][wave] = m;
+    }
+  }
+  __syncthreads();
+  if (kb_end > 0) store(kb_end - 1);
+}
+
+template <int D>
+static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t stream) {
+  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
+  hipLaunchKernelGGL((gate_target_bs64_kernel<D>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <int BS, int D>
 static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
@@ -220,8 +372,8 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, float* target
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_blockmax<64, 128>(p, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_blockmax<64, 64>(p, s);
+  if (block_size == 64 && head_dim == 128) err = launch_blockmax_bs64<128>(p, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_blockmax_bs64<64>(p, s);
   else if (block_size == 32 && head_dim == 128) err = launch_blockmax<32, 128>(p, s);
   else if (block_size == 32 && head_dim == 64) err = launch_blockmax<32, 64>(p, s);
   else if (block_size == 128 && head_dim == 128) err = launch_blockmax<128, 128>(p, s);
