@@ -160,40 +160,46 @@ gate_target_normalize_kernel(float* data, int64_t group_len, float inv_temp, flo
 }
 
 
-// Block size 64: four waves per (batch, query head, query block); wave w takes query rows
-// 32*(w&1).. and the key half 32*(w>>1).. of every causal key block. K tiles are copied
-// HBM -> LDS by buffer_load_dwordx4 ... lds (16-byte XOR swizzle, rows past S arrive as
-// zeros) into two stages, one barrier per block. Each wave reduces its 32 x 32 sub-tile to
-// one maximum with DPP / permlane swaps (no LDS round trips); the four partial maxima of a
-// block are combined one block later from a double-buffered LDS slot.
+// Block size 64. A workgroup owns one query block of HPW query heads of the same KV head
+// (the target is dense, so these heads read exactly the same K blocks) with four waves per
+// head: wave (hw, w) takes head hw, query rows 32*(w&1).. and the key half 32*(w>>1).. of
+// every causal key block. K tiles are copied HBM -> LDS once for all HPW heads by
+// buffer_load_dwordx4 ... lds (16-byte XOR swizzle, rows past S arrive as zeros) into two
+// stages, one barrier per block. Each wave reduces its 32 x 32 sub-tile to one maximum with
+// DPP / permlane swaps (no LDS round trips); the four partial maxima of a head's block are
+// combined one block later from a double-buffered LDS slot.
 template <int D>
 __device__ __forceinline__ int gt_swz(int r, int cc) {
   return cc ^ (D == 128 ? (r & 15) : ((r >> 1) & 7));
 }
 
-template <int D>
-__global__ void __launch_bounds__(256)
+template <int D, int HPW>
+__global__ void __launch_bounds__(HPW * 256)
 gate_target_bs64_kernel(const GateTargetParams p) {
   constexpr int BS = 64;
   constexpr int KSTEPS = D / 16;
   constexpr int ROWB = D * 2;
   constexpr int TILE = BS * ROWB;
-  constexpr int UNITS_PER_WAVE = (TILE / 1024) / 4;
+  constexpr int UNITS = TILE / 1024;  // 1 KB DMA units per tile
+  constexpr int NWAVES = 4 * HPW;
   __shared__ __attribute__((aligned(1024))) uint8_t kA[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t kB[TILE];
-  __shared__ float red[2][4];
+  __shared__ float red[2][HPW][4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int rh = wave & 1, kh = wave >> 1;
+  const int hw = wave >> 2;  // head within the workgroup
+  const int w4 = wave & 3;
+  const int rh = w4 & 1, kh = w4 >> 1;
   const int col = lane & 31;
   const int half = lane >> 5;
 
   // Item order: each XCD walks one KV group at a time, longest causal rows first.
+  const int chunks = p.G / HPW;
   const int64_t idx = blockIdx.x;
   const int64_t groups = (int64_t)p.B * p.Hkv;
-  const int64_t per_group = (int64_t)p.G * p.NB;
+  const int64_t per_group = (int64_t)chunks * p.NB;
   int64_t grp, r;
   if ((groups & 7) == 0) {
     const int64_t j = idx >> 3;
@@ -203,11 +209,11 @@ gate_target_bs64_kernel(const GateTargetParams p) {
     grp = idx / per_group;
     r = idx % per_group;
   }
-  const int qslot = (int)(r / p.G);
+  const int qslot = (int)(r / chunks);
   const int qb = p.causal ? (p.NB - 1 - qslot) : qslot;
   const int b = (int)(grp / p.Hkv);
   const int kvh = (int)(grp % p.Hkv);
-  const int h = kvh * p.G + (int)(r % p.G);
+  const int h = kvh * p.G + (int)(r % chunks) * HPW + hw;
 
   const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
@@ -222,12 +228,15 @@ gate_target_bs64_kernel(const GateTargetParams p) {
     if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
     qf[ks] = as_bf16x8(val);
   }
-  int koff[UNITS_PER_WAVE];
+  // DMA units of this wave: u = wave, wave + NWAVES, ...
+  constexpr int UPW = (UNITS + NWAVES - 1) / NWAVES;
+  int koff[UPW];
 #pragma unroll
-  for (int i = 0; i < UNITS_PER_WAVE; ++i) {
-    const int byte = (wave * UNITS_PER_WAVE + i) * 1024 + lane * 16;
+  for (int i = 0; i < UPW; ++i) {
+    const int u = wave + i * NWAVES;
+    const int byte = u * 1024 + lane * 16;
     const int row = byte / ROWB, pos = (byte % ROWB) / 16;
-    koff[i] = (row * (int)p.sk[2] + gt_swz<D>(row, pos) * 8) * 2;
+    koff[i] = u < UNITS ? (row * (int)p.sk[2] + gt_swz<D>(row, pos) * 8) * 2 : 0;
   }
   auto issue = [&](uint8_t* kt, int kb) {
     const int key0 = kb * BS;
@@ -237,8 +246,10 @@ gate_target_bs64_kernel(const GateTargetParams p) {
         (void*)(kbase + (int64_t)key0 * p.sk[2]), (short)0,
         bytes > 0x7fffffff ? 0x7fffffff : (int)bytes, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < UNITS_PER_WAVE; ++i)
-      gt_dma16(rs, kt + (wave * UNITS_PER_WAVE + i) * 1024, koff[i]);
+    for (int i = 0; i < UPW; ++i) {
+      const int u = wave + i * NWAVES;
+      if (UNITS % NWAVES == 0 || u < UNITS) gt_dma16(rs, kt + u * 1024, koff[i]);
+    }
   };
   const int krow_l = kh * 32 + col;
   // One block from stage kt: this wave's 32 x 32 sub-tile maximum (raw scores).
@@ -264,16 +275,16 @@ gate_target_bs64_kernel(const GateTargetParams p) {
       m4[j] = fmaxf(fmaxf(s[4 * j], s[4 * j + 1]), fmaxf(s[4 * j + 2], s[4 * j + 3]));
     return wave_max_dpp(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
   };
-  // Combine the four partial maxima of block kb (slot kb & 1) and store it, scaled.
+  // Combine the four partial maxima of this head's block kb (slot kb & 1), scaled.
   auto store = [&](int kb) {
-    if (tid == 0) {
-      const float* rm = red[kb & 1];
+    if ((tid & 255) == 0) {
+      const float* rm = red[kb & 1][hw];
       orow[kb] = fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3])) * p.scale;
     }
   };
 
   const int kb_end = p.causal ? qb + 1 : p.NB;
-  for (int kb = kb_end + tid; kb < p.NB; kb += 256) orow[kb] = -INFINITY;
+  for (int kb = kb_end + (tid & 255); kb < p.NB; kb += 256) orow[kb] = -INFINITY;
   if (kb_end > 0) issue(kA, 0);
   for (int kb = 0; kb < kb_end; kb += 2) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's DMA of block kb landed
@@ -282,7 +293,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
     if (kb + 1 < kb_end) issue(kB, kb + 1);
     {
       const float m = block_max(kA, kb);
-      if (lane == 0) red[kb & 1][wave] = m;
+      if (lane == 0) red[kb & 1][hw][w4] = m;
     }
     if (kb + 1 >= kb_end) break;
     __builtin_amdgcn_s_waitcnt(0x0f70);
@@ -291,7 +302,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
     if (kb + 2 < kb_end) issue(kA, kb + 2);
     {
       const float m = block_max(kB, kb + 1);
-      if (lane == 0) red[(kb + 1) & 1][wave] = m;
+      if (lane == 0) red[(kb + 1) & 1][hw][w4] = m;
     }
   }
   __syncthreads();
@@ -300,8 +311,14 @@ gate_target_bs64_kernel(const GateTargetParams p) {
 
 template <int D>
 static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t stream) {
-  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
-  hipLaunchKernelGGL((gate_target_bs64_kernel<D>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  const int hpw = (p.G % 4 == 0) ? 4 : (p.G % 2 == 0 ? 2 : 1);
+  const int64_t grid = (int64_t)p.NB * p.B * p.Hq / hpw;
+  if (hpw == 4)
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
+  else if (hpw == 2)
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2>), dim3((unsigned)grid), dim3(512), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -30,6 +30,8 @@ CASES = [
     (2, 8, 2, 1000, 128, 64, True),   # GQA, ragged
     (1, 4, 1, 300, 64, 32, False),    # non-causal, D=64
     (1, 2, 2, 384, 128, 128, True),   # bs=128
+    (2, 4, 2, 640, 64, 64, True),     # two query heads per KV head share the K tiles, D=64
+    (1, 3, 3, 200, 128, 64, False),   # one head per workgroup, non-causal, ragged
 ]
 
 
