@@ -52,24 +52,26 @@ struct PrefillItem {
   int b, kvh, h, qb;
 };
 
-__device__ __forceinline__ PrefillItem prefill_item(const PrefillParams& p, int64_t idx) {
-  const int64_t groups = (int64_t)p.B * p.Hkv;
-  const int64_t per_group = (int64_t)p.G * p.NB;
-  int64_t grp, r;
+__device__ __forceinline__ PrefillItem prefill_item(const PrefillParams& p, int64_t idx64) {
+  // 32-bit arithmetic: the host rejects B * Hq * NB >= 2^31.
+  const uint32_t idx = (uint32_t)idx64;
+  const uint32_t groups = (uint32_t)(p.B * p.Hkv);
+  const uint32_t per_group = (uint32_t)(p.G * p.NB);
+  uint32_t grp, r;
   if ((groups & 7) == 0) {
-    const int64_t j = idx >> 3;
+    const uint32_t j = idx >> 3;
     grp = (idx & 7) + 8 * (j / per_group);
     r = j % per_group;
   } else {
     grp = idx / per_group;
     r = idx % per_group;
   }
-  const int qslot = (int)(r / p.G);
+  const int qslot = (int)(r / (uint32_t)p.G);
   PrefillItem it;
   it.qb = p.causal ? (p.NB - 1 - qslot) : qslot;
-  it.b = (int)(grp / p.Hkv);
-  it.kvh = (int)(grp % p.Hkv);
-  it.h = it.kvh * p.G + (int)(r % p.G);
+  it.b = (int)(grp / (uint32_t)p.Hkv);
+  it.kvh = (int)(grp % (uint32_t)p.Hkv);
+  it.h = it.kvh * p.G + (int)(r % (uint32_t)p.G);
   return it;
 }
 
@@ -400,11 +402,14 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const int part = persistent ? (int)(blockIdx.x % p.parts) : 0;
   const int64_t per_part = persistent ? (int64_t)p.B * p.Hq * p.NB / p.parts : 1;
   int64_t slot = persistent ? (int64_t)(blockIdx.x / p.parts) : 0;
+  // A workgroup knows its next item one item ahead: the second is static (slot +
+  // wg_per_part), later ones come from tickets. The next item's first 64 mask bytes are
+  // loaded during this item, so its first K/V DMA starts without a mask round trip.
+  int64_t slot_nx = persistent ? slot + p.wg_per_part : per_part;
+  bool pre = false;   // mbyte holds the first 64 mask bytes of this item's row
+  uint8_t mbyte = 0;
   while (slot < per_part) {
   const int64_t idx = !persistent ? (int64_t)blockIdx.x : (p.parts == 8 ? part + 8 * slot : slot);
-  // The next ticket is fetched now; its latency hides behind this item.
-  int ticket = 0;
-  if (persistent && tid == 0) ticket = atomicAdd(&p.queue[part], 1);
   const PrefillItem item = prefill_item(p, idx);
   const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
 
@@ -416,13 +421,32 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 
   const int qrow = qb * BS + rh * 32 + col;
   const bool qvalid = qrow < p.S;
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  // Loads go out in the order their results are needed (returns are in order): this
+  // row's mask bytes (unless the previous item fetched them), Q, the next item's mask
+  // bytes, then the ticket of the item after the next.
+  uint8_t mb = mbyte;
+  if (!pre && lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
   bf16x8_t qf[KSTEPS];
+  {
+    // Rows past the end read row S-1: per-row results, never stored.
+    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : p.S - 1) * p.sq[2] + half * 8;
 #pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks) {
-    u32x4_t val = {0u, 0u, 0u, 0u};
-    if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
-    qf[ks] = as_bf16x8(val);
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
   }
+  mbyte = 0;
+  pre = slot_nx < per_part;
+  if (pre) {
+    const int64_t idx_nx = p.parts == 8 ? part + 8 * slot_nx : slot_nx;
+    const PrefillItem nx = prefill_item(p, idx_nx);
+    const int kb_end_nx = p.causal ? nx.qb + 1 : p.NB;
+    const uint8_t* mrow_nx = p.mask + nx.b * p.sm[0] + nx.h * p.sm[1] + (int64_t)nx.qb * p.sm[2];
+    if (lane < kb_end_nx) mbyte = mrow_nx[(int64_t)lane * p.sm[3]];
+  }
+  // atomicInc (not atomicAdd, which the compiler rewrites into a wave-aggregated form that
+  // waits for the result on the spot); the counter never reaches the wrap limit.
+  int ticket = 0;
+  if (persistent && tid == 0) ticket = (int)atomicInc((unsigned*)&p.queue[part], 0xffffffffu);
 
   // Start the DMA of key block kb into one stage (rows >= S arrive as zeros). With
   // small spans the resource base and size take 32-bit scalar math only.
@@ -452,12 +476,36 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 
   // One key block from stage (kt, vt): S^T MFMAs, online softmax, PV MFMAs.
   auto compute = [&](const uint8_t* kt, const uint8_t* vt, int kb) {
-    f32x16_t s = (f32x16_t){};
+    // Every LDS operand of the block is requested before the first MFMA: the K fragments,
+    // then (behind a scheduling fence) the V^T fragments, whose reads the S MFMAs cover.
+    u32x4_t kf[KSTEPS];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cc = ks * 2 + half;
-      const u32x4_t a = *(const u32x4_t*)(kt + krow_l * ROWB + swz_k<D>(krow_l, cc) * 16);
-      s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
+      kf[ks] = *(const u32x4_t*)(kt + krow_l * ROWB + swz_k<D>(krow_l, cc) * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x2_t vlo[2][DTILES], vhi[2][DTILES];
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const int kbase_k = kh * 32 + 16 * pp + 4 * (grp16 >> 1);  // first key of run 1
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+        const int d0 = dt * 32 + 16 * (grp16 & 1) + 4 * tr_cb;  // source column of this lane
+        const int cc = d0 >> 3, sub = (d0 & 7) * 2;
+        const int r1 = kbase_k + tr_row, r2 = r1 + 8;
+        vlo[pp][dt] = ds_read_tr16_b64((const void*)(vt + r1 * ROWB + swz_v<D>(r1, cc) * 16 + sub));
+        vhi[pp][dt] = ds_read_tr16_b64((const void*)(vt + r2 * ROWB + swz_v<D>(r2, cc) * 16 + sub));
+      }
+    }
+    f32x16_t s = (f32x16_t){};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) s = mfma_32x32x16_bf16(as_bf16x8(kf[ks]), qf[ks], s);
+    // Each S MFMA followed by two V^T reads.
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     const int key0 = kb * BS;
     // Causal diagonal block or partial last block: mask in one uniform branch.
@@ -500,23 +548,16 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
                          pack_bf16x2(s[8 * pp + 4], s[8 * pp + 5]),
                          pack_bf16x2(s[8 * pp + 6], s[8 * pp + 7])};
       const bf16x8_t pb = as_bf16x8(w);
-      const int kbase_k = kh * 32 + 16 * pp + 4 * (grp16 >> 1);  // first key of run 1
 #pragma unroll
       for (int dt = 0; dt < DTILES; ++dt) {
-        const int d0 = dt * 32 + 16 * (grp16 & 1) + 4 * tr_cb;  // source column of this lane
-        const int cc = d0 >> 3, sub = (d0 & 7) * 2;
-        const int r1 = kbase_k + tr_row, r2 = r1 + 8;
-        const u32x2_t lo = ds_read_tr16_b64((const void*)(vt + r1 * ROWB + swz_v<D>(r1, cc) * 16 + sub));
-        const u32x2_t hi = ds_read_tr16_b64((const void*)(vt + r2 * ROWB + swz_v<D>(r2, cc) * 16 + sub));
-        const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
+        const u32x4_t a = {vlo[pp][dt][0], vlo[pp][dt][1], vhi[pp][dt][0], vhi[pp][dt][1]};
         oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb, oacc[dt]);
       }
     }
   };
 
-  const int kb_end = p.causal ? qb + 1 : p.NB;
-  int chunk = -kWave;
-  uint64_t bits = 0;
+  int chunk = 0;
+  uint64_t bits = __ballot(mb != 0);
   int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
   if (kb >= 0) issue(kA, vA, kb);
   // Unrolled by two so each stage is a fixed LDS object.
@@ -580,9 +621,10 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     }
   }
   if (!persistent) break;
-  if (tid == 0) next_slot = p.wg_per_part + ticket;
+  if (tid == 0) next_slot = 2 * p.wg_per_part + ticket;
   __syncthreads();  // merge buffer, stages and next_slot are free for the next item
-  slot = next_slot;
+  slot = slot_nx;
+  slot_nx = __builtin_amdgcn_readfirstlane(next_slot);
   }
 }
 
