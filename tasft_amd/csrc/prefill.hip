@@ -377,7 +377,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar DMA addresses
   const int rh = wave & 1;   // row half
   const int kh = wave >> 1;  // key half
   const int col = lane & 31;
@@ -422,9 +422,10 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const int qrow = qb * BS + rh * 32 + col;
   const bool qvalid = qrow < p.S;
   const int kb_end = p.causal ? qb + 1 : p.NB;
-  // Loads go out in the order their results are needed (returns are in order): this
-  // row's mask bytes (unless the previous item fetched them), Q, the next item's mask
-  // bytes, then the ticket of the item after the next.
+  // Loads go out in the order their results are needed, since waits are in issue order:
+  // this row's mask bytes (unless the previous item fetched them) and Q; the first K/V
+  // DMA follows once the mask bytes are in, and only then the next item's mask bytes and
+  // the ticket of the item after the next, which the first wait also covers.
   uint8_t mb = mbyte;
   if (!pre && lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
   bf16x8_t qf[KSTEPS];
@@ -434,20 +435,6 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
   }
-  mbyte = 0;
-  pre = slot_nx < per_part;
-  if (pre) {
-    const int64_t idx_nx = p.parts == 8 ? part + 8 * slot_nx : slot_nx;
-    const PrefillItem nx = prefill_item(p, idx_nx);
-    const int kb_end_nx = p.causal ? nx.qb + 1 : p.NB;
-    const uint8_t* mrow_nx = p.mask + nx.b * p.sm[0] + nx.h * p.sm[1] + (int64_t)nx.qb * p.sm[2];
-    if (lane < kb_end_nx) mbyte = mrow_nx[(int64_t)lane * p.sm[3]];
-  }
-  // atomicInc (not atomicAdd, which the compiler rewrites into a wave-aggregated form that
-  // waits for the result on the spot); the counter never reaches the wrap limit.
-  int ticket = 0;
-  if (persistent && tid == 0) ticket = (int)atomicInc((unsigned*)&p.queue[part], 0xffffffffu);
-
   // Start the DMA of key block kb into one stage (rows >= S arrive as zeros). With
   // small spans the resource base and size take 32-bit scalar math only.
   const uint32_t krb = (uint32_t)p.sk[2] * 2u, vrb = (uint32_t)p.sv[2] * 2u;
@@ -560,6 +547,19 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   uint64_t bits = __ballot(mb != 0);
   int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
   if (kb >= 0) issue(kA, vA, kb);
+  mbyte = 0;
+  pre = slot_nx < per_part;
+  if (pre) {
+    const int64_t idx_nx = p.parts == 8 ? part + 8 * slot_nx : slot_nx;
+    const PrefillItem nx = prefill_item(p, idx_nx);
+    const int kb_end_nx = p.causal ? nx.qb + 1 : p.NB;
+    const uint8_t* mrow_nx = p.mask + nx.b * p.sm[0] + nx.h * p.sm[1] + (int64_t)nx.qb * p.sm[2];
+    if (lane < kb_end_nx) mbyte = mrow_nx[(int64_t)lane * p.sm[3]];
+  }
+  // atomicInc (not atomicAdd, which the compiler rewrites into a wave-aggregated form that
+  // waits for the result on the spot); the counter never reaches the wrap limit.
+  int ticket = 0;
+  if (persistent && tid == 0) ticket = (int)atomicInc((unsigned*)&p.queue[part], 0xffffffffu);
   // Unrolled by two so each stage is a fixed LDS object.
   while (kb >= 0) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's DMA of block kb landed
