@@ -21,6 +21,7 @@
 // with no shuffle. K (row major) and V^T (transposed while staging) go through LDS
 // rows padded so the MFMA operand reads are bank-conflict free on the 64-bank LDS.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -371,7 +372,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t vA[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t kB[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t vB[TILE];
-  __shared__ float xch_ml[2][2][kWave];
+  __shared__ float xch_ml[2][2][2][32];  // (m, l) by row half, key half
   __shared__ int next_slot;
   static_assert(DTILES * 16 * kWave * 4 == TILE, "merge buffer size");
 
@@ -406,11 +407,12 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   // wg_per_part), later ones come from tickets. The next item's first 64 mask bytes are
   // loaded during this item, so its first K/V DMA starts without a mask round trip.
   int64_t slot_nx = persistent ? slot + p.wg_per_part : per_part;
-  bool pre = false;   // mbyte holds the first 64 mask bytes of this item's row
+  bool pre = false;   // mbyte holds the first 64 mask bytes of this item's row, item_nx its item
   uint8_t mbyte = 0;
+  PrefillItem item_nx = {0, 0, 0, 0};
   while (slot < per_part) {
   const int64_t idx = !persistent ? (int64_t)blockIdx.x : (p.parts == 8 ? part + 8 * slot : slot);
-  const PrefillItem item = prefill_item(p, idx);
+  const PrefillItem item = pre ? item_nx : prefill_item(p, idx);
   const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
 
   const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
@@ -550,10 +552,10 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   mbyte = 0;
   pre = slot_nx < per_part;
   if (pre) {
-    const int64_t idx_nx = p.parts == 8 ? part + 8 * slot_nx : slot_nx;
-    const PrefillItem nx = prefill_item(p, idx_nx);
-    const int kb_end_nx = p.causal ? nx.qb + 1 : p.NB;
-    const uint8_t* mrow_nx = p.mask + nx.b * p.sm[0] + nx.h * p.sm[1] + (int64_t)nx.qb * p.sm[2];
+    item_nx = prefill_item(p, p.parts == 8 ? part + 8 * slot_nx : slot_nx);
+    const int kb_end_nx = p.causal ? item_nx.qb + 1 : p.NB;
+    const uint8_t* mrow_nx =
+        p.mask + item_nx.b * p.sm[0] + item_nx.h * p.sm[1] + (int64_t)item_nx.qb * p.sm[2];
     if (lane < kb_end_nx) mbyte = mrow_nx[(int64_t)lane * p.sm[3]];
   }
   // atomicInc (not atomicAdd, which the compiler rewrites into a wave-aggregated form that
@@ -577,41 +579,52 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     kb = kb_next;
   }
 
-  // Merge the two key halves of each row: waves 2,3 hand (m, l, O^T) to waves 0,1.
+  // Merge the two key halves of each row. Each wave finalises half of the head dims (key
+  // half 0 the first DTILES/2 tiles, key half 1 the rest) and hands its partner the other
+  // half of its partial O^T and its (m, l), through stage A.
+  constexpr int HT = DTILES / 2;
   const float l_tot = pair_sum32(l_run);
-  __syncthreads();
-  float* xo = (float*)(rh == 0 ? kA : vA);
-  if (kh == 1) {
+  __syncthreads();  // every wave is done with stage A
+  float* xo = (float*)(rh == 0 ? kA : vA);  // 2 x HT tiles of 16 x 64 floats per row half
+  auto send = [&](auto khc) {
+    constexpr int KH = decltype(khc)::value;
+    float* out = xo + KH * (HT * 16 * kWave);
+#pragma unroll
+    for (int j = 0; j < HT; ++j)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) out[(j * 16 + rr) * kWave + lane] = oacc[(1 - KH) * HT + j][rr];
     if (half == 0) {
-      xch_ml[rh][0][col] = m_ref;
-      xch_ml[rh][1][col] = l_tot;
+      xch_ml[rh][KH][0][col] = m_ref;
+      xch_ml[rh][KH][1][col] = l_tot;
     }
-#pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt)
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) xo[(dt * 16 + rr) * kWave + lane] = oacc[dt][rr];
-  }
-  __syncthreads();
-  if (kh == 0) {
-    const float m2 = xch_ml[rh][0][col];
-    const float l2 = xch_ml[rh][1][col];
-    const float M = fmaxf(m_ref, m2);
+  };
+  auto finish = [&](auto khc) {
+    constexpr int KH = decltype(khc)::value;
+    const float* in = xo + (1 - KH) * (HT * 16 * kWave);
+    const float mp = xch_ml[rh][1 - KH][0][col], lp = xch_ml[rh][1 - KH][1][col];
+    // The same expressions in both waves, in key-half order.
+    const float m0 = KH == 0 ? m_ref : mp, m1 = KH == 0 ? mp : m_ref;
+    const float l0 = KH == 0 ? l_tot : lp, l1 = KH == 0 ? lp : l_tot;
+    const float M = fmaxf(m0, m1);
     const float Mu = (M == -INFINITY) ? 0.f : M;
-    const float f1 = __builtin_amdgcn_exp2f(m_ref - Mu);  // 0 for an empty half
-    const float f2 = __builtin_amdgcn_exp2f(m2 - Mu);
-    const float L = l_tot * f1 + l2 * f2;
+    const float f0 = __builtin_amdgcn_exp2f(m0 - Mu);  // 0 for an empty half
+    const float f1 = __builtin_amdgcn_exp2f(m1 - Mu);
+    const float L = l0 * f0 + l1 * f1;
     const float inv = L > 0.f ? 1.f / L : 0.f;
     if (qvalid) {
       uint16_t* orow = obase + (int64_t)qrow * p.so[2];
 #pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) {
+      for (int j = 0; j < HT; ++j) {
+        const int dt = KH * HT + j;
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           float o4[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int rr = 4 * gq + e;
-            o4[e] = (oacc[dt][rr] * f1 + xo[(dt * 16 + rr) * kWave + lane] * f2) * inv;
+            const float mine = oacc[dt][rr], theirs = in[(j * 16 + rr) * kWave + lane];
+            const float p0 = KH == 0 ? mine : theirs, p1 = KH == 0 ? theirs : mine;
+            o4[e] = (p0 * f0 + p1 * f1) * inv;
           }
           const int d0 = dt * 32 + 8 * gq + 4 * half;
           const u32x2_t w = {pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
@@ -619,7 +632,16 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
         }
       }
     }
-  }
+  };
+  if (kh == 0)
+    send(std::integral_constant<int, 0>{});
+  else
+    send(std::integral_constant<int, 1>{});
+  __syncthreads();
+  if (kh == 0)
+    finish(std::integral_constant<int, 0>{});
+  else
+    finish(std::integral_constant<int, 1>{});
   if (!persistent) break;
   if (tid == 0) next_slot = 2 * p.wg_per_part + ticket;
   __syncthreads();  // merge buffer, stages and next_slot are free for the next item
