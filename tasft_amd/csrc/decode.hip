@@ -9,10 +9,12 @@
 // over the tokens < kv_len of the key blocks selected for query head h; a head with no
 // selected block outputs 0.
 //
-// Data path. A workgroup owns (batch b, KV head kvh, split s): the contiguous range of
-// key blocks [s*NB/P, (s+1)*NB/P). It reads the mask bytes of its range for the G query
-// heads of kvh in one round trip into LDS, then its 4 waves take the blocks selected by
-// any of those heads round-robin. Each selected KV block is read from HBM once per KV
+// Data path. A workgroup owns (batch b, KV head kvh, split s). For blocks of up to 64
+// keys the split is a share of the selected blocks: the blocks selected by any of the G
+// query heads of kvh are numbered in block order and split s takes entries
+// [s*n/P, (s+1)*n/P), so the splits of a row do equal work. (For 128-key blocks it is
+// the contiguous range of key blocks [s*NB/P, (s+1)*NB/P).) Its 4 waves take the
+// blocks round-robin. Each selected KV block is read from HBM once per KV
 // head, however many query heads chose it; all its K and V loads are issued together.
 // QK^T runs on MFMA (v_mfma_f32_32x32x16_bf16; K is loaded straight into the A-operand
 // layout, the G query heads are the N columns), PV on the VALU. Partial
@@ -24,7 +26,7 @@ namespace tasft {
 
 constexpr int kDecodeMaxG = 8;    // query heads per KV head handled by one workgroup
 constexpr int kDecodeWaves = 4;
-constexpr int kDecodeMaxRange = 256;  // key blocks per split (mask bytes staged in LDS)
+constexpr int kDecodeMaxRange = 1024;  // key blocks per split (mask bytes staged in LDS)
 
 struct DecodeParams {
   const uint16_t* q;
@@ -75,9 +77,9 @@ bsfa_decode_split_kernel(const DecodeParams p) {
 
   constexpr int VTILE = SUB * D * 2;  // bytes of one sub-block of V
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kDecodeWaves][VTILE];  // per-wave V tile
-  __shared__ uint8_t hb[kDecodeMaxRange];                     // head bits per block of the range
-  __shared__ uint16_t sel[kDecodeMaxRange];                   // selected blocks (range offsets)
-  __shared__ int nsel_lds;
+  __shared__ uint8_t hb[kDecodeMaxRange];  // head bits per block of the range / per entry
+  __shared__ int sel[kDecodeMaxRange];      // selected blocks (range offsets / block indices)
+  __shared__ int wsum[kDecodeWaves];
   __shared__ float p_lds[kDecodeWaves][SUB * MG + kWave];     // probabilities (+ dummy slots)
   __shared__ float a_lds[kDecodeWaves][MG];                   // rescale factor per head
   __shared__ float comb_ml[kDecodeWaves][MG][2];
@@ -102,14 +104,18 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   const int hi = min((int)(((int64_t)(s + 1) * p.NB) / p.P), nb_valid);
   const int range = max(hi - lo, 0);
 
-  // Mask bytes of the range for the group's heads, one round trip.
+  // Mask bits of key block t for the group's heads.
   const uint8_t* mbase = p.mask + b * p.sm[0] + (int64_t)h0 * p.sm[1];
-  for (int t = tid; t < range; t += kDecodeWaves * kWave) {
+  auto head_bits = [&](int t) -> uint32_t {
     uint32_t bitsv = 0;
 #pragma unroll
     for (int gg = 0; gg < MG; ++gg)
-      if (gg < G && mbase[(int64_t)gg * p.sm[1] + (int64_t)(lo + t) * p.sm[2]]) bitsv |= 1u << gg;
-    hb[t] = (uint8_t)bitsv;
+      if (gg < G && mbase[(int64_t)gg * p.sm[1] + (int64_t)t * p.sm[2]]) bitsv |= 1u << gg;
+    return bitsv;
+  };
+  if constexpr (NSUB != 1) {
+    // Mask bytes of the range for the group's heads, one round trip.
+    for (int t = tid; t < range; t += kDecodeWaves * kWave) hb[t] = (uint8_t)head_bits(lo + t);
   }
 
   // Q^T as the MFMA B operand: lane (col, half) holds head h0+col, head dims
@@ -158,24 +164,43 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     // the waves. Each wave keeps the next block's loads in flight: its K loads are issued
     // into the K registers as soon as the S MFMAs have read them, and its V DMA into the
     // wave's V tile as soon as the PV product has read it.
-    if (wave == 0) {
-      int base = 0;
-      for (int c0 = 0; c0 < range; c0 += kWave) {
-        const int t = c0 + lane;
-        const bool on = t < range && hb[t] != 0;
-        const uint64_t bits = __ballot(on);
-        if (on) sel[base + __popcll(bits & ((1ull << lane) - 1ull))] = (uint16_t)t;
-        base += __popcll(bits);
-      }
-      if (lane == 0) nsel_lds = base;
-    }
+    // Balanced splits: the blocks selected by any head of the group are numbered over
+    // the whole row in block order, and split s takes entries [s*n/P, (s+1)*n/P) (a
+    // range split would give the splits of one row unequal counts). Two passes over the
+    // row's mask bytes: count, then gather this split's (block, head bits) entries.
+    constexpr int NT = kDecodeWaves * kWave;
+    int cnt = 0;
+    for (int t = tid; t < nb_valid; t += NT) cnt += head_bits(t) != 0u ? 1 : 0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
+    if (lane == 0) wsum[wave] = cnt;
     __syncthreads();
+    const int n_all = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const int start = (int)(((int64_t)s * n_all) / p.P);
+    const int end = (int)(((int64_t)(s + 1) * n_all) / p.P);
+    __syncthreads();  // wsum is rewritten below
+    int base = 0;     // entries before this chunk (uniform)
+    for (int c0 = 0; c0 < nb_valid && base < end; c0 += NT) {
+      const int t = c0 + tid;
+      const uint32_t bv = t < nb_valid ? head_bits(t) : 0u;
+      const uint64_t bal = __ballot(bv != 0u);
+      if (lane == 0) wsum[wave] = __popcll(bal);
+      __syncthreads();
+      int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+      for (int w = 0; w < wave; ++w) pos += wsum[w];
+      if (bv != 0u && pos >= start && pos < end) {
+        sel[pos - start] = t;
+        hb[pos - start] = (uint8_t)bv;
+      }
+      base += (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+      __syncthreads();
+    }
     // Uniform values (scalar registers) keep the buffer resources scalar.
-    const int nsel = __builtin_amdgcn_readfirstlane(nsel_lds);
+    const int nsel = __builtin_amdgcn_readfirstlane(end - start);
     constexpr int NKL = KT * KSTEPS;  // K load instructions per block
     u32x4_t ka[KT][KSTEPS];
-    auto load_k = [&](int t_off) {
-      const int key0 = (lo + t_off) * BS;
+    auto load_k = [&](int kb) {
+      const int key0 = kb * BS;
       const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)SUB * ks2 * 2);
       if (key0 + SUB <= kv_len) {
 #pragma unroll
@@ -196,8 +221,8 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         }
       }
     };
-    auto dma_v = [&](int t_off) {
-      const int key0 = (lo + t_off) * BS;
+    auto dma_v = [&](int kb) {
+      const int key0 = kb * BS;
       // The resource ends at row kv_len-1, so rows past kv_len arrive as zeros.
       const __amdgpu_buffer_rsrc_t vr =
           decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(SUB, kv_len - key0) * vs2 * 2);
@@ -211,10 +236,9 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       dma_v(t0);
     }
     while (e < nsel) {
-      const int t_off = __builtin_amdgcn_readfirstlane((int)sel[e]);
-      const int kb = lo + t_off;
+      const int kb = __builtin_amdgcn_readfirstlane(sel[e]);
       const int key0 = kb * BS;
-      const uint32_t hsel = __builtin_amdgcn_readfirstlane((int)hb[t_off]);
+      const uint32_t hsel = __builtin_amdgcn_readfirstlane((int)hb[e]);
       const bool head_on = col < G && ((hsel >> col) & 1u);
       // S^T = K Q^T: rows = keys, cols = heads.
       f32x16_t sacc[KT];
@@ -452,11 +476,18 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       L += comb_ml[w][gg][1] * f;
       O += ((const float*)v_lds[w])[gg * D + d] * f;
     }
-    const int64_t row = ((int64_t)b * p.Hq + h0 + gg) * p.P + s;
-    p.ws_o[row * D + d] = O;
-    if (d == 0) {
-      p.ws_ml[row * 2 + 0] = M;
-      p.ws_ml[row * 2 + 1] = L;
+    if (p.P == 1) {
+      // One split: this is the whole row, written directly (no combine pass).
+      const float r = L > 0.f ? O / L : 0.f;
+      const __bf16 rb = (__bf16)r;
+      p.o[b * p.so[0] + (int64_t)(h0 + gg) * p.so[1] + d] = __builtin_bit_cast(uint16_t, rb);
+    } else {
+      const int64_t row = ((int64_t)b * p.Hq + h0 + gg) * p.P + s;
+      p.ws_o[row * D + d] = O;
+      if (d == 0) {
+        p.ws_ml[row * 2 + 0] = M;
+        p.ws_ml[row * 2 + 1] = L;
+      }
     }
   }
 }
@@ -491,7 +522,7 @@ static hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG>), dim3((unsigned)grid),
                      dim3(kDecodeWaves * kWave), 0, stream, p);
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
+  if (err != hipSuccess || p.P == 1) return err;
   hipLaunchKernelGGL((bsfa_decode_combine_kernel<D>), dim3((unsigned)((int64_t)p.B * p.Hq)), dim3(D),
                      0, stream, p);
   return hipGetLastError();

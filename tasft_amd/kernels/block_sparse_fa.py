@@ -444,12 +444,13 @@ def mask_to_csr(block_mask: torch.Tensor, causal: bool = False) -> tuple[torch.T
 
 
 def default_decode_splits(batch: int, num_kv_heads: int, num_blocks: int) -> int:
-    """Split-K factor giving about 1024 decode workgroups (4 per CU on 256 CUs: each
-    workgroup streams enough blocks to amortise its prologue), and at least the number
-    of splits that keeps every split within 256 key blocks."""
+    """Split-K factor giving about 512 decode workgroups: every workgroup is resident at
+    once (2 per CU on 256 CUs), each streams as many blocks as possible per prologue, and
+    one split per row needs no combine pass. At least the number of splits that keeps
+    every split within 1024 key blocks."""
     groups = max(1, batch * num_kv_heads)
-    want = min(max(1, num_blocks // 4), math.ceil(1024 / groups))
-    return int(max(1, want, math.ceil(num_blocks / 256)))
+    want = min(max(1, num_blocks // 4), math.ceil(512 / groups))
+    return int(max(1, want, math.ceil(num_blocks / 1024)))
 
 
 def executed_blocks(block_mask: torch.Tensor, causal: bool = True) -> torch.Tensor:

@@ -30,6 +30,8 @@ CASES = [
     (1, 8, 8, 300, 64, 32, 0.4, 64),        # D=64, bs=32, more splits than blocks
     (2, 8, 2, 1024, 128, 128, 0.5, None),   # bs=128
     (4, 32, 8, 4096, 128, 64, 0.1, None),   # config-3 grouping at a smaller cache
+    (1, 8, 2, 40000, 128, 64, 0.05, 1),     # 625 blocks in one split (no combine pass)
+    (2, 8, 2, 20000, 128, 64, 0.2, 2),      # splits share the selected blocks of a row
 ]
 
 
