@@ -424,6 +424,9 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const int qrow = qb * BS + rh * 32 + col;
   const bool qvalid = qrow < p.S;
   const int kb_end = p.causal ? qb + 1 : p.NB;
+  // Blocks from here on need element masks: the causal diagonal (the last block of a
+  // causal row, which is also the partial block if there is one) or the partial block.
+  const int mask_from = p.causal ? qb : ((p.S % BS) != 0 ? p.NB - 1 : p.NB);
   // Loads go out in the order their results are needed, since waits are in issue order:
   // this row's mask bytes (unless the previous item fetched them) and Q; the first K/V
   // DMA follows once the mask bytes are in, and only then the next item's mask bytes and
@@ -498,7 +501,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     }
     const int key0 = kb * BS;
     // Causal diagonal block or partial last block: mask in one uniform branch.
-    if ((p.causal && kb == qb) || (key0 + BS > p.S)) {
+    if (kb >= mask_from) {
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const int key = key0 + kh * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
