@@ -168,17 +168,21 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     // the whole row in block order, and split s takes entries [s*n/P, (s+1)*n/P) (a
     // range split would give the splits of one row unequal counts). Two passes over the
     // row's mask bytes: count, then gather this split's (block, head bits) entries.
+    // With one split the count pass is skipped: the split takes every entry.
     constexpr int NT = kDecodeWaves * kWave;
-    int cnt = 0;
-    for (int t = tid; t < nb_valid; t += NT) cnt += head_bits(t) != 0u ? 1 : 0;
+    int start = 0, end = 0x7fffffff;
+    if (p.P > 1) {
+      int cnt = 0;
+      for (int t = tid; t < nb_valid; t += NT) cnt += head_bits(t) != 0u ? 1 : 0;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
-    if (lane == 0) wsum[wave] = cnt;
-    __syncthreads();
-    const int n_all = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-    const int start = (int)(((int64_t)s * n_all) / p.P);
-    const int end = (int)(((int64_t)(s + 1) * n_all) / p.P);
-    __syncthreads();  // wsum is rewritten below
+      for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
+      if (lane == 0) wsum[wave] = cnt;
+      __syncthreads();
+      const int n_all = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+      start = (int)(((int64_t)s * n_all) / p.P);
+      end = (int)(((int64_t)(s + 1) * n_all) / p.P);
+      __syncthreads();  // wsum is rewritten below
+    }
     int base = 0;     // entries before this chunk (uniform)
     for (int c0 = 0; c0 < nb_valid && base < end; c0 += NT) {
       const int t = c0 + tid;
@@ -196,7 +200,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       __syncthreads();
     }
     // Uniform values (scalar registers) keep the buffer resources scalar.
-    const int nsel = __builtin_amdgcn_readfirstlane(end - start);
+    const int nsel = __builtin_amdgcn_readfirstlane(min(end, base) - start);
     constexpr int NKL = KT * KSTEPS;  // K load instructions per block
     u32x4_t ka[KT][KSTEPS];
     auto load_k = [&](int kb) {
