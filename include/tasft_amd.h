@@ -103,7 +103,8 @@ int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cach
                           const int64_t* o_strides, const int64_t* mask_strides, float scale,
                           void* stream);
 
-/* Bytes of workspace tasft_gate_fwd needs (pooled and projected block features). */
+/* Bytes of workspace tasft_gate_fwd needs (projected block features; head_dim is checked
+ * but does not change the size). */
 size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                   int64_t seq_len, int64_t head_dim, int64_t block_size,
                                   int64_t hidden);

@@ -11,9 +11,8 @@
 // per key block, so each pair costs hidden x (add, max, fma) instead of a 2D-wide GEMV.
 //
 // Pooling streams Q and K from HBM exactly once (GQA-native: K is pooled per KV head,
-// never expanded); for block size 64 and D in {64, 128} it is a pure streaming kernel
-// followed by an LDS-tiled fp32 projection GEMM, otherwise one fused pool + project
-// kernel. The pairwise kernel evaluates the MLP for the causal pairs in fp32, applies
+// never expanded) in one kernel that also projects the block means (a streaming variant
+// for block size 64 and D in {64, 128}, a generic one otherwise). The pairwise kernel evaluates the MLP for the causal pairs in fp32, applies
 // sigmoid, the causal zero and the per-head threshold, and writes soft scores (fp32),
 // optional logits, the uint8 hard mask and the active count. Flag bit 1 forces the
 // diagonal blocks on in the hard mask (soft scores unchanged).
@@ -34,8 +33,6 @@ struct GatePoolParams {
   const float* b_in;  // [hidden]
   float* uq;          // [B, Hq, NB, hidden]
   float* uk;          // [B, Hkv, NB, hidden]
-  float* pq;          // [B, Hq, NB, D] block means (fast path)
-  float* pk;          // [B, Hkv, NB, D]
   unsigned long long* counter;
   int64_t sq[3], sk[3];
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
@@ -113,14 +110,14 @@ gate_pool_project_kernel(const GatePoolParams p) {
 }
 
 
-// Fast path for block size 64 and D in {64, 128}: pooling and projection are two
-// kernels. gate_pool64_kernel is a pure stream: a workgroup pools kFastPB blocks of one
-// (batch, head), issuing every row load of all its blocks up front through a buffer
-// resource that ends at row S-1, so rows of a partial last block arrive as zeros, which
-// is exactly the reference's zero padding (the mean still divides by the block size).
-// The means go to an fp32 [rows, D] buffer that gate_project_kernel multiplies by the
-// W_in halves as an LDS-tiled fp32 GEMM (coalesced W_in reads, 16 outputs per thread).
-constexpr int kFastPB = 4;
+// Fast path for block size 64 and D in {64, 128}: one streaming kernel pools kFusePB
+// blocks of one (batch, head) and projects their means. Each group of 4 blocks issues
+// every row load up front through a buffer resource that ends at row S-1, so rows of a
+// partial last block arrive as zeros, which is exactly the reference's zero padding (the
+// mean still divides by the block size). The means stay in LDS; each thread then
+// computes one hidden unit for 8 of the blocks from one read of its W_in row (the W_in
+// halves are L2-resident), so the projection adds no HBM traffic and no launch.
+constexpr int kFusePB = 16;
 // Cache policy of the pooling loads: sc0 + nt (streamed: every byte of Q and K is read
 // once here), measured 5% faster than the default policy.
 constexpr int kStreamLoad = 3;
@@ -132,18 +129,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, in
 
 template <int D>
 __global__ void __launch_bounds__(256)
-gate_pool64_kernel(const GatePoolParams p) {
+gate_pool_proj64_kernel(const GatePoolParams p) {
   constexpr int BSZ = 64;
   constexpr int DOCT = D / 8;        // 16-byte chunks per row
   constexpr int RG = 256 / DOCT;     // row groups in the workgroup
   constexpr int RPT = BSZ / RG;      // rows per thread per block
   constexpr int WRG = kWave / DOCT;  // row groups per wave
+  constexpr int GB = 4;              // blocks per load group
   static_assert(WRG == 4 || WRG == 8, "row groups per wave");
-  __shared__ float red[4][kFastPB][D];
+  __shared__ __attribute__((aligned(16))) float red[4][kFusePB][D];  // per-wave sums, then means
 
   const int tid = threadIdx.x;
   if (blockIdx.x == 0 && tid == 0 && p.counter) *p.counter = 0ull;
-  const int chunks = (p.NB + kFastPB - 1) / kFastPB;
+  const int chunks = (p.NB + kFusePB - 1) / kFusePB;
   const int64_t nq = (int64_t)p.B * p.Hq * chunks;
   const bool is_q = blockIdx.x < nq;
   const int64_t local = is_q ? blockIdx.x : blockIdx.x - nq;
@@ -154,136 +152,86 @@ gate_pool64_kernel(const GatePoolParams p) {
   const int h = (int)(bh % heads);
   const uint16_t* src = is_q ? p.q + b * p.sq[0] + h * p.sq[1] : p.k + b * p.sk[0] + h * p.sk[1];
   const int srow = (int)(is_q ? p.sq[2] : p.sk[2]);
-  const int blk0 = chunk * kFastPB;
+  const int blk0 = chunk * kFusePB;
+  const int nblk = min(kFusePB, p.NB - blk0);
   const int row0 = blk0 * BSZ;
   const __amdgpu_buffer_rsrc_t r =
       gate_rsrc(src + (int64_t)row0 * srow, (int64_t)(p.S - row0) * srow * 2);
 
   const int dc = tid % DOCT, rg = tid / DOCT;
-  u32x4_t v[kFastPB][RPT];
-#pragma unroll
-  for (int bi = 0; bi < kFastPB; ++bi)
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int row = bi * BSZ + rg + RG * i;
-      v[bi][i] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (row * srow + dc * 8) * 2, 0, kStreamLoad));
-    }
   const int wave = tid / kWave;
+  for (int g = 0; g < nblk; g += GB) {
+    u32x4_t v[GB][RPT];
 #pragma unroll
-  for (int bi = 0; bi < kFastPB; ++bi) {
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int bi = 0; bi < GB; ++bi)
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      float f[8];
-      unpack_bf16x8(v[bi][i], f);
+      for (int i = 0; i < RPT; ++i) {
+        const int row = (g + bi) * BSZ + rg + RG * i;
+        v[bi][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   r, (row * srow + dc * 8) * 2, 0, kStreamLoad));
+      }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += f[j];
-    }
-    // Lanes l, l + DOCT, ... of a wave hold the same columns of different rows.
+    for (int bi = 0; bi < GB; ++bi) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float x = pair_sum32(acc[j]);
-      x += __shfl_xor(x, 16, 64);
-      if (WRG == 8) x += __shfl_xor(x, 8, 64);
-      acc[j] = x;
-    }
-    if ((tid % kWave) < DOCT) {
+      for (int i = 0; i < RPT; ++i) {
+        float f[8];
+        unpack_bf16x8(v[bi][i], f);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) red[wave][bi][dc * 8 + j] = acc[j];
+        for (int j = 0; j < 8; ++j) acc[j] += f[j];
+      }
+      // Lanes l, l + DOCT, ... of a wave hold the same columns of different rows.
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float x = pair_sum32(acc[j]);
+        x += __shfl_xor(x, 16, 64);
+        if (WRG == 8) x += __shfl_xor(x, 8, 64);
+        acc[j] = x;
+      }
+      if ((tid % kWave) < DOCT && g + bi < kFusePB) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[wave][g + bi][dc * 8 + j] = acc[j];
+      }
     }
   }
   __syncthreads();
-  const int nblk = min(kFastPB, p.NB - blk0);
-  float* dst = (is_q ? p.pq : p.pk) + (bh * p.NB + blk0) * (int64_t)D;
+  // Block means, in place in red[0] (each element is read and written by one thread).
   const float inv_bs = 1.f / (float)BSZ;
   for (int e = tid; e < nblk * D; e += 256) {
     const int bi = e / D, d = e % D;
-    dst[e] = ((red[0][bi][d] + red[1][bi][d]) + (red[2][bi][d] + red[3][bi][d])) * inv_bs;
+    red[0][bi][d] = ((red[0][bi][d] + red[1][bi][d]) + (red[2][bi][d] + red[3][bi][d])) * inv_bs;
   }
-}
+  __syncthreads();
 
-// u[row][c] = sum_d pooled[row][d] * W_in[c][off + d] (+ b_in[c] for query rows).
-// Workgroup: 64 rows x 64 hidden units, d staged 32 at a time (transposed in LDS);
-// thread (tr, tc) accumulates rows 4tr..4tr+3 x units 4tc..4tc+3.
-constexpr int kProjTile = 64;
-constexpr int kProjK = 32;
-constexpr int kProjLd = kProjTile + 4;
-
-__global__ void __launch_bounds__(256)
-gate_project_kernel(const GatePoolParams p) {
-  __shared__ __attribute__((aligned(16))) float a_t[kProjK][kProjLd];
-  __shared__ __attribute__((aligned(16))) float w_t[kProjK][kProjLd];
-  const int tid = threadIdx.x;
-  const int tr = tid / 16, tc = tid % 16;
-  const int64_t rq = (int64_t)p.B * p.Hq * p.NB, rk = (int64_t)p.B * p.Hkv * p.NB;
-  const int64_t qtiles = (rq + kProjTile - 1) / kProjTile;
-  const int col_tiles = (p.hidden + kProjTile - 1) / kProjTile;
-  const int64_t rt = blockIdx.x / col_tiles;
-  const int c0 = (int)(blockIdx.x % col_tiles) * kProjTile;
-  const bool is_q = rt < qtiles;
-  const int64_t r0 = (is_q ? rt : rt - qtiles) * kProjTile;
-  const int64_t rows = is_q ? rq : rk;
-  const float* src = is_q ? p.pq : p.pk;
-  float* dst = is_q ? p.uq : p.uk;
-  const int off = is_q ? 0 : p.D;
-
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-
-  // Staging: thread t loads 8 consecutive d of row / unit t / 4; the loads of the next
-  // d chunk are in flight while the current one is multiplied.
-  const int sr = tid / 4, sd = (tid % 4) * 8;
-  const int64_t arow = r0 + sr;
-  const int wc = c0 + sr;
-  const float* asrc = src + arow * p.D + sd;
-  const float* wsrc = p.w_in + (int64_t)wc * 2 * p.D + off + sd;
-  f32x4_t xa0 = {}, xa1 = {}, xw0 = {}, xw1 = {};
-  auto load = [&](int d0) {
-    if (arow < rows) {
-      xa0 = *(const f32x4_t*)(asrc + d0);
-      xa1 = *(const f32x4_t*)(asrc + d0 + 4);
-    }
-    if (wc < p.hidden) {
-      xw0 = *(const f32x4_t*)(wsrc + d0);
-      xw1 = *(const f32x4_t*)(wsrc + d0 + 4);
-    }
-  };
-  load(0);
-  for (int d0 = 0; d0 < p.D; d0 += kProjK) {
-    if (d0 > 0) __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a_t[sd + j][sr] = xa0[j];
-      a_t[sd + 4 + j][sr] = xa1[j];
-      w_t[sd + j][sr] = xw0[j];
-      w_t[sd + 4 + j][sr] = xw1[j];
-    }
-    __syncthreads();
-    if (d0 + kProjK < p.D) load(d0 + kProjK);
-#pragma unroll 8
-    for (int d = 0; d < kProjK; ++d) {
-      const f32x4_t av = *(const f32x4_t*)&a_t[d][4 * tr];
-      const f32x4_t wv = *(const f32x4_t*)&w_t[d][4 * tc];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], wv[j], acc[i][j]);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = c0 + 4 * tc + j;
+  // u[blk][c] = sum_d mean[blk][d] * W_in[c][off + d] (+ b_in[c] for query rows). Thread t
+  // takes unit c0 + t % 128 of blocks 8 * (t / 128) .. +7; the mean reads are broadcasts.
+  constexpr int HB = kFusePB / 2;
+  const int off = is_q ? 0 : D;
+  float* dst = (is_q ? p.uq : p.uk) + (bh * p.NB + blk0) * (int64_t)p.hidden;
+  const int bsel = (tid / 128) * HB, cl = tid % 128;
+  for (int c0 = 0; c0 < p.hidden; c0 += 128) {
+    const int c = c0 + cl;
     if (c >= p.hidden) continue;
+    const float* w = p.w_in + (int64_t)c * 2 * D + off;
+    float acc[HB];
+#pragma unroll
+    for (int k = 0; k < HB; ++k) acc[k] = 0.f;
+#pragma unroll 4
+    for (int d = 0; d < D; d += 4) {
+      const f32x4_t wv = *(const f32x4_t*)(w + d);
+#pragma unroll
+      for (int k = 0; k < HB; ++k) {
+        const f32x4_t m4 = *(const f32x4_t*)&red[0][bsel + k][d];
+        acc[k] = fmaf(m4[0], wv[0], acc[k]);
+        acc[k] = fmaf(m4[1], wv[1], acc[k]);
+        acc[k] = fmaf(m4[2], wv[2], acc[k]);
+        acc[k] = fmaf(m4[3], wv[3], acc[k]);
+      }
+    }
     const float bias = is_q ? p.b_in[c] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = r0 + 4 * tr + i;
-      if (row < rows) dst[row * p.hidden + c] = acc[i][j] + bias;
-    }
+    for (int k = 0; k < HB; ++k)
+      if (bsel + k < nblk) dst[(int64_t)(bsel + k) * p.hidden + c] = acc[k] + bias;
   }
 }
 
@@ -444,9 +392,8 @@ extern "C" size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads,
       block_size <= 0 || hidden <= 0)
     return 0;
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  // Projected units (hidden per block) and block means (head_dim per block), fp32.
-  return (size_t)(batch * (num_q_heads + num_kv_heads) * nb * (hidden + head_dim)) *
-             sizeof(float) + 256;
+  // Projected units, hidden fp32 values per query block and per key block.
+  return (size_t)(batch * (num_q_heads + num_kv_heads) * nb * hidden) * sizeof(float);
 }
 
 extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float* b_in,
@@ -494,10 +441,6 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   pp.b_in = b_in;
   pp.uq = (float*)workspace;
   pp.uk = pp.uq + batch * num_q_heads * nb * hidden;
-  // Block means start on a 256-byte boundary (16-byte vector loads); the slack is part of
-  // the workspace size.
-  pp.pq = (float*)workspace + ((batch * (num_q_heads + num_kv_heads) * nb * hidden + 63) & ~63LL);
-  pp.pk = pp.pq + batch * num_q_heads * nb * head_dim;
   pp.counter = active_count;
   for (int j = 0; j < 3; ++j) {
     pp.sq[j] = q_strides[j];
@@ -517,16 +460,12 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   const bool fast = block_size == 64 && (head_dim == 64 || head_dim == 128) &&
                     seq_len * std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
   if (fast) {
-    const int64_t fchunks = (nb + kFastPB - 1) / kFastPB;
+    const int64_t fchunks = (nb + kFusePB - 1) / kFusePB;
     const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * fchunks;
     if (head_dim == 128)
-      hipLaunchKernelGGL(gate_pool64_kernel<128>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+      hipLaunchKernelGGL(gate_pool_proj64_kernel<128>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
     else
-      hipLaunchKernelGGL(gate_pool64_kernel<64>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
-    const int64_t rq = batch * num_q_heads * nb, rk = batch * num_kv_heads * nb;
-    const int64_t gridp = ((rq + kProjTile - 1) / kProjTile + (rk + kProjTile - 1) / kProjTile) *
-                          ((hidden + kProjTile - 1) / kProjTile);
-    hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)gridp), dim3(256), 0, s, pp);
+      hipLaunchKernelGGL(gate_pool_proj64_kernel<64>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
   } else {
     const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * chunks;
     hipLaunchKernelGGL(gate_pool_project_kernel, dim3((unsigned)grid1), dim3(256), 0, s, pp);

@@ -39,7 +39,7 @@ def test_abi_version_and_workspace_sizes():
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
     assert lib.tasft_bsfa_decode_workspace_bytes(0, 32, 128, 4) == 0
     nb = 8192 // 64
-    assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 128, 64, 128) == 4 * 40 * nb * 256 * 4 + 256
+    assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 128, 64, 128) == 4 * 40 * nb * 128 * 4
     assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 0, 64, 128) == 0
     assert lib.tasft_mask_compact_workspace_bytes(4, 32, 128) == 4 * 32 * 128 * 4
     assert lib.tasft_mask_compact_workspace_bytes(0, 32, 128) == 0
