@@ -248,11 +248,15 @@ struct GatePairParams {
 };
 
 // Pairwise MLP: a workgroup evaluates a kPairTile x kPairTile tile of (query block,
-// key block) pairs of one (batch, head). The hidden units are staged kPairHid at a time
-// (transposed) and split over the four waves, 32 each; lane (tr, tc) of a wave
-// accumulates the 4 x 4 pairs rows 4tr.., cols 4tc.. (three LDS reads per 16 pairs and
-// hidden unit). The four partial sums meet in LDS; the epilogue applies sigmoid, the
-// causal zero and the threshold with coalesced stores.
+// key block) pairs of one (batch, head). With relu(x) = (x + |x|) / 2,
+//   logit[i][j] = sum_c w_c relu(u_ic + v_jc)
+//               = (A_i + B_j) / 2 + (sum_c w_c |u_ic + v_jc|) / 2,  A_i = sum_c w_c u_ic,
+// so each (pair, unit) costs one add and one fma with an |.| source modifier instead of
+// add, max and fma. The hidden units are staged kPairHid at a time (transposed) and
+// split over the four waves, 32 each; lane (tr, tc) of a wave accumulates the 4 x 4 pairs
+// rows 4tr.., cols 4tc.. (three LDS reads per 16 pairs and hidden unit). The four
+// partial sums meet in LDS; the epilogue applies sigmoid, the causal zero and the
+// threshold with coalesced stores.
 constexpr int kPairTile = 32;
 constexpr int kPairLd = kPairTile + 4;
 
@@ -262,6 +266,7 @@ gate_pairwise_kernel(const GatePairParams p) {
   // partial-sum tiles [4][kPairTile][kPairLd] (the same size).
   __shared__ __attribute__((aligned(16))) float lds[2 * kPairHid * kPairLd];
   __shared__ float wo[kPairHid];
+  __shared__ float ab[2][kPairTile];  // A_i of the tile's query rows, B_j of its key rows
   static_assert(2 * kPairHid >= 4 * kPairTile, "partial sums alias the staging tiles");
   __shared__ unsigned int wave_count[4];
   float* uq_t = lds;
@@ -290,6 +295,7 @@ gate_pairwise_kernel(const GatePairParams p) {
     for (int r = 0; r < 4; ++r)
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
+    float a_part = 0.f, b_part = 0.f;             // this thread's share of A_sr and B_sr
     constexpr int SU = kPairHid / 8;              // units staged per thread
     const int sr = tid / 8, su = (tid % 8) * SU;  // staging: row sr, units su..su+SU-1
     const bool vec = (p.hidden % 4) == 0;         // rows start 16-byte aligned
@@ -307,16 +313,24 @@ gate_pairwise_kernel(const GatePairParams p) {
           const f32x4_t c = j < p.NB ? *(const f32x4_t*)(krow + su + u) : (f32x4_t){};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
+            const float w = p.w_out[c0 + su + u + e];
             uq_t[(su + u + e) * kPairLd + sr] = a[e];
             uk_t[(su + u + e) * kPairLd + sr] = c[e];
+            a_part = fmaf(w, a[e], a_part);
+            b_part = fmaf(w, c[e], b_part);
           }
         }
       } else {
 #pragma unroll
         for (int u = 0; u < SU; ++u) {
           const int cc = su + u;
-          uq_t[cc * kPairLd + sr] = (cc < hc && i < p.NB) ? qrow[cc] : 0.f;
-          uk_t[cc * kPairLd + sr] = (cc < hc && j < p.NB) ? krow[cc] : 0.f;
+          const float a = (cc < hc && i < p.NB) ? qrow[cc] : 0.f;
+          const float c = (cc < hc && j < p.NB) ? krow[cc] : 0.f;
+          const float w = cc < hc ? p.w_out[c0 + cc] : 0.f;
+          uq_t[cc * kPairLd + sr] = a;
+          uk_t[cc * kPairLd + sr] = c;
+          a_part = fmaf(w, a, a_part);
+          b_part = fmaf(w, c, b_part);
         }
       }
       if (tid < kPairHid) wo[tid] = tid < hc ? p.w_out[c0 + tid] : 0.f;
@@ -333,8 +347,18 @@ gate_pairwise_kernel(const GatePairParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(w, fmaxf(av[r] + bv[c], 0.f), acc[r][c]);
+          for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(fabsf(av[r] + bv[c]), w, acc[r][c]);
       }
+    }
+    // The 8 threads that staged row sr are consecutive lanes.
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+      a_part += __shfl_xor(a_part, off, kWave);
+      b_part += __shfl_xor(b_part, off, kWave);
+    }
+    if ((tid & 7) == 0) {
+      ab[0][sr] = a_part;
+      ab[1][sr] = b_part;
     }
     __syncthreads();
     float* part = lds + wave * (kPairTile * kPairLd);
@@ -358,7 +382,8 @@ gate_pairwise_kernel(const GatePairParams p) {
     if (!skip) {
       const int o = ii * kPairLd + jj;
       const int t = kPairTile * kPairLd;
-      logit = (lds[o] + lds[t + o]) + (lds[2 * t + o] + lds[3 * t + o]);
+      const float sabs = (lds[o] + lds[t + o]) + (lds[2 * t + o] + lds[3 * t + o]);
+      logit = 0.5f * ((ab[0][ii] + ab[1][jj]) + sabs);
     }
     float soft = 1.f / (1.f + expf(-logit));
     if (p.causal && j > i) soft = 0.f;
