@@ -24,7 +24,7 @@ namespace tasft {
 
 constexpr int kPoolBlocks = 8;    // blocks pooled per workgroup (amortises the W_in read)
 constexpr int kGateMaxD = 256;
-constexpr int kPairHid = 128;     // hidden units staged per LDS round (pairwise)
+constexpr int kPairHid = 64;      // hidden units staged per LDS round (pairwise)
 
 struct GatePoolParams {
   const uint16_t* q;
