@@ -114,18 +114,19 @@ def bench_config2(torch, dev, steps, warmup):
 
     for _ in range(warmup):
         g, _out = step()
-    torch.cuda.synchronize()
-    n_exec = int(executed_blocks(g.hard_mask, causal=True).item())
-    nb = shape.nb
-    n_causal = shape.batch * shape.q_heads * nb * (nb + 1) // 2
+    # No host round trip between the warm-up and the timed steps (a device->host read here
+    # idles the GPU, and the next ~40 steps then run up to 15% slower).
     t_gate.reset()
     t_pref.reset()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step()
+        g, _out = step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    n_exec = int(executed_blocks(g.hard_mask, causal=True).item())
+    nb = shape.nb
+    n_causal = shape.batch * shape.q_heads * nb * (nb + 1) // 2
     gate_ms = t_gate.total_ms() / steps
     pref_ms = t_pref.total_ms() / steps
     flop = n_exec * FLOP_PER_BLOCK
@@ -286,10 +287,10 @@ def copy_probe(torch, dev, mib: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    # The GPU clock ramps for the first ~50 steps after an idle setup phase (about 1.2 ms
-    # per step at first, about 0.79 ms steady); warm-up steps are untimed.
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
+    # The GPU settles over the first ~150 steps after the idle setup phase (about 1.2 ms
+    # per step at first, 0.85 ms after 50 steps, 0.73 ms steady); warm-up steps are untimed.
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--extras", default="decode,qwen,gate_target",
                     help="comma list of extra workloads (decode, qwen, gate_target) or 'none'")
     ap.add_argument("--no-extras", action="store_true", help="same as --extras none")
