@@ -366,7 +366,7 @@ def main() -> int:
             "block": res["shape"].block, "gate_hidden": 128, "target_causal_sparsity": 0.8,
         },
         "roofline": {
-            "kernel": "bsfa_prefill_bs64_kernel<128>",
+            "kernel": "bsfa_prefill_bs64_2w_kernel<128>",
             "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": round(PREFILL_TRAFFIC_BYTES),

@@ -653,6 +653,227 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Block size 64, head dim 128: two waves per query block.
+//
+// Wave w owns query rows 32*w..+31 and all 64 keys of every active key block: 16 S MFMAs
+// (two 32-key tiles) and 16 PV MFMAs per block, so a row needs no merge of partial
+// results. Four such workgroups (32 KB of LDS each: one K tile and one V tile) share a CU,
+// two waves per SIMD. Per block: the V DMA starts once every wave has read the previous
+// V tile, the next block's K DMA once every wave has read this K tile, and the PV product
+// waits only for V. Each DMA instruction moves 1 KB; one LDS base (M0) serves four of them
+// through the instruction offset, which the hardware adds to both the global and the LDS
+// address (the field holds 12 bits, so units four apart need their own base).
+// ---------------------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void dma_tile_2w(uint8_t* tile, __amdgpu_buffer_rsrc_t rsrc,
+                                            const int* voff, int wave) {
+  static_assert(D == 128, "eight 1 KB units per wave and tile");
+  TASFT_LDS void* b0 = (TASFT_LDS void*)(tile + wave * 8192);
+  TASFT_LDS void* b1 = (TASFT_LDS void*)(tile + wave * 8192 + 4096);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[0], 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[1], 0, 1024, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[2], 0, 2048, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[3], 0, 3072, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[4], 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[5], 0, 1024, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[6], 0, 2048, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[7], 0, 3072, 0);
+}
+
+template <int D>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2)))
+bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
+  constexpr int BS = 64;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DTILES = D / 32;
+  constexpr int ROWB = D * 2;
+  constexpr int TILE = BS * ROWB;
+  constexpr int UPW = (TILE / 1024) / 2;  // DMA units per wave and tile
+
+  __shared__ __attribute__((aligned(1024))) uint8_t kS[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t vS[TILE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar DMA addresses
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // Per-lane source offsets of this wave's DMA units (see dma_tile), less the instruction
+  // offset that dma_tile_2w adds. Unit u starts at tile row 4u >= 4 (u & 3), so the
+  // difference stays non-negative.
+  int kvoff[UPW], vvoff[UPW];
+#pragma unroll
+  for (int i = 0; i < UPW; ++i) {
+    const int byte = (wave * UPW + i) * 1024 + lane * 16;
+    const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+    kvoff[i] = (row * (int)p.sk[2] + swz_k<D>(row, pos) * 8) * 2 - (i & 3) * 1024;
+    vvoff[i] = (row * (int)p.sv[2] + swz_v<D>(row, pos) * 8) * 2 - (i & 3) * 1024;
+  }
+  const int grp16 = lane >> 4, t16 = lane & 15;  // ds_read_tr group and lane in group
+  const int tr_row = t16 >> 2;                   // source row offset within a 4-row run
+  const int tr_cb = t16 & 3;                     // source 8-byte column block
+  const uint32_t krb = (uint32_t)p.sk[2] * 2u, vrb = (uint32_t)p.sv[2] * 2u;
+
+  const PrefillItem item = prefill_item(p, (int64_t)blockIdx.x);
+  const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
+  uint16_t* obase = p.o + b * p.so[0] + h * p.so[1];
+  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
+
+  const int qrow = qb * BS + wave * 32 + col;
+  const bool qvalid = qrow < p.S;
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  // Blocks from here on need element masks (causal diagonal or partial last block).
+  const int mask_from = p.causal ? qb : ((p.S % BS) != 0 ? p.NB - 1 : p.NB);
+  // Loads in the order their results are needed: mask bytes, Q, then the first K DMA.
+  uint8_t mb = 0;
+  if (lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
+  bf16x8_t qf[KSTEPS];
+  {
+    // Rows past the end read row S-1: per-row results, never stored.
+    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : p.S - 1) * p.sq[2] + half * 8;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
+  }
+  // Buffer resource of key block kb of K or V (rows >= S are out of range: zeros).
+  auto block_rsrc = [&](const uint16_t* base, uint32_t rb, int64_t stride, int kb) {
+    if (p.small_spans) {
+      const uint32_t key0 = (uint32_t)kb * BS, left = (uint32_t)p.S - key0;
+      return __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)base + key0 * rb), (short)0,
+                                               (int)(left * rb), 0x00020000);
+    }
+    const int key0 = kb * BS;
+    return tile_rsrc(base + (int64_t)key0 * stride, (int64_t)(p.S - key0) * stride * 2);
+  };
+
+  f32x16_t oacc[DTILES];
+#pragma unroll
+  for (int dt = 0; dt < DTILES; ++dt) oacc[dt] = (f32x16_t){};
+  float m_ref = -INFINITY;  // exp2 reference of this lane's query row (log2 domain)
+  float l_run = 0.f;
+
+  int chunk = 0;
+  uint64_t bits = __ballot(mb != 0);
+  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+  if (kb >= 0) dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb), kvoff, wave);
+
+  while (kb >= 0) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's share of K(kb) landed
+    __syncthreads();                      // K(kb) visible; every wave is done with the V tile
+    dma_tile_2w<D>(vS, block_rsrc(vbase, vrb, p.sv[2], kb), vvoff, wave);
+    u32x4_t kf[2][KSTEPS];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int r = kt * 32 + col;
+        kf[kt][ks] = *(const u32x4_t*)(kS + r * ROWB + swz_k<D>(r, ks * 2 + half) * 16);
+      }
+    f32x16_t s0 = (f32x16_t){}, s1 = (f32x16_t){};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      s0 = mfma_32x32x16_bf16(as_bf16x8(kf[0][ks]), qf[ks], s0);
+      s1 = mfma_32x32x16_bf16(as_bf16x8(kf[1][ks]), qf[ks], s1);
+    }
+    __syncthreads();  // every wave has read K(kb): the K tile is free
+    const int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    if (kb_next >= 0) dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb_next), kvoff, wave);
+    if (kb >= mask_from) {
+      const int key0 = kb * BS;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int k0 = key0 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+        const int k1 = k0 + 32;
+        s0[rr] = (k0 >= p.S || (p.causal && k0 > qrow)) ? -INFINITY : s0[rr];
+        s1[rr] = (k1 >= p.S || (p.causal && k1 > qrow)) ? -INFINITY : s1[rr];
+      }
+    }
+    // Scores stay unscaled: scale > 0 commutes with max, and exp2 takes one FMA.
+    float mraw = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int rr = 1; rr < 16; ++rr) mraw = fmaxf(mraw, fmaxf(s0[rr], s1[rr]));
+    const float mloc = pair_max32(mraw) * p.scale_log2;
+    const bool move = mloc > m_ref + kRescaleLog2;
+    if (__ballot(move)) {
+      // exp2(-inf) = 0 clears the (empty) accumulators on a row's first finite score.
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - mloc) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) oacc[dt] *= alpha;
+      m_ref = move ? mloc : m_ref;
+    }
+    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+    float lsum0 = 0.f, lsum1 = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const float e0 = __builtin_amdgcn_exp2f(fmaf(s0[rr], p.scale_log2, -m_use));
+      const float e1 = __builtin_amdgcn_exp2f(fmaf(s1[rr], p.scale_log2, -m_use));
+      s0[rr] = e0;
+      s1[rr] = e1;
+      lsum0 += e0;
+      lsum1 += e1;
+    }
+    l_run += lsum0 + lsum1;
+    // P^T as the B operand of four 16-key k-steps: keys 16pp + 8*(j>>2) + 4*half + (j&3)
+    // for element j, the same key order the V^T reads below use.
+    bf16x8_t pb[4];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const f32x16_t& sv = (pp < 2) ? s0 : s1;
+      const int o = 8 * (pp & 1);
+      const u32x4_t w = {pack_bf16x2(sv[o + 0], sv[o + 1]), pack_bf16x2(sv[o + 2], sv[o + 3]),
+                         pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
+      pb[pp] = as_bf16x8(w);
+    }
+    // This wave's share of V(kb) landed; the K DMA of the next block (8 units) may not have.
+    if (kb_next >= 0)
+      __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();  // V(kb) visible
+    u32x2_t vlo[4][DTILES], vhi[4][DTILES];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const int kk = 16 * pp + 4 * (grp16 >> 1);  // first key of run 1
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+        const int d0 = dt * 32 + 16 * (grp16 & 1) + 4 * tr_cb;  // source column of this lane
+        const int cc = d0 >> 3, sub = (d0 & 7) * 2;
+        const int r1 = kk + tr_row, r2 = r1 + 8;
+        vlo[pp][dt] = ds_read_tr16_b64((const void*)(vS + r1 * ROWB + swz_v<D>(r1, cc) * 16 + sub));
+        vhi[pp][dt] = ds_read_tr16_b64((const void*)(vS + r2 * ROWB + swz_v<D>(r2, cc) * 16 + sub));
+      }
+    }
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+        const u32x4_t a = {vlo[pp][dt][0], vlo[pp][dt][1], vhi[pp][dt][0], vhi[pp][dt][1]};
+        oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb[pp], oacc[dt]);
+      }
+    kb = kb_next;
+  }
+
+  const float l_tot = pair_sum32(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // empty rows output 0
+  if (qvalid) {
+    uint16_t* orow = obase + (int64_t)qrow * p.so[2];
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d0 = dt * 32 + 8 * gq + 4 * half;
+        const u32x2_t w = {pack_bf16x2(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
+                           pack_bf16x2(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
+        *(u32x2_t*)(orow + d0) = w;
+      }
+  }
+}
+
 // Compute units of the current device (cached per device).
 static int device_cus() {
   static int cached[64] = {0};
@@ -679,10 +900,16 @@ template <int D>
 static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t stream) {
   const int64_t total = (int64_t)p.NB * p.B * p.Hq;
   int64_t grid = total;
+  // Head dim 128 runs the two-wave kernel, one workgroup per item (measured faster than
+  // the persistent ticket loop with four such workgroups per CU); head dim 64 runs the
+  // four-wave one, persistent when the caller passes a workspace.
+  constexpr bool two_wave = D == 128;
+  constexpr int threads = two_wave ? 128 : 256;
+  if (two_wave) queue = nullptr;
   if (queue) {
     // Every resident workgroup slot filled once, a whole number per partition.
     p.parts = (((int64_t)p.B * p.Hkv) % 8 == 0) ? 8 : 1;
-    static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D>, 256);
+    static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D>, threads);
     int64_t wg = std::min<int64_t>(total, (int64_t)per_cu * device_cus());
     wg = std::max<int64_t>(p.parts, wg / p.parts * p.parts);
     p.wg_per_part = (int)(wg / p.parts);
@@ -690,7 +917,10 @@ static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t s
     grid = wg;
     hipLaunchKernelGGL(bsfa_queue_reset_kernel, dim3(1), dim3(64), 0, stream, queue);
   }
-  hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  if constexpr (two_wave)
+    hipLaunchKernelGGL((bsfa_prefill_bs64_2w_kernel<D>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
   return hipGetLastError();
 }
 
