@@ -660,8 +660,10 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 // (two 32-key tiles) and 16 PV MFMAs per block, so a row needs no merge of partial
 // results. Four such workgroups (32 KB of LDS each: one K tile and one V tile) share a CU,
 // two waves per SIMD. Per block: the V DMA starts once every wave has read the previous
-// V tile, the next block's K DMA once every wave has read this K tile, and the PV product
-// waits only for V. Each DMA instruction moves 1 KB; one LDS base (M0) serves four of them
+// V tile, and the next block's K DMA once every wave has read this K tile. The barriers are
+// __syncthreads(), whose workgroup fence also waits for every DMA still in flight (a
+// fence-free barrier waiting only for what each step needs measured no faster). Each DMA
+// instruction moves 1 KB; one LDS base (M0) serves four of them
 // through the instruction offset, which the hardware adds to both the global and the LDS
 // address (the field holds 12 bits, so units four apart need their own base).
 // ---------------------------------------------------------------------------------------
@@ -829,12 +831,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
                          pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
       pb[pp] = as_bf16x8(w);
     }
-    // This wave's share of V(kb) landed; the K DMA of the next block (8 units) may not have.
-    if (kb_next >= 0)
-      __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __syncthreads();  // V(kb) visible
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's share of V(kb) landed
+    __syncthreads();                      // V(kb) visible
     u32x2_t vlo[4][DTILES], vhi[4][DTILES];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
