@@ -660,13 +660,18 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 // (two 32-key tiles) and 16 PV MFMAs per block, so a row needs no merge of partial
 // results. Four such workgroups (32 KB of LDS each: one K tile and one V tile) share a CU,
 // two waves per SIMD. Per block: the V DMA starts once every wave has read the previous
-// V tile, and the next block's K DMA once every wave has read this K tile. The barriers are
-// __syncthreads(), whose workgroup fence also waits for every DMA still in flight (a
-// fence-free barrier waiting only for what each step needs measured no faster). Each DMA
+// V tile, and the next block's K DMA once every wave has read this K tile; PV waits for V
+// only. The barriers carry no memory fence (a __syncthreads() fence would also wait for
+// the DMA still in flight): each is preceded by the explicit wait it needs. Each DMA
 // instruction moves 1 KB; one LDS base (M0) serves four of them
 // through the instruction offset, which the hardware adds to both the global and the LDS
 // address (the field holds 12 bits, so units four apart need their own base).
 // ---------------------------------------------------------------------------------------
+// Workgroup barrier without a memory fence. The caller waits (s_waitcnt) for what the
+// barrier publishes; the memory clobber keeps the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 template <int D>
 __device__ __forceinline__ void dma_tile_2w(uint8_t* tile, __amdgpu_buffer_rsrc_t rsrc,
                                             const int* voff, int wave) {
@@ -764,8 +769,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   if (kb >= 0) dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb), kvoff, wave);
 
   while (kb >= 0) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's share of K(kb) landed
-    __syncthreads();                      // K(kb) visible; every wave is done with the V tile
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): own share of K(kb) landed
+    block_barrier();                      // K(kb) visible; every wave is done with the V tile
     dma_tile_2w<D>(vS, block_rsrc(vbase, vrb, p.sv[2], kb), vvoff, wave);
     u32x4_t kf[2][KSTEPS];
 #pragma unroll
@@ -781,9 +786,12 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
       s0 = mfma_32x32x16_bf16(as_bf16x8(kf[0][ks]), qf[ks], s0);
       s1 = mfma_32x32x16_bf16(as_bf16x8(kf[1][ks]), qf[ks], s1);
     }
-    __syncthreads();  // every wave has read K(kb): the K tile is free
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's K reads returned
+    block_barrier();                      // every wave has read K(kb): the K tile is free
     const int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
-    if (kb_next >= 0) dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb_next), kvoff, wave);
+    // Always eight DMA units after V(kb) (the last block of a row loads its own K tile
+    // again), so the V wait below is one fixed count.
+    dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb_next >= 0 ? kb_next : kb), kvoff, wave);
     if (kb >= mask_from) {
       const int key0 = kb * BS;
 #pragma unroll
@@ -831,8 +839,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
                          pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
       pb[pp] = as_bf16x8(w);
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's share of V(kb) landed
-    __syncthreads();                      // V(kb) visible
+    __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8): own share of V(kb) landed, next K in flight
+    block_barrier();                      // V(kb) visible
     u32x2_t vlo[4][DTILES], vhi[4][DTILES];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
@@ -855,6 +863,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
       }
     kb = kb_next;
   }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // no DMA into this workgroup's LDS outlives it
 
   const float l_tot = pair_sum32(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // empty rows output 0
