@@ -793,19 +793,27 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
     // again), so the V wait below is one fixed count.
     dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb_next >= 0 ? kb_next : kb), kvoff, wave);
     if (kb >= mask_from) {
-      const int key0 = kb * BS;
+      // Register rr of tile t holds key kb*BS + 32t + 4*half + off(rr), off = 8*(rr/4) +
+      // rr%4; a key is admissible iff it is <= min(qrow, S-1) (causal) or S-1, i.e. iff
+      // 32t + off <= lim below: one compare per score.
+      const int last = p.causal ? min(qrow, p.S - 1) : p.S - 1;
+      const int lim = last - kb * BS - 4 * half;
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
-        const int k0 = key0 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-        const int k1 = k0 + 32;
-        s0[rr] = (k0 >= p.S || (p.causal && k0 > qrow)) ? -INFINITY : s0[rr];
-        s1[rr] = (k1 >= p.S || (p.causal && k1 > qrow)) ? -INFINITY : s1[rr];
+        const int off = 8 * (rr >> 2) + (rr & 3);
+        s0[rr] = off > lim ? -INFINITY : s0[rr];
+        s1[rr] = off + 32 > lim ? -INFINITY : s1[rr];
       }
     }
-    // Scores stay unscaled: scale > 0 commutes with max, and exp2 takes one FMA.
-    float mraw = fmaxf(s0[0], s1[0]);
+    // Scores stay unscaled: scale > 0 commutes with max, and exp2 takes one FMA. Two
+    // chains of three-input maxima.
+    float ma = fmaxf(fmaxf(s0[0], s0[1]), s0[2]), mb = fmaxf(fmaxf(s1[0], s1[1]), s1[2]);
 #pragma unroll
-    for (int rr = 1; rr < 16; ++rr) mraw = fmaxf(mraw, fmaxf(s0[rr], s1[rr]));
+    for (int rr = 3; rr < 15; rr += 2) {
+      ma = fmaxf(fmaxf(ma, s0[rr]), s0[rr + 1]);
+      mb = fmaxf(fmaxf(mb, s1[rr]), s1[rr + 1]);
+    }
+    const float mraw = fmaxf(fmaxf(ma, s0[15]), fmaxf(mb, s1[15]));
     const float mloc = pair_max32(mraw) * p.scale_log2;
     const bool move = mloc > m_ref + kRescaleLog2;
     if (__ballot(move)) {
