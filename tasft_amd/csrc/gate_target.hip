@@ -161,37 +161,40 @@ gate_target_normalize_kernel(float* data, int64_t group_len, float inv_temp, flo
 
 
 // Block size 64. A workgroup owns one query block of HPW query heads of the same KV head
-// (the target is dense, so these heads read exactly the same K blocks) with four waves per
-// head: wave (hw, w) takes head hw, query rows 32*(w&1).. and the key half 32*(w>>1).. of
-// every causal key block. K tiles are copied HBM -> LDS once for all HPW heads by
-// buffer_load_dwordx4 ... lds (16-byte XOR swizzle, rows past S arrive as zeros) into two
-// stages, one barrier per block. Each wave reduces its 32 x 32 sub-tile to one maximum with
-// DPP / permlane swaps (no LDS round trips); the four partial maxima of a head's block are
-// combined one block later from a double-buffered LDS slot.
+// (the target is dense, so these heads read exactly the same K blocks) with WPH waves per
+// head: with WPH = 2 (the launched form) wave (hw, w) takes head hw, query rows 32*w..+31
+// and all 64 keys of every causal key block (16 MFMAs per block); with WPH = 4 it takes
+// rows 32*(w&1).. and the key half 32*(w>>1).. (8 MFMAs, measured 9% slower at config 5).
+// K tiles are copied HBM -> LDS once for all HPW heads by buffer_load_dwordx4 ... lds
+// (16-byte XOR swizzle, rows past S arrive as zeros) into two stages, one barrier per
+// block. Each wave reduces its sub-tile to one maximum with DPP / permlane swaps (no LDS
+// round trips); the WPH partial maxima of a head's block are combined one block later
+// from a double-buffered LDS slot.
 template <int D>
 __device__ __forceinline__ int gt_swz(int r, int cc) {
   return cc ^ (D == 128 ? (r & 15) : ((r >> 1) & 7));
 }
 
-template <int D, int HPW>
-__global__ void __launch_bounds__(HPW * 256)
+template <int D, int HPW, int WPH = 2>
+__global__ void __launch_bounds__(HPW * WPH * 64)
 gate_target_bs64_kernel(const GateTargetParams p) {
   constexpr int BS = 64;
   constexpr int KSTEPS = D / 16;
   constexpr int ROWB = D * 2;
   constexpr int TILE = BS * ROWB;
   constexpr int UNITS = TILE / 1024;  // 1 KB DMA units per tile
-  constexpr int NWAVES = 4 * HPW;
+  constexpr int NWAVES = WPH * HPW;
+  constexpr int HT = WPH * kWave;  // threads per head
   __shared__ __attribute__((aligned(1024))) uint8_t kA[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t kB[TILE];
-  __shared__ float red[2][HPW][4];
+  __shared__ float red[2][HPW][WPH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int hw = wave >> 2;  // head within the workgroup
-  const int w4 = wave & 3;
-  const int rh = w4 & 1, kh = w4 >> 1;
+  const int hw = wave / WPH;  // head within the workgroup
+  const int w4 = wave % WPH;
+  const int rh = w4 & 1, kh = WPH == 4 ? (w4 >> 1) : 0;
   const int col = lane & 31;
   const int half = lane >> 5;
 
@@ -252,39 +255,57 @@ gate_target_bs64_kernel(const GateTargetParams p) {
     }
   };
   const int krow_l = kh * 32 + col;
-  // One block from stage kt: this wave's 32 x 32 sub-tile maximum (raw scores).
+  // One block from stage kt: this wave's 32 x 32 (or 32 x 64) sub-tile maximum.
+  constexpr int NKT = WPH == 4 ? 1 : 2;  // 32-key tiles per wave
   auto block_max = [&](const uint8_t* kt, int kb) {
-    f32x16_t s = (f32x16_t){};
+    f32x16_t s[NKT];
+#pragma unroll
+    for (int t = 0; t < NKT; ++t) s[t] = (f32x16_t){};
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cc = ks * 2 + half;
-      const u32x4_t a = *(const u32x4_t*)(kt + krow_l * ROWB + gt_swz<D>(krow_l, cc) * 16);
-      s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
+#pragma unroll
+      for (int t = 0; t < NKT; ++t) {
+        const int kr = krow_l + 32 * t;
+        const u32x4_t a = *(const u32x4_t*)(kt + kr * ROWB + gt_swz<D>(kr, cc) * 16);
+        s[t] = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s[t]);
+      }
     }
     const int key0 = kb * BS;
     if ((p.causal && kb == qb) || (key0 + BS > p.S) || qb * BS + BS > p.S) {
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int key = key0 + kh * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-        s[rr] = (!qvalid || key >= p.S || (p.causal && key > qrow)) ? -INFINITY : s[rr];
-      }
-    }
-    float m4[4];
+      for (int t = 0; t < NKT; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      m4[j] = fmaxf(fmaxf(s[4 * j], s[4 * j + 1]), fmaxf(s[4 * j + 2], s[4 * j + 3]));
-    return wave_max_dpp(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+        for (int rr = 0; rr < 16; ++rr) {
+          const int key = key0 + kh * 32 + 32 * t + 8 * (rr >> 2) + 4 * half + (rr & 3);
+          s[t][rr] = (!qvalid || key >= p.S || (p.causal && key > qrow)) ? -INFINITY : s[t][rr];
+        }
+    }
+    float m = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
+#pragma unroll
+    for (int rr = 3; rr < 15; rr += 2) m = fmaxf(fmaxf(m, s[0][rr]), s[0][rr + 1]);
+    m = fmaxf(m, s[0][15]);
+    if constexpr (NKT == 2) {
+      float m2 = fmaxf(fmaxf(s[1][0], s[1][1]), s[1][2]);
+#pragma unroll
+      for (int rr = 3; rr < 15; rr += 2) m2 = fmaxf(fmaxf(m2, s[1][rr]), s[1][rr + 1]);
+      m = fmaxf(m, fmaxf(m2, s[1][15]));
+    }
+    return wave_max_dpp(m);
   };
   // Combine the four partial maxima of this head's block kb (slot kb & 1), scaled.
   auto store = [&](int kb) {
-    if ((tid & 255) == 0) {
+    if ((tid % HT) == 0) {
       const float* rm = red[kb & 1][hw];
-      orow[kb] = fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3])) * p.scale;
+      float m = rm[0];
+#pragma unroll
+      for (int i = 1; i < WPH; ++i) m = fmaxf(m, rm[i]);
+      orow[kb] = m * p.scale;
     }
   };
 
   const int kb_end = p.causal ? qb + 1 : p.NB;
-  for (int kb = kb_end + (tid & 255); kb < p.NB; kb += 256) orow[kb] = -INFINITY;
+  for (int kb = kb_end + (tid % HT); kb < p.NB; kb += HT) orow[kb] = -INFINITY;
   if (kb_end > 0) issue(kA, 0);
   for (int kb = 0; kb < kb_end; kb += 2) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's DMA of block kb landed
@@ -314,11 +335,11 @@ static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t st
   const int hpw = (p.G % 4 == 0) ? 4 : (p.G % 2 == 0 ? 2 : 1);
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq / hpw;
   if (hpw == 4)
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4>), dim3((unsigned)grid), dim3(4 * 128), 0, stream, p);
   else if (hpw == 2)
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2>), dim3((unsigned)grid), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2>), dim3((unsigned)grid), dim3(2 * 128), 0, stream, p);
   else
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1>), dim3((unsigned)grid), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 
