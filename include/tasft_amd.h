@@ -33,7 +33,7 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (2). */
+/* ABI version of this library (3). */
 int tasft_abi_version(void);
 
 /*
@@ -64,6 +64,32 @@ int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* ou
                            int64_t block_size, const int64_t* q_strides, const int64_t* k_strides,
                            const int64_t* v_strides, const int64_t* o_strides,
                            const int64_t* mask_strides, float scale, int causal, void* stream);
+
+/*
+ * Block-sparse prefill of a packed batch of variable-length sequences, in one launch.
+ * Stands in for the flat-token prefill of TASFTvLLMAttentionBackend.forward
+ * (reference tasft/inference/vllm_patch.py:172-176 and :199-203), which views all
+ * num_tokens tokens as one sequence (B = 1) and so lets a request attend to the tokens of
+ * the requests packed before it; here sequence n is tokens cu_seqlens[n] ..
+ * cu_seqlens[n+1]-1 and attends only within itself, with the semantics of
+ * tasft_bsfa_prefill_fwd applied per sequence (positions and blocks counted from its
+ * first token).
+ *
+ * q, out [T, Hq, D]; k, v [T, Hkv, D] (strides of token, head, dim in elements, dim
+ * contiguous, token and head strides multiples of 8). cu_seqlens: device int32
+ * [num_seqs + 1], cu_seqlens[0] = 0, non-decreasing, every length <= max_seqlen.
+ * block_mask: [num_seqs, Hq, NB, NB] bytes with NB = ceil(max_seqlen / bs); sequence n
+ * uses its leading ceil(len_n / bs) x ceil(len_n / bs) corner. Lengths are clamped to
+ * [0, max_seqlen]; the caller guarantees the tokens exist. No workspace.
+ */
+int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const void* v, void* out,
+                                  const uint8_t* block_mask, const int32_t* cu_seqlens,
+                                  int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
+                                  int64_t max_seqlen, int64_t head_dim, int64_t block_size,
+                                  const int64_t* q_strides, const int64_t* k_strides,
+                                  const int64_t* v_strides, const int64_t* o_strides,
+                                  const int64_t* mask_strides, float scale, int causal,
+                                  void* stream);
 
 /*
  * Bytes of the optional workspace of tasft_bsfa_prefill_fwd (work-queue counters).

@@ -17,6 +17,9 @@ asks for float64. How each function is pinned (checked independently of itself):
   pure-Python loop implementation on tiny inputs.
 * ``attention_block_gather``: equals ``attention_dense_masked``.
 * ``sparse_decode``: equals the last row of ``attention_block_gather``; brute force.
+* ``attention_varlen``: equals ``attention_dense_masked`` over the whole packed token
+  range with an independently built block-diagonal token mask (tests/test_oracle.py), and
+  with one sequence equals the reference's flat-token call (B = 1).
 * ``gate_target_from_scores``: literal vectors of tests/unit/test_objectives.py:169-191,
   test_numerical_correctness.py:119-157 and :714-721; torch max_pool2d + softmax.
 * ``block_max`` / ``gate_target_from_qk``: equal ``gate_target_from_scores`` applied to
@@ -193,6 +196,34 @@ def attention_block_gather(q, k, v, block_mask, bs: int, causal: bool = True,
             p = np.exp(sco - np.where(np.isfinite(mx), mx, 0.0))
             l = p.sum(axis=-1, keepdims=True)
             out[b, h, q0:q1] = np.where(l > 0, (p @ vh[idx]) / np.where(l > 0, l, 1.0), 0.0)
+    return out
+
+
+def attention_varlen(q, k, v, cu_seqlens, block_mask, bs: int, causal: bool = True,
+                     scale: float | None = None, dtype: type = np.float32) -> np.ndarray:
+    """Packed variable-length prefill: ``attention_block_gather`` per sequence.
+
+    q ``[T, Hq, D]``, k/v ``[T, Hkv, D]`` (the flat token layout of
+    tasft/inference/vllm_patch.py:172-176); sequence n is tokens ``cu_seqlens[n] ..
+    cu_seqlens[n+1]-1`` and uses the leading corner of ``block_mask[n]`` (``[Hq, NB, NB]``).
+    The reference views the whole packed range as one sequence (B = 1, :172-176); this
+    keeps each request to its own tokens, with positions and blocks counted from its first
+    token (the kernel semantics of block_sparse_fa.py:192-269 per sequence). Tokens after
+    ``cu_seqlens[-1]`` stay 0.
+    """
+    cu = [int(x) for x in cu_seqlens]
+    out = np.zeros(q.shape, dtype=dtype)
+    for n in range(len(cu) - 1):
+        t0, t1 = cu[n], cu[n + 1]
+        if t1 <= t0:
+            continue
+        nb = math.ceil((t1 - t0) / bs)
+        qs = q[t0:t1].transpose(1, 0, 2)[None]
+        ks = k[t0:t1].transpose(1, 0, 2)[None]
+        vs = v[t0:t1].transpose(1, 0, 2)[None]
+        o = attention_block_gather(qs, ks, vs, block_mask[n:n + 1, :, :nb, :nb], bs, causal,
+                                   scale, dtype)
+        out[t0:t1] = o[0].transpose(1, 0, 2)
     return out
 
 

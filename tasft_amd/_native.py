@@ -22,6 +22,7 @@ EXPORTED_SYMBOLS = (
     "tasft_abi_version",
     "tasft_bsfa_prefill_workspace_bytes",
     "tasft_bsfa_prefill_fwd",
+    "tasft_bsfa_prefill_varlen_fwd",
     "tasft_bsfa_decode_workspace_bytes",
     "tasft_bsfa_decode_fwd",
     "tasft_gate_workspace_bytes",
@@ -49,6 +50,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_bsfa_prefill_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
+    ),
+    "tasft_bsfa_prefill_varlen_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
     ),
     "tasft_bsfa_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),

@@ -42,6 +42,10 @@ struct PrefillParams {
   int* queue;        // per-partition ticket counters of the persistent launch, or null
   int parts;         // work partitions: 8 (one per XCD) or 1
   int wg_per_part;   // persistent workgroups per partition
+  // Packed variable-length batch: sequence b holds tokens cu_seqlens[b] .. cu_seqlens[b+1]-1
+  // of dimension s (the b strides are 0), S is the longest length and NB its block count.
+  // Null for a dense [B, H, S, D] launch.
+  const int* cu_seqlens;
 };
 
 // Static order of the (batch, query head, query block) work items. gfx950 dispatches
@@ -74,6 +78,22 @@ __device__ __forceinline__ PrefillItem prefill_item(const PrefillParams& p, int6
   it.kvh = (int)(grp % (uint32_t)p.Hkv);
   it.h = it.kvh * p.G + (int)(r % (uint32_t)p.G);
   return it;
+}
+
+// Token span of batch entry b: the whole sequence dimension (dense launch), or sequence b
+// of a packed batch (its first token and length, clamped to [0, S]).
+struct SeqSpan {
+  int S, NB;
+  int64_t tok0;
+};
+
+template <int BS>
+__device__ __forceinline__ SeqSpan seq_span(const PrefillParams& p, int b) {
+  if (!p.cu_seqlens) return {p.S, p.NB, 0};
+  const int t0 = p.cu_seqlens[b];
+  int len = p.cu_seqlens[b + 1] - t0;
+  len = len < 0 ? 0 : (len > p.S ? p.S : len);
+  return {len, (len + BS - 1) / BS, (int64_t)t0};
 }
 
 // Persistent launch (block size 64). Rows differ widely in cost (a gate can light whole
@@ -111,17 +131,22 @@ bsfa_prefill_kernel(const PrefillParams p) {
 
   const PrefillItem item = prefill_item(p, (int64_t)blockIdx.x);
   const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
+  // Varlen launch: items past the last query block of a shorter sequence have no work.
+  const SeqSpan span = seq_span<BS>(p, b);
+  if (qb >= span.NB) return;
+  const int S = span.S, NB = span.NB;
 
-  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
-  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
-  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
-  uint16_t* obase = p.o + b * p.so[0] + h * p.so[1];
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + span.tok0 * p.sq[2] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + span.tok0 * p.sk[2] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + span.tok0 * p.sv[2] + kvh * p.sv[1];
+  uint16_t* obase = p.o + b * p.so[0] + span.tok0 * p.so[2] + h * p.so[1];
   const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
 
   // Q^T as the B operand: lane (col, half) holds query row `qrow`, head dims
   // ks*16 + half*8 .. +7 for every k-step.
   const int qrow = qb * BS + wave * 32 + col;
-  const bool qvalid = qrow < p.S;
+  const bool qvalid = qrow < S;
   bf16x8_t qf[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -136,7 +161,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
   float m_run = -INFINITY;  // running max (log2 domain), identical in lanes l and l^32
   float l_run = 0.f;        // this lane's share of the running denominator
 
-  const int kb_end = p.causal ? qb + 1 : p.NB;
+  const int kb_end = p.causal ? qb + 1 : NB;
   for (int chunk = 0; chunk < kb_end; chunk += kWave) {
     // Every wave reads the same 64 mask bytes, so all waves walk the same key blocks.
     const int kbl = chunk + lane;
@@ -154,7 +179,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
         const int r = c / (D / 8);
         const int cc = c % (D / 8);
         u32x4_t val = {0u, 0u, 0u, 0u};
-        if (key0 + r < p.S) val = *(const u32x4_t*)(kbase + (int64_t)(key0 + r) * p.sk[2] + cc * 8);
+        if (key0 + r < S) val = *(const u32x4_t*)(kbase + (int64_t)(key0 + r) * p.sk[2] + cc * 8);
         *(u32x4_t*)(k_lds + r * KST + cc * 8) = val;
       }
       // Stage V transposed: a unit is 4 keys x 8 head dims, written as 8 rows of V^T.
@@ -167,7 +192,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
         for (int j = 0; j < 4; ++j) {
           const int key = key0 + kq * 4 + j;
           rows[j] = (u32x4_t){0u, 0u, 0u, 0u};
-          if (key < p.S) rows[j] = *(const u32x4_t*)(vbase + (int64_t)key * p.sv[2] + dc * 8);
+          if (key < S) rows[j] = *(const u32x4_t*)(vbase + (int64_t)key * p.sv[2] + dc * 8);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -194,7 +219,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
       }
 
       // Register r of tile t holds key t*32 + 8*(r/4) + 4*half + r%4 for query `qrow`.
-      const bool need_mask = (p.causal && kb == qb) || (key0 + BS > p.S);
+      const bool need_mask = (p.causal && kb == qb) || (key0 + BS > S);
       float mloc = -INFINITY;
 #pragma unroll
       for (int t = 0; t < KTILES; ++t) {
@@ -203,7 +228,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
           float x = s[t][r] * p.scale_log2;
           if (need_mask) {
             const int key = key0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
+            if (key >= S || (p.causal && key > qrow)) x = -INFINITY;
           }
           s[t][r] = x;
           mloc = fmaxf(mloc, x);
@@ -414,19 +439,24 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const int64_t idx = !persistent ? (int64_t)blockIdx.x : (p.parts == 8 ? part + 8 * slot : slot);
   const PrefillItem item = pre ? item_nx : prefill_item(p, idx);
   const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
+  // Varlen launch: items past the last query block of a shorter sequence have no work.
+  const SeqSpan span = seq_span<BS>(p, b);
+  if (qb >= span.NB) return;  // (never in a persistent launch, which is dense)
+  const int S = span.S, NB = span.NB;
 
-  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
-  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
-  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
-  uint16_t* obase = p.o + b * p.so[0] + h * p.so[1];
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + span.tok0 * p.sq[2] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + span.tok0 * p.sk[2] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + span.tok0 * p.sv[2] + kvh * p.sv[1];
+  uint16_t* obase = p.o + b * p.so[0] + span.tok0 * p.so[2] + h * p.so[1];
   const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
 
   const int qrow = qb * BS + rh * 32 + col;
-  const bool qvalid = qrow < p.S;
-  const int kb_end = p.causal ? qb + 1 : p.NB;
+  const bool qvalid = qrow < S;
+  const int kb_end = p.causal ? qb + 1 : NB;
   // Blocks from here on need element masks: the causal diagonal (the last block of a
   // causal row, which is also the partial block if there is one) or the partial block.
-  const int mask_from = p.causal ? qb : ((p.S % BS) != 0 ? p.NB - 1 : p.NB);
+  const int mask_from = p.causal ? qb : ((S % BS) != 0 ? NB - 1 : NB);
   // Loads go out in the order their results are needed, since waits are in issue order:
   // this row's mask bytes (unless the previous item fetched them) and Q; the first K/V
   // DMA follows once the mask bytes are in, and only then the next item's mask bytes and
@@ -436,7 +466,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   bf16x8_t qf[KSTEPS];
   {
     // Rows past the end read row S-1: per-row results, never stored.
-    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : p.S - 1) * p.sq[2] + half * 8;
+    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : S - 1) * p.sq[2] + half * 8;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
   }
@@ -445,7 +475,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const uint32_t krb = (uint32_t)p.sk[2] * 2u, vrb = (uint32_t)p.sv[2] * 2u;
   auto issue = [&](uint8_t* kt, uint8_t* vt, int kb) {
     if (p.small_spans) {
-      const uint32_t key0 = (uint32_t)kb * BS, left = (uint32_t)p.S - key0;
+      const uint32_t key0 = (uint32_t)kb * BS, left = (uint32_t)S - key0;
       dma_tile<D>(kt, __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)kbase + key0 * krb),
                                                         (short)0, (int)(left * krb), 0x00020000),
                   kvoff, wave);
@@ -454,7 +484,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
                   vvoff, wave);
     } else {
       const int key0 = kb * BS;
-      const int64_t rows_left = (int64_t)(p.S - key0);
+      const int64_t rows_left = (int64_t)(S - key0);
       dma_tile<D>(kt, tile_rsrc(kbase + (int64_t)key0 * p.sk[2], rows_left * p.sk[2] * 2), kvoff, wave);
       dma_tile<D>(vt, tile_rsrc(vbase + (int64_t)key0 * p.sv[2], rows_left * p.sv[2] * 2), vvoff, wave);
     }
@@ -505,7 +535,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const int key = key0 + kh * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-        s[rr] = (key >= p.S || (p.causal && key > qrow)) ? -INFINITY : s[rr];
+        s[rr] = (key >= S || (p.causal && key > qrow)) ? -INFINITY : s[rr];
       }
     }
     // Scores stay unscaled: scale > 0 commutes with max, and exp2 takes one FMA.
@@ -724,37 +754,42 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
 
   const PrefillItem item = prefill_item(p, (int64_t)blockIdx.x);
   const int qb = item.qb, b = item.b, kvh = item.kvh, h = item.h;
+  // Varlen launch: items past the last query block of a shorter sequence have no work.
+  const SeqSpan span = seq_span<BS>(p, b);
+  if (qb >= span.NB) return;
+  const int S = span.S, NB = span.NB;
 
-  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
-  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
-  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
-  uint16_t* obase = p.o + b * p.so[0] + h * p.so[1];
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + span.tok0 * p.sq[2] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + span.tok0 * p.sk[2] + kvh * p.sk[1];
+  const uint16_t* vbase = p.v + b * p.sv[0] + span.tok0 * p.sv[2] + kvh * p.sv[1];
+  uint16_t* obase = p.o + b * p.so[0] + span.tok0 * p.so[2] + h * p.so[1];
   const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
 
   const int qrow = qb * BS + wave * 32 + col;
-  const bool qvalid = qrow < p.S;
-  const int kb_end = p.causal ? qb + 1 : p.NB;
+  const bool qvalid = qrow < S;
+  const int kb_end = p.causal ? qb + 1 : NB;
   // Blocks from here on need element masks (causal diagonal or partial last block).
-  const int mask_from = p.causal ? qb : ((p.S % BS) != 0 ? p.NB - 1 : p.NB);
+  const int mask_from = p.causal ? qb : ((S % BS) != 0 ? NB - 1 : NB);
   // Loads in the order their results are needed: mask bytes, Q, then the first K DMA.
   uint8_t mb = 0;
   if (lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
   bf16x8_t qf[KSTEPS];
   {
     // Rows past the end read row S-1: per-row results, never stored.
-    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : p.S - 1) * p.sq[2] + half * 8;
+    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : S - 1) * p.sq[2] + half * 8;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
   }
   // Buffer resource of key block kb of K or V (rows >= S are out of range: zeros).
   auto block_rsrc = [&](const uint16_t* base, uint32_t rb, int64_t stride, int kb) {
     if (p.small_spans) {
-      const uint32_t key0 = (uint32_t)kb * BS, left = (uint32_t)p.S - key0;
+      const uint32_t key0 = (uint32_t)kb * BS, left = (uint32_t)S - key0;
       return __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)base + key0 * rb), (short)0,
                                                (int)(left * rb), 0x00020000);
     }
     const int key0 = kb * BS;
-    return tile_rsrc(base + (int64_t)key0 * stride, (int64_t)(p.S - key0) * stride * 2);
+    return tile_rsrc(base + (int64_t)key0 * stride, (int64_t)(S - key0) * stride * 2);
   };
 
   f32x16_t oacc[DTILES];
@@ -796,7 +831,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
       // Register rr of tile t holds key kb*BS + 32t + 4*half + off(rr), off = 8*(rr/4) +
       // rr%4; a key is admissible iff it is <= min(qrow, S-1) (causal) or S-1, i.e. iff
       // 32t + off <= lim below: one compare per score.
-      const int last = p.causal ? min(qrow, p.S - 1) : p.S - 1;
+      const int last = p.causal ? min(qrow, S - 1) : S - 1;
       const int lim = last - kb * BS - 4 * half;
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
@@ -945,6 +980,20 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 using namespace tasft;
 
+static int dispatch_prefill(const PrefillParams& p, int* queue, int64_t head_dim,
+                            int64_t block_size, hipStream_t s, const char* what) {
+  hipError_t err;
+  if (block_size == 64 && head_dim == 128) err = launch_prefill_bs64<128>(p, queue, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_prefill_bs64<64>(p, queue, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_prefill<32, 128>(p, s);
+  else if (block_size == 32 && head_dim == 64) err = launch_prefill<32, 64>(p, s);
+  else if (block_size == 128 && head_dim == 128) err = launch_prefill<128, 128>(p, s);
+  else err = launch_prefill<128, 64>(p, s);
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "%s: launch failed: %s", what, hipGetErrorString(err));
+  return kOk;
+}
+
 extern "C" size_t tasft_bsfa_prefill_workspace_bytes(int64_t batch, int64_t num_q_heads,
                                                      int64_t seq_len, int64_t block_size) {
   if (batch <= 0 || num_q_heads <= 0 || seq_len <= 0 || block_size <= 0) return 0;
@@ -1024,17 +1073,84 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   p.queue = nullptr;
   p.parts = 1;
   p.wg_per_part = 1;
+  p.cu_seqlens = nullptr;
+  // Ticket counters of the persistent launch (block size 64).
+  return dispatch_prefill(p, (int*)workspace, head_dim, block_size, (hipStream_t)stream,
+                          "prefill");
+}
 
-  hipStream_t s = (hipStream_t)stream;
-  hipError_t err;
-  int* queue = (int*)workspace;  // ticket counters of the persistent launch (block size 64)
-  if (block_size == 64 && head_dim == 128) err = launch_prefill_bs64<128>(p, queue, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_prefill_bs64<64>(p, queue, s);
-  else if (block_size == 32 && head_dim == 128) err = launch_prefill<32, 128>(p, s);
-  else if (block_size == 32 && head_dim == 64) err = launch_prefill<32, 64>(p, s);
-  else if (block_size == 128 && head_dim == 128) err = launch_prefill<128, 128>(p, s);
-  else err = launch_prefill<128, 64>(p, s);
-  if (err != hipSuccess)
-    return set_error(kErrLaunch, "prefill: launch failed: %s", hipGetErrorString(err));
-  return kOk;
+extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const void* v,
+                                             void* out, const uint8_t* block_mask,
+                                             const int32_t* cu_seqlens, int64_t num_seqs,
+                                             int64_t num_q_heads, int64_t num_kv_heads,
+                                             int64_t max_seqlen, int64_t head_dim,
+                                             int64_t block_size, const int64_t* q_strides,
+                                             const int64_t* k_strides, const int64_t* v_strides,
+                                             const int64_t* o_strides,
+                                             const int64_t* mask_strides, float scale, int causal,
+                                             void* stream) {
+  if (!q || !k || !v || !out || !block_mask || !cu_seqlens || !q_strides || !k_strides ||
+      !v_strides || !o_strides || !mask_strides)
+    return set_error(kErrInvalidArgument, "prefill_varlen: null pointer argument");
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seqlen <= 0)
+    return set_error(kErrInvalidArgument,
+                     "prefill_varlen: num_seqs, heads and max_seqlen must be positive");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument,
+                     "prefill_varlen: num_q_heads (%lld) must be a multiple of num_kv_heads (%lld)",
+                     (long long)num_q_heads, (long long)num_kv_heads);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(kErrUnsupported, "prefill_varlen: head_dim must be 64 or 128, got %lld",
+                     (long long)head_dim);
+  if (block_size != 32 && block_size != 64 && block_size != 128)
+    return set_error(kErrUnsupported, "prefill_varlen: block_size must be 32, 64 or 128, got %lld",
+                     (long long)block_size);
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  for (int i = 0; i < 4; ++i) {
+    if (st[i][2] != 1)
+      return set_error(kErrInvalidArgument,
+                       "prefill_varlen: head_dim must be the contiguous dimension");
+    for (int j = 0; j < 2; ++j)
+      if (st[i][j] % 8 != 0)
+        return set_error(kErrInvalidArgument,
+                         "prefill_varlen: strides must be multiples of 8 elements (16-byte rows)");
+  }
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return set_error(kErrInvalidArgument, "prefill_varlen: tensors must be 16-byte aligned");
+  const int64_t nb = (max_seqlen + block_size - 1) / block_size;
+  if (nb * num_seqs * num_q_heads > 0x7fffffffLL || max_seqlen > 0x3fffffffLL)
+    return set_error(kErrUnsupported, "prefill_varlen: problem too large for one launch");
+
+  PrefillParams p;
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v;
+  p.o = (uint16_t*)out;
+  p.mask = block_mask;
+  // Packed [tokens, heads, D]: no batch stride; the kernels add cu_seqlens[b] tokens.
+  const int64_t* src[4] = {q_strides, k_strides, v_strides, o_strides};
+  int64_t* dst[4] = {p.sq, p.sk, p.sv, p.so};
+  for (int i = 0; i < 4; ++i) {
+    dst[i][0] = 0;
+    dst[i][1] = src[i][1];
+    dst[i][2] = src[i][0];
+  }
+  for (int j = 0; j < 4; ++j) p.sm[j] = mask_strides[j];
+  p.B = (int)num_seqs;
+  p.Hq = (int)num_q_heads;
+  p.Hkv = (int)num_kv_heads;
+  p.G = (int)(num_q_heads / num_kv_heads);
+  p.S = (int)max_seqlen;
+  p.NB = (int)nb;
+  p.scale_log2 = scale * kLog2e;
+  p.causal = causal ? 1 : 0;
+  p.small_spans = (max_seqlen * k_strides[0] * 2 < 0x7fffffffLL &&
+                   max_seqlen * v_strides[0] * 2 < 0x7fffffffLL) ? 1 : 0;
+  p.queue = nullptr;
+  p.parts = 1;
+  p.wg_per_part = 1;
+  p.cu_seqlens = cu_seqlens;
+  // One workgroup per (sequence, head, query block); never the persistent loop.
+  return dispatch_prefill(p, nullptr, head_dim, block_size, (hipStream_t)stream,
+                          "prefill_varlen");
 }

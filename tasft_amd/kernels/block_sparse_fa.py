@@ -262,6 +262,119 @@ class BlockSparseFlashAttention:
         gqa = k.shape[1] != q.shape[1]
         return functional.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa)
 
+    # ------------------------------------------------------------------ varlen prefill
+    def forward_varlen(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        block_mask: torch.Tensor,
+        cu_seqlens: torch.Tensor,
+        max_seqlen: int | None = None,
+        *,
+        causal: bool = True,
+    ) -> torch.Tensor:
+        """Block-sparse prefill of a packed batch of variable-length sequences (one launch).
+
+        The reference's vLLM backend views all packed tokens as one sequence
+        (``tasft/inference/vllm_patch.py:172-176``), so a request also attends to the
+        requests packed before it; here each sequence attends only within itself, with the
+        semantics of ``forward`` per sequence. There is no low-sparsity dense fallback.
+
+        Args:
+            q: ``[T, Hq, D]`` bf16 packed queries; k, v: ``[T, Hkv, D]`` bf16, ``Hq % Hkv == 0``.
+            block_mask: ``[N, Hq, NB, NB]`` with ``NB = ceil(max_seqlen / block_size)``;
+                sequence n uses its leading ``ceil(len_n / block_size)`` square.
+            cu_seqlens: ``[N + 1]`` int32 cumulative lengths (``cu_seqlens[0] == 0``,
+                non-decreasing, ``cu_seqlens[N] <= T``). On the CPU it is checked here and
+                copied to the device; on the device it is trusted (no synchronisation),
+                and ``max_seqlen`` must be given.
+            max_seqlen: the longest sequence (default: from a CPU ``cu_seqlens``).
+            causal: causal masking within each sequence.
+
+        Returns:
+            ``[T, Hq, D]``; rows of tokens after ``cu_seqlens[N]`` are 0.
+        """
+        if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+            raise KernelError(
+                "Expected packed q, k, v of shape [T, H, D]",
+                context={"q_shape": list(q.shape), "k_shape": list(k.shape), "v_shape": list(v.shape)},
+            )
+        T, H, D = q.shape
+        if k.shape != v.shape or k.shape[0] != T or k.shape[2] != D or k.shape[1] <= 0 or H % k.shape[1] != 0:
+            raise KernelError(
+                f"K/V must be [T, Hkv, D] with Hq % Hkv == 0; got q {tuple(q.shape)}, "
+                f"k {tuple(k.shape)}, v {tuple(v.shape)}",
+                context={"q_shape": list(q.shape), "k_shape": list(k.shape), "v_shape": list(v.shape)},
+            )
+        if D not in _VALID_HEAD_DIMS:
+            raise KernelError(
+                f"HIP kernel supports head_dim in {sorted(_VALID_HEAD_DIMS)}, got {D}",
+                context={"head_dim": D, "supported": sorted(_VALID_HEAD_DIMS)},
+            )
+        if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+            raise KernelError("cu_seqlens must be a 1-D tensor of N + 1 >= 2 offsets",
+                              context={"cu_seqlens_shape": list(cu_seqlens.shape)})
+        n_seq = cu_seqlens.numel() - 1
+        if cu_seqlens.device.type == "cpu":
+            cu = cu_seqlens.to(torch.int64)
+            lens = cu[1:] - cu[:-1]
+            if int(cu[0]) != 0 or bool((lens < 0).any()) or int(cu[-1]) > T:
+                raise KernelError(
+                    "cu_seqlens must start at 0, be non-decreasing and end at <= T",
+                    context={"cu_seqlens": cu.tolist()[:16], "T": T},
+                )
+            longest = int(lens.max())
+            if max_seqlen is None:
+                max_seqlen = max(longest, 1)
+            elif longest > max_seqlen:
+                raise KernelError(
+                    f"a sequence has {longest} tokens, more than max_seqlen={max_seqlen}",
+                    context={"max_seqlen": max_seqlen, "longest": longest},
+                )
+            covered = int(cu[-1])
+        else:
+            if max_seqlen is None:
+                raise KernelError("max_seqlen is required when cu_seqlens is on the device",
+                                  context={"device": str(cu_seqlens.device)})
+            covered = -1  # unknown without a synchronisation
+        if max_seqlen <= 0:
+            raise KernelError(f"max_seqlen must be positive, got {max_seqlen}",
+                              context={"max_seqlen": max_seqlen})
+        nb = math.ceil(max_seqlen / self.block_size)
+        expected = (n_seq, H, nb, nb)
+        if tuple(block_mask.shape) != expected:
+            raise KernelError(
+                f"block_mask shape mismatch: expected {expected}, got {tuple(block_mask.shape)}",
+                context={"expected": list(expected), "got": list(block_mask.shape)},
+            )
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if t.dtype != torch.bfloat16:
+                raise KernelError(
+                    f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
+                    context={"tensor": name, "dtype": str(t.dtype)},
+                )
+            if not t.is_cuda or t.device != q.device:
+                raise KernelError("Q, K, V must be on the same GPU device",
+                                  context={"tensor": name, "device": str(t.device)})
+        lib = _native.load_library()
+        q = _kernel_ready(q)
+        k = _kernel_ready(k)
+        v = _kernel_ready(v)
+        mask = _mask_bytes(block_mask.to(q.device))
+        cu_dev = cu_seqlens.to(device=q.device, dtype=torch.int32)
+        out = (torch.empty_like(q) if covered == T else torch.zeros_like(q))
+        status = lib.tasft_bsfa_prefill_varlen_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
+            cu_dev.data_ptr(), n_seq, H, k.shape[1], max_seqlen, D, self.block_size,
+            _native.strides(q), _native.strides(k), _native.strides(v), _native.strides(out),
+            _native.strides(mask), 1.0 / math.sqrt(D), 1 if causal else 0,
+            _native.stream_handle(q.device),
+        )
+        _native.check(status, "tasft_bsfa_prefill_varlen_fwd",
+                      {"tokens": T, "sequences": n_seq, "max_seqlen": max_seqlen})
+        return out
+
     # ------------------------------------------------------------------ decode
     def forward_decode(
         self,

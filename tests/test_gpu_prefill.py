@@ -193,3 +193,61 @@ def test_persistent_queue_is_bit_identical(B, Hq, Hkv, S, bs):
     ref = orc.attention_block_gather(to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu()),
                                      mask.cpu().numpy(), bs, True)
     assert_close_bf16(out_ws, ref, "persistent prefill")
+
+
+# ----------------------------------------------------------------------------- varlen
+def _packed(lens, Hq, Hkv, D, seed, pad=5):
+    """Packed bf16 q [T, Hq, D], k/v [T, Hkv, D] (T = sum(lens) + pad) and cu_seqlens."""
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens) + pad
+    q = (torch.randn(T, Hq, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    k = (torch.randn(T, Hkv, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    v = (torch.randn(T, Hkv, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    return q, k, v, cu
+
+
+VARLEN_CASES = [
+    # lengths, Hq, Hkv, D, bs, causal, density
+    ([100, 0, 257, 64, 1], 8, 2, 128, 64, True, 0.5),   # two-wave kernel; empty and 1-token
+    ([300, 45, 128], 4, 4, 64, 64, True, 0.5),          # four-wave kernel (D=64)
+    ([130, 77], 4, 2, 64, 32, False, 0.6),              # generic kernel, non-causal
+    ([513, 200], 7, 1, 128, 128, True, 0.4),            # bs=128, G=7
+]
+
+
+@pytest.mark.parametrize(("lens", "Hq", "Hkv", "D", "bs", "causal", "density"), VARLEN_CASES)
+def test_prefill_varlen_matches_oracle(lens, Hq, Hkv, D, bs, causal, density):
+    dev = require_gpu()
+    print(f"varlen lens={lens} Hq={Hq} Hkv={Hkv} D={D} bs={bs} causal={causal}", flush=True)
+    q, k, v, cu = _packed(lens, Hq, Hkv, D, 6100 + sum(lens))
+    nb = math.ceil(max(lens) / bs)
+    g = torch.Generator().manual_seed(6200 + sum(lens))
+    mask = torch.rand((len(lens), Hq, nb, nb), generator=g) < density
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward_varlen(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                              torch.tensor(cu, dtype=torch.int32), causal=causal)
+    torch.cuda.synchronize()
+    ref = orc.attention_varlen(to_np(q), to_np(k), to_np(v), cu, mask.numpy(), bs, causal)
+    assert_close_bf16(out, ref, f"varlen prefill {lens}")
+    assert (out[cu[-1]:] == 0).all()
+
+
+def test_prefill_varlen_one_sequence_is_bit_identical_to_forward():
+    """One packed sequence runs the same kernel arithmetic as the dense call on the
+    [1, H, T, D] view of the same memory (the reference's flat-token layout)."""
+    dev = require_gpu()
+    T, Hq, Hkv, D, bs = 1000, 8, 2, 128, 64
+    q, k, v, cu = _packed([T], Hq, Hkv, D, 6300, pad=0)
+    mask = wl.bernoulli_causal_mask(wl.Shape(1, Hq, Hkv, T, D, bs), 0.3, 6301)
+    q, k, v, mask = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    dense = bsfa.forward(q.transpose(0, 1)[None], k.transpose(0, 1)[None],
+                         v.transpose(0, 1)[None], mask, causal=True)
+    # cu_seqlens on the device: no host check, max_seqlen given.
+    packed = bsfa.forward_varlen(q, k, v, mask, torch.tensor(cu, dtype=torch.int32, device=dev),
+                                 max_seqlen=T, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, dense[0].transpose(0, 1))

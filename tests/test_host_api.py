@@ -199,3 +199,37 @@ class TestGateTargetDense:
     def test_block_size_zero(self):
         with pytest.raises(ValueError, match="block_size must be > 0"):
             TASFTObjective.compute_gate_target(torch.randn(1, 1, 4, 4), block_size=0)
+
+
+# ----------------------------------------------------------------------------- varlen validation
+def _varlen_args(T=40, H=4, Hkv=2, D=64):
+    q = torch.zeros(T, H, D, dtype=torch.bfloat16)
+    k = torch.zeros(T, Hkv, D, dtype=torch.bfloat16)
+    return q, k, k.clone()
+
+
+def test_forward_varlen_validates_before_any_launch():
+    bsfa = BlockSparseFlashAttention(block_size=32, min_sparsity_for_speedup=0.0)
+    q, k, v = _varlen_args()
+    mask = torch.ones(2, 4, 1, 1, dtype=torch.bool)
+    with pytest.raises(KernelError, match=r"packed q, k, v of shape \[T, H, D\]"):
+        bsfa.forward_varlen(q[None], k, v, mask, torch.tensor([0, 10, 30], dtype=torch.int32))
+    with pytest.raises(KernelError, match="Hq % Hkv == 0"):
+        bsfa.forward_varlen(q, k[:, :1].expand(40, 3, 64), v, mask, torch.tensor([0, 10, 30]))
+    with pytest.raises(KernelError, match="start at 0"):
+        bsfa.forward_varlen(q, k, v, mask, torch.tensor([1, 10, 30], dtype=torch.int32))
+    with pytest.raises(KernelError, match="non-decreasing"):
+        bsfa.forward_varlen(q, k, v, mask, torch.tensor([0, 20, 10], dtype=torch.int32))
+    with pytest.raises(KernelError, match="end at <= T"):
+        bsfa.forward_varlen(q, k, v, mask, torch.tensor([0, 20, 41], dtype=torch.int32))
+    with pytest.raises(KernelError, match="more than max_seqlen"):
+        bsfa.forward_varlen(q, k, v, mask, torch.tensor([0, 10, 30], dtype=torch.int32), 16)
+    with pytest.raises(KernelError, match="block_mask shape mismatch"):
+        bsfa.forward_varlen(q, k, v, torch.ones(2, 4, 2, 2, dtype=torch.bool),
+                            torch.tensor([0, 10, 30], dtype=torch.int32))
+    with pytest.raises(KernelError, match="head_dim"):
+        q2, k2, v2 = _varlen_args(D=32)
+        bsfa.forward_varlen(q2, k2, v2, mask, torch.tensor([0, 10, 30], dtype=torch.int32))
+    # valid arguments on CPU tensors stop at the device check, before the library
+    with pytest.raises(KernelError, match="same GPU device"):
+        bsfa.forward_varlen(q, k, v, mask, torch.tensor([0, 10, 30], dtype=torch.int32))

@@ -209,6 +209,53 @@ def test_attention_gather_equals_dense_masked_gqa():
     np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_varlen_equals_block_diagonal_dense(causal):
+    """Packed sequences == one dense masked attention over all tokens whose token mask is
+    block-diagonal by sequence (built here element by element, not by the oracle)."""
+    rng = np.random.default_rng(21)
+    Hq, Hkv, D, bs = 4, 2, 16, 32
+    cu = [0, 37, 37, 130, 200]  # an empty and a ragged sequence; tokens 200..207 unused
+    T = 208
+    nbmax = 4
+    q = rng.standard_normal((T, Hq, D)).astype(np.float32)
+    k = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    mask = rng.random((len(cu) - 1, Hq, nbmax, nbmax)) < 0.6
+    got = orc.attention_varlen(q, k, v, cu, mask, bs, causal, dtype=np.float64)
+    ref = np.zeros((T, Hq, D))
+    sc = 1 / math.sqrt(D)
+    for h in range(Hq):
+        allow = np.zeros((T, T), dtype=bool)
+        for n in range(len(cu) - 1):
+            for i in range(cu[n], cu[n + 1]):
+                for j in range(cu[n], cu[n + 1]):
+                    bi, bj = (i - cu[n]) // bs, (j - cu[n]) // bs
+                    allow[i, j] = mask[n, h, bi, bj] and (not causal or j <= i)
+        sco = (q[:, h].astype(np.float64) @ k[:, h // 2].astype(np.float64).T) * sc
+        for i in range(T):
+            if allow[i].any():
+                row = np.where(allow[i], sco[i], -np.inf)
+                p_ = np.exp(row - row.max())
+                ref[i, h] = (p_ / p_.sum()) @ v[:, h // 2].astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-12)
+    assert (got[200:] == 0).all()
+
+
+def test_attention_varlen_single_sequence_is_flat_token_call():
+    """One packed sequence is the reference's flat-token view (B = 1, vllm_patch.py:172-176)."""
+    rng = np.random.default_rng(22)
+    T, Hq, Hkv, D, bs = 150, 4, 1, 8, 64
+    q = rng.standard_normal((T, Hq, D)).astype(np.float32)
+    k = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    mask = rng.random((1, Hq, 3, 3)) < 0.7
+    got = orc.attention_varlen(q, k, v, [0, T], mask, bs, True, dtype=np.float64)
+    flat = orc.attention_dense_masked(q.transpose(1, 0, 2)[None], k.transpose(1, 0, 2)[None],
+                                      v.transpose(1, 0, 2)[None], mask, bs, True, dtype=np.float64)
+    np.testing.assert_allclose(got, flat[0].transpose(1, 0, 2), rtol=1e-10, atol=1e-12)
+
+
 # ----------------------------------------------------------------------------- decode
 def test_decode_equals_last_prefill_row_and_brute_force():
     rng = np.random.default_rng(9)
