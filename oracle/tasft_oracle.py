@@ -17,6 +17,8 @@ asks for float64. How each function is pinned (checked independently of itself):
   pure-Python loop implementation on tiny inputs.
 * ``attention_block_gather``: equals ``attention_dense_masked``.
 * ``sparse_decode``: equals the last row of ``attention_block_gather``; brute force.
+* ``sparse_decode_paged``: equals ``sparse_decode`` on the contiguous cache from which the
+  test scatters the page pools through a random page permutation.
 * ``attention_varlen``: equals ``attention_dense_masked`` over the whole packed token
   range with an independently built block-diagonal token mask (tests/test_oracle.py), and
   with one sequence equals the reference's flat-token call (B = 1).
@@ -257,6 +259,27 @@ def sparse_decode(q, k_cache, v_cache, block_mask, bs: int, kv_lens=None,
 
 
 # ----------------------------------------------------------------------------- gate target
+def sparse_decode_paged(q, k_pages, v_pages, block_table, kv_lens, block_mask, bs: int,
+                        scale: float | None = None, dtype: type = np.float32) -> np.ndarray:
+    """Sparse decode over a paged cache: gather each sequence's tokens, then ``sparse_decode``.
+
+    Pools ``[pages, page_size, Hkv, D]`` in vLLM's block-table layout (the cache that
+    tasft/inference/vllm_patch.py:189-196 hands to PagedAttention): token t of sequence b
+    is row ``t % page_size`` of page ``block_table[b, t // page_size]``.
+    """
+    b_ = q.shape[0]
+    ps, hkv, d = k_pages.shape[1], k_pages.shape[2], k_pages.shape[3]
+    s_kv = block_mask.shape[-1] * bs
+    k = np.zeros((b_, hkv, s_kv, d), dtype=k_pages.dtype)
+    v = np.zeros((b_, hkv, s_kv, d), dtype=v_pages.dtype)
+    for b in range(b_):
+        for t in range(int(kv_lens[b])):
+            page = int(block_table[b, t // ps])
+            k[b, :, t] = k_pages[page, t % ps]
+            v[b, :, t] = v_pages[page, t % ps]
+    return sparse_decode(q, k, v, block_mask, bs, kv_lens, scale, dtype)
+
+
 def _softmax(x: np.ndarray, axis: int) -> np.ndarray:
     mx = x.max(axis=axis, keepdims=True)
     e = np.exp(x - mx)

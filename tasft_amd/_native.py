@@ -25,6 +25,7 @@ EXPORTED_SYMBOLS = (
     "tasft_bsfa_prefill_varlen_fwd",
     "tasft_bsfa_decode_workspace_bytes",
     "tasft_bsfa_decode_fwd",
+    "tasft_bsfa_decode_paged_fwd",
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
     "tasft_gate_target_fwd",
@@ -62,6 +63,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64P, _I64P, _I64P, _I64P, _I64P, _F, _P],
+    ),
+    "tasft_bsfa_decode_paged_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64P, _I64P, _I64P, _I64P, _I64P, _I64, _F, _P],
     ),
     "tasft_gate_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_fwd": (

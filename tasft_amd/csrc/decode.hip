@@ -40,6 +40,12 @@ struct DecodeParams {
   int64_t sq[2], sk[3], sv[3], so[2], sm[3];
   int B, Hq, Hkv, G, S_kv, NB, P;
   float scale_log2;
+  // Paged cache (kernels instantiated with PAGED): K/V are page pools whose strides sk, sv
+  // are (page, head, token); token t of sequence b lives in page
+  // block_table[b * bt_stride + t / page_size], row t % page_size.
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int page_size;
 };
 
 // Raw buffer resource (stride 0) over `bytes` bytes starting at `base`.
@@ -67,9 +73,10 @@ __device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int voff
 // SUB keys (<= 64) of one KV block are processed at a time; a block of BS keys is
 // BS/SUB sub-blocks. MG >= G is the head count the loops are unrolled for (padding heads
 // carry zero probability).
-template <int BS, int D, int MG>
+template <int BS, int D, int MG, bool PAGED = false>
 __global__ void __launch_bounds__(kDecodeWaves * kWave, 2)
 bsfa_decode_split_kernel(const DecodeParams p) {
+  static_assert(!PAGED || BS <= 64, "paged caches use the one-sub-block path");
   constexpr int SUB = BS < 64 ? BS : 64;
   constexpr int NSUB = BS / SUB;
   constexpr int KT = SUB / 32;        // 32-key MFMA tiles per sub-block
@@ -136,8 +143,8 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   }
   __syncthreads();
 
-  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
-  const uint16_t* vbase = p.v + b * p.sv[0] + kvh * p.sv[1];
+  const uint16_t* kbase = PAGED ? p.k + kvh * p.sk[1] : p.k + b * p.sk[0] + kvh * p.sk[1];
+  const uint16_t* vbase = PAGED ? p.v + kvh * p.sv[1] : p.v + b * p.sv[0] + kvh * p.sv[1];
   const int ks2 = (int)p.sk[2], vs2 = (int)p.sv[2];  // row strides (elements)
 
   // QK-layout state of this lane's head (identical in lanes l and l^32).
@@ -206,7 +213,50 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     const int nsel = __builtin_amdgcn_readfirstlane(min(end, base) - start);
     constexpr int NKL = KT * KSTEPS;  // K load instructions per block
     u32x4_t ka[KT][KSTEPS];
-    auto load_k = [&](int kb) {
+    // Paged cache: lane j < npg of `pgv` holds the page of the block's j-th page-sized
+    // piece (one block ahead of use, so its load is covered by the fixed V wait). A block
+    // of BS keys starts at row off0 of its first page.
+    constexpr int RPU_ = 1024 / (D * 2);
+    const int ps = p.page_size;
+    const int npg = ps >= BS ? 1 : BS / ps;
+    auto load_pg = [&](int kb) -> int {
+      const int first = (kb * BS) / ps;
+      // Only pages that hold a token below kv_len are read (later entries may not exist).
+      const int jmax = (kv_len - 1 - kb * BS + (kb * BS) % ps) / ps;
+      return p.block_table[(int64_t)b * p.bt_stride + first + min(lane < npg ? lane : 0, jmax)];
+    };
+    auto load_k_paged = [&](int kb, int pgv) {
+      const int key0 = kb * BS;
+      const int off0 = key0 % ps;
+      const int last = kv_len - 1 - key0;  // rows past it read row kv_len-1 (masked)
+#pragma unroll
+      for (int t2 = 0; t2 < KT; ++t2) {
+        const int row = min(t2 * 32 + col, last) + off0;
+        const int page = __shfl(pgv, row / ps, kWave);
+        const uint16_t* src = kbase + (int64_t)page * p.sk[0] + (int64_t)(row % ps) * ks2 + half * 8;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) ka[t2][ks] = *(const u32x4_t*)(src + ks * 16);
+      }
+    };
+    auto dma_v_paged = [&](int kb, int pgv) {
+      const int key0 = kb * BS;
+      const int off0 = key0 % ps;
+#pragma unroll
+      for (int u = 0; u < VTILE / 1024; ++u) {
+        // Unit u covers rows u*RPU_ .. +RPU_-1 of the block, inside one page (ps % RPU_ == 0).
+        const int row = u * RPU_ + off0;
+        const int page = __builtin_amdgcn_readlane(pgv, row / ps);
+        const int rows = min(RPU_, kv_len - key0 - u * RPU_);
+        const __amdgpu_buffer_rsrc_t vr = decode_rsrc(
+            vbase + (int64_t)page * p.sv[0] + (int64_t)(row % ps) * vs2, (int64_t)max(rows, 0) * vs2 * 2);
+        dma16(vr, v_lds[wave] + u * 1024, v_dma_base);
+      }
+    };
+    auto load_k = [&](int kb, int pgv) {
+      if constexpr (PAGED) {
+        load_k_paged(kb, pgv);
+        return;
+      }
       const int key0 = kb * BS;
       const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)SUB * ks2 * 2);
       if (key0 + SUB <= kv_len) {
@@ -228,7 +278,11 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         }
       }
     };
-    auto dma_v = [&](int kb) {
+    auto dma_v = [&](int kb, int pgv) {
+      if constexpr (PAGED) {
+        dma_v_paged(kb, pgv);
+        return;
+      }
       const int key0 = kb * BS;
       // The resource ends at row kv_len-1, so rows past kv_len arrive as zeros.
       const __amdgpu_buffer_rsrc_t vr =
@@ -237,10 +291,16 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       for (int u = 0; u < VTILE / 1024; ++u) dma16(vr, v_lds[wave] + u * 1024, v_dma_base + u * v_unit_stride);
     };
     int e = wave;
+    int pg_n = 0;  // pages of the next block (paged cache)
     if (e < nsel) {
       const int t0 = __builtin_amdgcn_readfirstlane((int)sel[e]);
-      load_k(t0);
-      dma_v(t0);
+      const int pg0 = PAGED ? load_pg(t0) : 0;
+      if constexpr (PAGED) {
+        const int e1 = e + kDecodeWaves;
+        pg_n = load_pg(e1 < nsel ? __builtin_amdgcn_readfirstlane((int)sel[e1]) : t0);
+      }
+      load_k(t0, pg0);
+      dma_v(t0, pg0);
     }
     while (e < nsel) {
       const int kb = __builtin_amdgcn_readfirstlane(sel[e]);
@@ -260,7 +320,14 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       const int en = e + kDecodeWaves;
       const bool more = en < nsel;
       const int tn = more ? __builtin_amdgcn_readfirstlane((int)sel[en]) : 0;
-      if (more) load_k(tn);
+      int pg_nn = 0;
+      if constexpr (PAGED) {
+        // Pages of the block after the next, issued before the next block's K loads so
+        // the fixed V wait below also covers them.
+        const int enn = en + kDecodeWaves;
+        pg_nn = load_pg(enn < nsel ? __builtin_amdgcn_readfirstlane((int)sel[enn]) : kb);
+      }
+      if (more) load_k(tn, pg_n);
       // Register r of tile t2 holds key t2*32 + 8*(r/4) + 4*half + r%4 of head `col`.
       float mx = -INFINITY;
 #pragma unroll
@@ -326,8 +393,9 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         // The DMA writes the V tile through the memory path: every LDS read of it must
         // have returned first.
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-        dma_v(tn);
+        dma_v(tn, pg_n);
       }
+      pg_n = pg_nn;
       e = en;
     }
   } else {
@@ -523,10 +591,10 @@ bsfa_decode_combine_kernel(const DecodeParams p) {
   p.o[b * p.so[0] + h * p.so[1] + d] = __builtin_bit_cast(uint16_t, rb);
 }
 
-template <int BS, int D, int MG>
+template <int BS, int D, int MG, bool PAGED = false>
 static hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.B * p.Hkv * p.P;
-  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG, PAGED>), dim3((unsigned)grid),
                      dim3(kDecodeWaves * kWave), 0, stream, p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.P == 1) return err;
@@ -535,12 +603,12 @@ static hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int BS, int D>
+template <int BS, int D, bool PAGED = false>
 static hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
-  if (p.G <= 1) return launch_decode_g<BS, D, 1>(p, stream);
-  if (p.G <= 2) return launch_decode_g<BS, D, 2>(p, stream);
-  if (p.G <= 4) return launch_decode_g<BS, D, 4>(p, stream);
-  return launch_decode_g<BS, D, 8>(p, stream);
+  if (p.G <= 1) return launch_decode_g<BS, D, 1, PAGED>(p, stream);
+  if (p.G <= 2) return launch_decode_g<BS, D, 2, PAGED>(p, stream);
+  if (p.G <= 4) return launch_decode_g<BS, D, 4, PAGED>(p, stream);
+  return launch_decode_g<BS, D, 8, PAGED>(p, stream);
 }
 
 }  // namespace tasft
@@ -630,6 +698,10 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
   p.P = (int)num_splits;
   p.scale_log2 = scale * kLog2e;
 
+  p.block_table = nullptr;
+  p.bt_stride = 0;
+  p.page_size = 0;
+
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
   if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128>(p, s);
@@ -640,5 +712,108 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
   else err = launch_decode<128, 64>(p, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "decode: launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}
+
+extern "C" int tasft_bsfa_decode_paged_fwd(
+    const void* q, const void* k_pages, const void* v_pages, void* out, const uint8_t* block_mask,
+    const int32_t* block_table, const int32_t* kv_lens, void* workspace, size_t workspace_bytes,
+    int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t kv_len_max,
+    int64_t head_dim, int64_t block_size, int64_t page_size, int64_t num_splits,
+    const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+    const int64_t* o_strides, const int64_t* mask_strides, int64_t block_table_stride,
+    float scale, void* stream) {
+  if (!q || !k_pages || !v_pages || !out || !block_mask || !block_table || !kv_lens ||
+      !workspace || !q_strides || !k_strides || !v_strides || !o_strides || !mask_strides)
+    return set_error(kErrInvalidArgument, "decode_paged: null pointer argument");
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || kv_len_max <= 0 || num_splits <= 0)
+    return set_error(kErrInvalidArgument, "decode_paged: sizes must be positive");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument,
+                     "decode_paged: num_q_heads must be a multiple of num_kv_heads");
+  const int64_t G = num_q_heads / num_kv_heads;
+  if (G > kDecodeMaxG)
+    return set_error(kErrUnsupported, "decode_paged: at most %d query heads per KV head, got %lld",
+                     kDecodeMaxG, (long long)G);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(kErrUnsupported, "decode_paged: head_dim must be 64 or 128, got %lld",
+                     (long long)head_dim);
+  if (block_size != 32 && block_size != 64)
+    return set_error(kErrUnsupported, "decode_paged: block_size must be 32 or 64, got %lld",
+                     (long long)block_size);
+  if (page_size < 8 || page_size > 4096 || (page_size & (page_size - 1)) != 0)
+    return set_error(kErrUnsupported,
+                     "decode_paged: page_size must be a power of two in [8, 4096], got %lld",
+                     (long long)page_size);
+  const int64_t nb = (kv_len_max + block_size - 1) / block_size;
+  if ((nb + num_splits - 1) / num_splits > kDecodeMaxRange)
+    return set_error(kErrInvalidArgument,
+                     "decode_paged: num_splits must be >= ceil(num_blocks / %d) (got %lld for %lld blocks)",
+                     kDecodeMaxRange, (long long)num_splits, (long long)nb);
+  const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+  if (workspace_bytes < need)
+    return set_error(kErrWorkspace, "decode_paged: workspace too small: need %zu bytes, got %zu",
+                     need, workspace_bytes);
+  // q, out [B, Hq, 1, D]; K/V pools [pages, page_size, Hkv, D].
+  if (q_strides[3] != 1 || k_strides[3] != 1 || v_strides[3] != 1 || o_strides[3] != 1)
+    return set_error(kErrInvalidArgument, "decode_paged: head_dim must be the contiguous dimension");
+  for (int j = 0; j < 3; ++j)
+    if (k_strides[j] % 8 != 0 || v_strides[j] % 8 != 0)
+      return set_error(kErrInvalidArgument,
+                       "decode_paged: K/V strides must be multiples of 8 elements");
+  if (q_strides[0] % 8 != 0 || q_strides[1] % 8 != 0)
+    return set_error(kErrInvalidArgument, "decode_paged: q strides must be multiples of 8 elements");
+  if ((((uintptr_t)q) & 15u) || (((uintptr_t)k_pages) & 15u) || (((uintptr_t)v_pages) & 15u) ||
+      (((uintptr_t)workspace) & 15u))
+    return set_error(kErrInvalidArgument,
+                     "decode_paged: q, K/V pools and workspace must be 16-byte aligned");
+  if (batch * num_kv_heads * num_splits > 0x7fffffffLL || kv_len_max > 0x3fffffffLL ||
+      page_size * k_strides[1] * 2 > 0x7fffffffLL || page_size * v_strides[1] * 2 > 0x7fffffffLL)
+    return set_error(kErrUnsupported, "decode_paged: problem too large for one launch");
+
+  DecodeParams p;
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k_pages;
+  p.v = (const uint16_t*)v_pages;
+  p.o = (uint16_t*)out;
+  p.mask = block_mask;
+  p.kv_lens = kv_lens;
+  const size_t o_bytes = (size_t)(batch * num_q_heads * num_splits) * head_dim * sizeof(float);
+  p.ws_o = (float*)workspace;
+  p.ws_ml = (float*)((char*)workspace + o_bytes);
+  p.sq[0] = q_strides[0];
+  p.sq[1] = q_strides[1];
+  p.so[0] = o_strides[0];
+  p.so[1] = o_strides[1];
+  // (page, head, token) strides of the pools.
+  p.sk[0] = k_strides[0];
+  p.sk[1] = k_strides[2];
+  p.sk[2] = k_strides[1];
+  p.sv[0] = v_strides[0];
+  p.sv[1] = v_strides[2];
+  p.sv[2] = v_strides[1];
+  p.sm[0] = mask_strides[0];
+  p.sm[1] = mask_strides[1];
+  p.sm[2] = mask_strides[3];
+  p.B = (int)batch;
+  p.Hq = (int)num_q_heads;
+  p.Hkv = (int)num_kv_heads;
+  p.G = (int)G;
+  p.S_kv = (int)kv_len_max;
+  p.NB = (int)nb;
+  p.P = (int)num_splits;
+  p.scale_log2 = scale * kLog2e;
+  p.block_table = block_table;
+  p.bt_stride = block_table_stride;
+  p.page_size = (int)page_size;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t err;
+  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128, true>(p, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64, true>(p, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128, true>(p, s);
+  else err = launch_decode<32, 64, true>(p, s);
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "decode_paged: launch failed: %s", hipGetErrorString(err));
   return kOk;
 }

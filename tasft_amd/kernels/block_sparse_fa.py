@@ -478,6 +478,118 @@ class BlockSparseFlashAttention:
         return out
 
     # ------------------------------------------------------------------ stats
+    def forward_decode_paged(
+        self,
+        q: torch.Tensor,
+        k_pages: torch.Tensor,
+        v_pages: torch.Tensor,
+        block_table: torch.Tensor,
+        kv_lens: torch.Tensor,
+        block_mask: torch.Tensor | None = None,
+        *,
+        block_indices: torch.Tensor | None = None,
+        num_splits: int | None = None,
+    ) -> torch.Tensor:
+        """Block-sparse decode over a paged KV cache (vLLM's block-table layout).
+
+        The reference hands paged decode to vLLM's dense PagedAttention
+        (``tasft/inference/vllm_patch.py:189-196, 215-252``); this reads only the selected
+        key blocks, through the block table, with the result of ``forward_decode`` on the
+        equivalent contiguous cache.
+
+        Args:
+            q: ``[B, Hq, 1, D]`` bf16.
+            k_pages, v_pages: ``[num_pages, page_size, Hkv, D]`` bf16 page pools; token t of
+                sequence b is row ``t % page_size`` of page ``block_table[b, t // page_size]``.
+            block_table: ``[B, max_pages]`` int32 on the device; only the pages holding a
+                token below ``kv_lens[b]`` are read.
+            kv_lens: ``[B]`` int32 valid lengths (on the device).
+            block_mask: ``[B, Hq, 1, NB]`` with ``NB = ceil(max_pages * page_size / block_size)``.
+            block_indices: instead of ``block_mask``, ``[B, Hq, K]`` index lists (``-1`` empty).
+            num_splits: split-K factor (default: sized so the launch fills the GPU).
+
+        Returns:
+            ``[B, Hq, 1, D]``.
+        """
+        if q.ndim != _EXPECTED_TENSOR_NDIM or q.shape[2] != 1:
+            raise KernelError(f"Expected q of shape [B, H, 1, D], got {tuple(q.shape)}",
+                              context={"q_shape": list(q.shape)})
+        B, H, _, D = q.shape
+        if (
+            k_pages.ndim != _EXPECTED_TENSOR_NDIM
+            or k_pages.shape != v_pages.shape
+            or k_pages.shape[3] != D
+            or H % k_pages.shape[2] != 0
+        ):
+            raise KernelError(
+                "page pools must be [num_pages, page_size, Hkv, D] with Hq % Hkv == 0",
+                context={"q": list(q.shape), "k": list(k_pages.shape), "v": list(v_pages.shape)},
+            )
+        page_size, Hkv = k_pages.shape[1], k_pages.shape[2]
+        if block_table.ndim != 2 or block_table.shape[0] != B:
+            raise KernelError(f"block_table must have shape [{B}, max_pages], got {tuple(block_table.shape)}",
+                              context={"block_table": list(block_table.shape)})
+        if kv_lens.shape != (B,):
+            raise KernelError(f"kv_lens must have shape ({B},), got {tuple(kv_lens.shape)}",
+                              context={"kv_lens": list(kv_lens.shape)})
+        if self.block_size not in (32, 64):
+            raise KernelError(f"paged decode supports block_size 32 or 64, got {self.block_size}",
+                              context={"block_size": self.block_size})
+        if page_size < 8 or page_size & (page_size - 1):
+            raise KernelError(f"page_size must be a power of two >= 8, got {page_size}",
+                              context={"page_size": page_size})
+        if D not in _VALID_HEAD_DIMS:
+            raise KernelError(f"HIP kernel supports head_dim in {sorted(_VALID_HEAD_DIMS)}, got {D}",
+                              context={"head_dim": D})
+        S_kv = block_table.shape[1] * page_size
+        nb = math.ceil(S_kv / self.block_size)
+        if (block_mask is None) == (block_indices is None):
+            raise KernelError("Pass exactly one of block_mask and block_indices",
+                              context={"block_mask": block_mask is not None,
+                                       "block_indices": block_indices is not None})
+        for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages)):
+            if t.dtype != torch.bfloat16:
+                raise KernelError(f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
+                                  context={"tensor": name, "dtype": str(t.dtype)})
+            if not t.is_cuda or t.device != q.device:
+                raise KernelError("Tensors must be on one CUDA device",
+                                  context={"tensor": name, "device": str(t.device)})
+        if block_indices is not None:
+            if block_indices.ndim != 3 or tuple(block_indices.shape[:2]) != (B, H):
+                raise KernelError(
+                    f"block_indices must have shape [{B}, {H}, K], got {tuple(block_indices.shape)}",
+                    context={"expected": [B, H, -1], "got": list(block_indices.shape)},
+                )
+            block_mask = indices_to_mask(block_indices.to(q.device), nb).view(B, H, 1, nb)
+        if tuple(block_mask.shape) != (B, H, 1, nb):
+            raise KernelError(
+                f"block_mask shape mismatch: expected {(B, H, 1, nb)}, got {tuple(block_mask.shape)}",
+                context={"expected": [B, H, 1, nb], "got": list(block_mask.shape)},
+            )
+        lib = _native.load_library()
+        if num_splits is None:
+            num_splits = default_decode_splits(B, Hkv, nb)
+        q = q.contiguous()
+        k_pages = _kernel_ready(k_pages)
+        v_pages = _kernel_ready(v_pages)
+        mask = _mask_bytes(block_mask.to(q.device))
+        table = block_table.to(device=q.device, dtype=torch.int32)
+        lens = kv_lens.to(device=q.device, dtype=torch.int32).contiguous()
+        ws_bytes = lib.tasft_bsfa_decode_workspace_bytes(B, H, D, num_splits)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        out = torch.empty((B, H, 1, D), dtype=q.dtype, device=q.device)
+        status = lib.tasft_bsfa_decode_paged_fwd(
+            q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), out.data_ptr(), mask.data_ptr(),
+            table.data_ptr(), lens.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, Hkv, S_kv, D,
+            self.block_size, page_size, num_splits,
+            _native.strides(q), _native.strides(k_pages), _native.strides(v_pages),
+            _native.strides(out), _native.strides(mask), table.stride(0), 1.0 / math.sqrt(D),
+            _native.stream_handle(q.device),
+        )
+        _native.check(status, "tasft_bsfa_decode_paged_fwd", {"shape": [B, H, S_kv, D],
+                                                              "page_size": page_size})
+        return out
+
     def compute_sparsity_stats(self, block_mask: torch.Tensor) -> SparsityStats:
         """Full-grid statistics (reference ``block_sparse_fa.py:574-595``; syncs the device)."""
         total_blocks = block_mask.numel()

@@ -97,3 +97,51 @@ def test_config3_geometry_shared_kv_selection():
     out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), shape.block)
     ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), shape.block)
     assert_close_bf16(out, ref, "config-3 geometry")
+
+
+# ----------------------------------------------------------------------------- paged cache
+PAGED_CASES = [
+    # B, Hq, Hkv, S, D, bs, page_size, splits
+    (3, 32, 8, 1000, 128, 64, 16, None),   # vLLM's default page size, partial last block
+    (2, 8, 2, 777, 128, 64, 32, 1),        # one split: direct write, no combine
+    (2, 4, 4, 512, 64, 64, 64, None),      # page = block, D=64
+    (2, 8, 1, 300, 128, 32, 64, None),     # page larger than the block
+    (1, 16, 2, 640, 64, 32, 16, 3),
+]
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "ps", "splits"), PAGED_CASES)
+def test_decode_paged_equals_contiguous_and_oracle(B, Hq, Hkv, S, D, bs, ps, splits):
+    dev = require_gpu()
+    print(f"paged decode B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} bs={bs} ps={ps}", flush=True)
+    g = torch.Generator().manual_seed(7000 + S + ps)
+    per = (S + ps - 1) // ps
+    cap = per * ps
+    q = (torch.randn(B, Hq, 1, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    k = (torch.randn(B, Hkv, cap, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    v = (torch.randn(B, Hkv, cap, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    lens = torch.randint(1, S + 1, (B,), generator=g, dtype=torch.int32)
+    lens[0] = S
+    nb = (cap + bs - 1) // bs
+    mask = torch.rand((B, Hq, 1, nb), generator=g) < 0.4
+    mask[:, :, :, 0] = True
+    # Pools: the pages of every sequence in a random order among spare pages of noise.
+    n_pages = B * per + 7
+    perm = torch.randperm(n_pages, generator=g)
+    table = perm[: B * per].view(B, per).to(torch.int32)
+    kp = torch.randn(n_pages, ps, Hkv, D, generator=g).to(torch.bfloat16)
+    vp = torch.randn(n_pages, ps, Hkv, D, generator=g).to(torch.bfloat16)
+    for b in range(B):
+        for j in range(per):
+            kp[table[b, j]] = k[b, :, j * ps:(j + 1) * ps].transpose(0, 1)
+            vp[table[b, j]] = v[b, :, j * ps:(j + 1) * ps].transpose(0, 1)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    paged = bsfa.forward_decode_paged(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                      lens.to(dev), mask.to(dev), num_splits=splits)
+    contig = bsfa.forward_decode(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                 kv_lens=lens.to(dev), num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(paged, contig)
+    ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),
+                                  mask.numpy(), bs)
+    assert_close_bf16(paged, ref, f"paged decode ps={ps}")

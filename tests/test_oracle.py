@@ -277,6 +277,29 @@ def test_decode_equals_last_prefill_row_and_brute_force():
     np.testing.assert_allclose(dec, brute, rtol=1e-10, atol=1e-12)
 
 
+def test_decode_paged_equals_contiguous_cache():
+    """Pools scattered from a contiguous cache through a random page permutation."""
+    rng = np.random.default_rng(23)
+    B, H, Hkv, S, D, bs, ps = 3, 4, 2, 128, 8, 32, 16
+    q = rng.standard_normal((B, H, 1, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    lens = np.array([128, 77, 16])
+    mask = rng.random((B, H, 1, S // bs)) < 0.6
+    per = S // ps
+    perm = rng.permutation(B * per + 5)  # spare pages stay unused
+    table = perm[: B * per].reshape(B, per)
+    kp = rng.standard_normal((B * per + 5, ps, Hkv, D)).astype(np.float32)
+    vp = rng.standard_normal((B * per + 5, ps, Hkv, D)).astype(np.float32)
+    for b in range(B):
+        for j in range(per):
+            kp[table[b, j]] = k[b, :, j * ps:(j + 1) * ps].transpose(1, 0, 2)
+            vp[table[b, j]] = v[b, :, j * ps:(j + 1) * ps].transpose(1, 0, 2)
+    got = orc.sparse_decode_paged(q, kp, vp, table, lens, mask, bs, dtype=np.float64)
+    ref = orc.sparse_decode(q, k, v, mask, bs, lens, dtype=np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-14)
+
+
 def test_decode_kv_lens_equals_truncated_cache():
     rng = np.random.default_rng(10)
     q = rng.standard_normal((2, 2, 1, 8)).astype(np.float32)
