@@ -233,3 +233,38 @@ def test_forward_varlen_validates_before_any_launch():
     # valid arguments on CPU tensors stop at the device check, before the library
     with pytest.raises(KernelError, match="same GPU device"):
         bsfa.forward_varlen(q, k, v, mask, torch.tensor([0, 10, 30], dtype=torch.int32))
+
+
+# ----------------------------------------------------------------------------- kernel_config.json
+def test_kernel_config_loads_reference_and_exporter_files_and_per_head_thresholds():
+    import json
+
+    from tasft_amd.kernels import KernelConfig
+
+    # A file in the reference loader's format loads unchanged.
+    ref = {"block_size": 64, "global_threshold": 0.5, "min_sparsity_for_speedup": 0.5,
+           "per_layer_config": {"0": {"layer_idx": 0, "threshold_tau": 0.4, "target_sparsity": 0.8,
+                                      "achieved_sparsity_validation": 0.79}}}
+    cfg = KernelConfig.model_validate(ref)
+    assert cfg.get_layer_threshold(0) == 0.4 and cfg.get_layer_threshold(3) == 0.5
+    assert cfg.get_layer_head_thresholds(0, 4) == (0.4, 0.4, 0.4, 0.4)
+    # The exporter's per-layer record (with gate_loss_validation) loads too.
+    exp = json.loads(json.dumps(ref))
+    exp["per_layer_config"]["0"]["gate_loss_validation"] = 0.031
+    assert KernelConfig.model_validate(exp).per_layer_config[0].gate_loss_validation == 0.031
+    # Per-head thresholds and the gate width round-trip through JSON.
+    ph = json.loads(json.dumps(ref))
+    ph["per_layer_config"]["0"].update(threshold_tau_per_head=[0.3, 0.4, 0.5, 0.6], gate_hidden_dim=32)
+    cfg2 = KernelConfig.model_validate_json(KernelConfig.model_validate(ph).model_dump_json())
+    assert cfg2.get_layer_head_thresholds(0, 4) == (0.3, 0.4, 0.5, 0.6)
+    assert cfg2.per_layer_config[0].gate_hidden_dim == 32
+    with pytest.raises(ValueError, match="expected 8"):
+        cfg2.get_layer_head_thresholds(0, 8)
+    bad = json.loads(json.dumps(ph))
+    bad["per_layer_config"]["0"]["threshold_tau_per_head"] = [0.3, 1.0]
+    with pytest.raises(ValueError, match=r"threshold_tau_per_head\[1\] must be in \(0, 1\)"):
+        KernelConfig.model_validate(bad)
+    unknown = json.loads(json.dumps(ref))
+    unknown["per_layer_config"]["0"]["surprise"] = 1
+    with pytest.raises(ValueError):
+        KernelConfig.model_validate(unknown)
