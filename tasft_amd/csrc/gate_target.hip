@@ -4,8 +4,9 @@
 //   scores = Q K^T * scale + triu(-inf, 1)            (tasft/modules/tasft_attention.py:426-443)
 //   pooled = max_pool2d(pad(scores, -inf), bs, bs)    (tasft/training/objectives.py:170-178)
 //   target = softmax(pooled over the flat NB_q*NB_k grid)  (objectives.py:181-185)
-// plus two options: a per-row softmax over key blocks (the BASELINE wording of the
-// target) and the clamp(+-50) / temperature variant of
+// plus two options: a per-row softmax over key blocks (the "softmax over k-blocks" reading
+// of the target that the benchmark configuration uses) and the clamp(+-50) / temperature
+// variant of
 // tasft/modules/tasft_attention.py:272-290.
 //
 // Kernel 1 computes each block maximum with the same S^T = K . Q^T bf16 MFMA tiling as
