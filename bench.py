@@ -5,7 +5,8 @@ causal GQA block-sparse prefill at the Llama-3-8B geometry (config 2: B=4, S=819
 heads, D=128, block 64, gate hidden 128, per-head tau for 80% causal sparsity with the
 diagonal forced on). Inputs are resident in HBM before timing. ``value`` is tokens/s of
 the step. The same run also measures, as extra figures, the split-K decode (config 3:
-B=64, S_kv=32768, 51 of 512 blocks per KV head) in HBM GB/s, the Qwen-2.5-7B prefill
+B=64, S_kv=32768, 51 of 512 blocks per KV head) in HBM GB/s, with the same tokens also
+read from a 16-token paged cache (checked bit-identical), the Qwen-2.5-7B prefill
 (config 4) and the gate target (config 5), plus a CPU baseline of the oracle on a bounded
 sample of config 2.
 
@@ -178,10 +179,36 @@ def bench_decode(torch, dev, steps, warmup):
     kv_bytes = blocks * shape.block * shape.head_dim * 2 * 2
     small = q.numel() * 2 * 2 + mask.numel()
     total = kv_bytes + small
-    del kc, vc
+    # The same tokens in a paged cache (16-token pages, vLLM's default) behind a block table
+    # whose pages are a random permutation of the pool; the output must match bit for bit.
+    ps = 16
+    per = shape.seq // ps
+    perm = torch.randperm(shape.batch * per, generator=torch.Generator().manual_seed(3003)).to(dev)
+    table = perm.view(shape.batch, per).to(torch.int32)
+    lens = torch.full((shape.batch,), shape.seq, dtype=torch.int32, device=dev)
+    pool_shape = (shape.batch * per, ps, shape.kv_heads, shape.head_dim)
+    kp = torch.empty(pool_shape, dtype=torch.bfloat16, device=dev)
+    vp = torch.empty(pool_shape, dtype=torch.bfloat16, device=dev)
+    for src, dst in ((kc, kp), (vc, vp)):
+        dst[table.view(-1).long()] = (src.view(shape.batch, shape.kv_heads, per, ps, shape.head_dim)
+                                      .permute(0, 2, 3, 1, 4).reshape(pool_shape))
+    ref = bsfa.forward_decode(q, kc, vc, mask, kv_lens=lens)
+    for _ in range(warmup):
+        out = bsfa.forward_decode_paged(q, kp, vp, table, lens, mask)
+    torch.cuda.synchronize()
+    if not torch.equal(out, ref):
+        raise RuntimeError("paged decode differs from the contiguous decode")
+    tp = LaunchTimer(torch)
+    with _Span(tp):
+        for _ in range(steps):
+            bsfa.forward_decode_paged(q, kp, vp, table, lens, mask)
+    torch.cuda.synchronize()
+    ms_paged = tp.total_ms() / steps
+    del kc, vc, kp, vp
     torch.cuda.empty_cache()
     return {"decode_ms": ms, "decode_hbm_gbps": total / (ms * 1e-3) / 1e9,
-            "decode_bytes": total, "decode_kv_blocks": blocks}
+            "decode_bytes": total, "decode_kv_blocks": blocks,
+            "decode_paged_ms": ms_paged, "decode_paged_hbm_gbps": total / (ms_paged * 1e-3) / 1e9}
 
 
 def bench_qwen(torch, dev, steps, warmup):
@@ -330,7 +357,9 @@ def main() -> int:
         d = bench_decode(torch, dev, max(10, args.steps), max(20, args.warmup))
         extra.update({"decode_ms": round(d["decode_ms"], 4), "decode_hbm_gbps": round(d["decode_hbm_gbps"], 1),
                       "decode_hbm_frac": round(d["decode_hbm_gbps"] / PEAK_HBM_GBPS, 4),
-                      "decode_bytes": d["decode_bytes"]})
+                      "decode_bytes": d["decode_bytes"],
+                      "decode_paged16_ms": round(d["decode_paged_ms"], 4),
+                      "decode_paged16_hbm_gbps": round(d["decode_paged_hbm_gbps"], 1)})
     if "qwen" in extras:
         log("bench: config 4 Qwen prefill")
         qw = bench_qwen(torch, dev, max(5, args.steps // 2), max(10, args.warmup // 4))
