@@ -145,3 +145,30 @@ def test_decode_paged_equals_contiguous_and_oracle(B, Hq, Hkv, S, D, bs, ps, spl
     ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),
                                   mask.numpy(), bs)
     assert_close_bf16(paged, ref, f"paged decode ps={ps}")
+
+
+def test_decode_paged_block_indices_equals_mask():
+    """Index-list selection on a paged cache equals the dense-mask call."""
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs, ps = 2, 8, 2, 512, 128, 64, 16
+    g = torch.Generator().manual_seed(7300)
+    per = S // ps
+    q = (torch.randn(B, Hq, 1, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(dev)
+    kp = (torch.randn(B * per, ps, Hkv, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(dev)
+    vp = torch.randn(B * per, ps, Hkv, D, generator=g).to(torch.bfloat16).to(dev)
+    table = torch.randperm(B * per, generator=g).view(B, per).to(torch.int32).to(dev)
+    lens = torch.tensor([S, 300], dtype=torch.int32, device=dev)
+    idx = torch.randint(0, S // bs, (B, Hq, 3), generator=g)
+    idx[:, :, 2] = -1  # padding slot
+    nb = S // bs
+    mask = torch.zeros(B, Hq, 1, nb, dtype=torch.bool)
+    for b in range(B):
+        for h in range(Hq):
+            for j in idx[b, h].tolist():
+                if j >= 0:
+                    mask[b, h, 0, j] = True
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    a = bsfa.forward_decode_paged(q, kp, vp, table, lens, block_indices=idx.to(dev))
+    m = bsfa.forward_decode_paged(q, kp, vp, table, lens, mask.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(a, m)

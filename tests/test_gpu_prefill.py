@@ -215,6 +215,8 @@ VARLEN_CASES = [
     ([300, 45, 128], 4, 4, 64, 64, True, 0.5),          # four-wave kernel (D=64)
     ([130, 77], 4, 2, 64, 32, False, 0.6),              # generic kernel, non-causal
     ([513, 200], 7, 1, 128, 128, True, 0.4),            # bs=128, G=7
+    ([64, 1, 95, 700], 16, 2, 128, 32, True, 0.3),      # G=8, bs=32, block-aligned and 1-token
+    ([333, 334], 8, 1, 64, 64, False, 0.7),             # non-causal four-wave kernel
 ]
 
 
