@@ -72,6 +72,25 @@ def test_invalid_arguments_return_errors_without_launch():
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
     rc = lib.tasft_mask_from_indices(fake, 4, 3, 2, 10, fake, fake, None)
     assert rc == -1 and b"invalid sizes" in lib.tasft_last_error()
+    st3 = _i64([0, 0, 1])
+    rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, None, 2, 32, 8, 128, 128,
+                                           64, st3, st3, st3, st3, st, 1.0, 1, None)
+    assert rc == -1 and b"null pointer" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128,
+                                           48, st3, st3, st3, st3, st, 1.0, 1, None)
+    assert rc == -2 and b"block_size" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128,
+                                           64, _i64([8, 8, 2]), st3, st3, st3, st, 1.0, 1, None)
+    assert rc == -1 and b"contiguous" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
+                                         8, 1024, 128, 128, 16, 4, st, st, st, st, st, 64, 1.0, None)
+    assert rc == -2 and b"block_size" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
+                                         8, 1024, 128, 64, 12, 4, st, st, st, st, st, 64, 1.0, None)
+    assert rc == -2 and b"page_size" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
+                                         8, 1024, 128, 64, 16, 4, st, st, st, st, st, 64, 1.0, None)
+    assert rc == -4 and b"workspace" in lib.tasft_last_error()
 
 
 def test_check_raises_kernel_error_with_message():
