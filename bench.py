@@ -83,18 +83,11 @@ class _Span:
 
 def setup_config2(torch, dev):
     from tasft_amd import workloads as wl
-    from tasft_amd.modules import AttnGate
 
     shape = wl.CONFIG_SHAPES[2]
     q, k, v = wl.qkv(shape, 1002)
-    gate = AttnGate(num_heads=shape.q_heads, head_dim=shape.head_dim, block_size=shape.block,
-                    gate_hidden_dim=128)
-    gate.load_state_dict(wl.gate_params(128, shape.head_dim, 3002))
-    gate = gate.to(dev).requires_grad_(False)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
-    with torch.no_grad():
-        probe = gate(qd, kd, threshold=0.5)
-    taus = wl.per_head_threshold(probe.soft_scores, keep_causal=0.20)
+    gate, taus = wl.config2_gate(dev, qd, kd)
     return shape, (q, k, v), (qd, kd, vd), gate, taus
 
 

@@ -33,7 +33,7 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (4). */
+/* ABI version of this library (5). */
 int tasft_abi_version(void);
 
 /*
@@ -140,7 +140,9 @@ int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cach
  * k_pages, v_pages [num_pages, page_size, Hkv, D] (strides of page, token, head, dim in
  * elements, dim contiguous); token t of sequence b is row t % page_size of page
  * block_table[b * block_table_stride + t / page_size] (device int32; only the pages that
- * hold a token below kv_lens[b] are read). kv_lens: device int32 [B], required.
+ * hold a token below kv_lens[b] are read). num_pages: the number of pages in each pool;
+ * a table entry outside [0, num_pages) is clamped into it, so a corrupt table gives wrong
+ * values but never reads outside the pools. kv_lens: device int32 [B], required.
  * kv_len_max bounds every kv_lens[b]; block_mask [B, Hq, 1, ceil(kv_len_max/bs)].
  * block_size 32 or 64; page_size a power of two >= 8. Other arguments as in
  * tasft_bsfa_decode_fwd (same workspace size).
@@ -151,7 +153,7 @@ int tasft_bsfa_decode_paged_fwd(const void* q, const void* k_pages, const void* 
                                 void* workspace, size_t workspace_bytes, int64_t batch,
                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t kv_len_max,
                                 int64_t head_dim, int64_t block_size, int64_t page_size,
-                                int64_t num_splits, const int64_t* q_strides,
+                                int64_t num_pages, int64_t num_splits, const int64_t* q_strides,
                                 const int64_t* k_strides, const int64_t* v_strides,
                                 const int64_t* o_strides, const int64_t* mask_strides,
                                 int64_t block_table_stride, float scale, void* stream);

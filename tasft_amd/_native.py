@@ -67,7 +67,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_bsfa_decode_paged_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64P, _I64P, _I64P, _I64P, _I64P, _I64, _F, _P],
+         _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64, _F, _P],
     ),
     "tasft_gate_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_fwd": (

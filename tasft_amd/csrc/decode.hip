@@ -43,9 +43,12 @@ struct DecodeParams {
   // Paged cache (kernels instantiated with PAGED): K/V are page pools whose strides sk, sv
   // are (page, head, token); token t of sequence b lives in page
   // block_table[b * bt_stride + t / page_size], row t % page_size.
+  // Page ids are clamped to [0, num_pages): a bad table entry reads a wrong page of the
+  // pool, never memory outside it.
   const int32_t* block_table;
   int64_t bt_stride;
   int page_size;
+  int num_pages;
 };
 
 // Raw buffer resource (stride 0) over `bytes` bytes starting at `base`.
@@ -223,7 +226,8 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       const int first = (kb * BS) / ps;
       // Only pages that hold a token below kv_len are read (later entries may not exist).
       const int jmax = (kv_len - 1 - kb * BS + (kb * BS) % ps) / ps;
-      return p.block_table[(int64_t)b * p.bt_stride + first + min(lane < npg ? lane : 0, jmax)];
+      const int id = p.block_table[(int64_t)b * p.bt_stride + first + min(lane < npg ? lane : 0, jmax)];
+      return min(max(id, 0), p.num_pages - 1);
     };
     auto load_k_paged = [&](int kb, int pgv) {
       const int key0 = kb * BS;
@@ -701,6 +705,7 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
   p.block_table = nullptr;
   p.bt_stride = 0;
   p.page_size = 0;
+  p.num_pages = 0;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
@@ -719,14 +724,15 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
     const void* q, const void* k_pages, const void* v_pages, void* out, const uint8_t* block_mask,
     const int32_t* block_table, const int32_t* kv_lens, void* workspace, size_t workspace_bytes,
     int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t kv_len_max,
-    int64_t head_dim, int64_t block_size, int64_t page_size, int64_t num_splits,
-    const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-    const int64_t* o_strides, const int64_t* mask_strides, int64_t block_table_stride,
-    float scale, void* stream) {
+    int64_t head_dim, int64_t block_size, int64_t page_size, int64_t num_pages,
+    int64_t num_splits, const int64_t* q_strides, const int64_t* k_strides,
+    const int64_t* v_strides, const int64_t* o_strides, const int64_t* mask_strides,
+    int64_t block_table_stride, float scale, void* stream) {
   if (!q || !k_pages || !v_pages || !out || !block_mask || !block_table || !kv_lens ||
       !workspace || !q_strides || !k_strides || !v_strides || !o_strides || !mask_strides)
     return set_error(kErrInvalidArgument, "decode_paged: null pointer argument");
-  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || kv_len_max <= 0 || num_splits <= 0)
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || kv_len_max <= 0 || num_splits <= 0 ||
+      num_pages <= 0)
     return set_error(kErrInvalidArgument, "decode_paged: sizes must be positive");
   if (num_q_heads % num_kv_heads != 0)
     return set_error(kErrInvalidArgument,
@@ -768,7 +774,8 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
     return set_error(kErrInvalidArgument,
                      "decode_paged: q, K/V pools and workspace must be 16-byte aligned");
   if (batch * num_kv_heads * num_splits > 0x7fffffffLL || kv_len_max > 0x3fffffffLL ||
-      page_size * k_strides[1] * 2 > 0x7fffffffLL || page_size * v_strides[1] * 2 > 0x7fffffffLL)
+      page_size * k_strides[1] * 2 > 0x7fffffffLL || page_size * v_strides[1] * 2 > 0x7fffffffLL ||
+      num_pages > 0x7fffffffLL)
     return set_error(kErrUnsupported, "decode_paged: problem too large for one launch");
 
   DecodeParams p;
@@ -806,6 +813,7 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
   p.block_table = block_table;
   p.bt_stride = block_table_stride;
   p.page_size = (int)page_size;
+  p.num_pages = (int)num_pages;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;

@@ -362,7 +362,7 @@ class BlockSparseFlashAttention:
         k = _kernel_ready(k)
         v = _kernel_ready(v)
         mask = _mask_bytes(block_mask.to(q.device))
-        cu_dev = cu_seqlens.to(device=q.device, dtype=torch.int32)
+        cu_dev = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
         out = (torch.empty_like(q) if covered == T else torch.zeros_like(q))
         status = lib.tasft_bsfa_prefill_varlen_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
@@ -502,7 +502,9 @@ class BlockSparseFlashAttention:
             k_pages, v_pages: ``[num_pages, page_size, Hkv, D]`` bf16 page pools; token t of
                 sequence b is row ``t % page_size`` of page ``block_table[b, t // page_size]``.
             block_table: ``[B, max_pages]`` int32 on the device; only the pages holding a
-                token below ``kv_lens[b]`` are read.
+                token below ``kv_lens[b]`` are read. An entry outside
+                ``[0, num_pages)`` is clamped into it by the kernel (wrong values, never an
+                access outside the pools).
             kv_lens: ``[B]`` int32 valid lengths (on the device).
             block_mask: ``[B, Hq, 1, NB]`` with ``NB = ceil(max_pages * page_size / block_size)``.
             block_indices: instead of ``block_mask``, ``[B, Hq, K]`` index lists (``-1`` empty).
@@ -573,7 +575,8 @@ class BlockSparseFlashAttention:
         k_pages = _kernel_ready(k_pages)
         v_pages = _kernel_ready(v_pages)
         mask = _mask_bytes(block_mask.to(q.device))
-        table = block_table.to(device=q.device, dtype=torch.int32)
+        # The kernel reads the table with a unit column stride.
+        table = block_table.to(device=q.device, dtype=torch.int32).contiguous()
         lens = kv_lens.to(device=q.device, dtype=torch.int32).contiguous()
         ws_bytes = lib.tasft_bsfa_decode_workspace_bytes(B, H, D, num_splits)
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
@@ -581,7 +584,7 @@ class BlockSparseFlashAttention:
         status = lib.tasft_bsfa_decode_paged_fwd(
             q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), out.data_ptr(), mask.data_ptr(),
             table.data_ptr(), lens.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, Hkv, S_kv, D,
-            self.block_size, page_size, num_splits,
+            self.block_size, page_size, k_pages.shape[0], num_splits,
             _native.strides(q), _native.strides(k_pages), _native.strides(v_pages),
             _native.strides(out), _native.strides(mask), table.stride(0), 1.0 / math.sqrt(D),
             _native.stream_handle(q.device),

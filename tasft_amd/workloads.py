@@ -155,12 +155,32 @@ def per_head_threshold(soft: torch.Tensor, keep_causal: float) -> torch.Tensor:
     return taus
 
 
+def config2_gate(device: torch.device, q: torch.Tensor, k: torch.Tensor):
+    """The config-2 gate as benchmarked: ``AttnGate`` with hidden 128 and the reference init
+    order from seed 3002, and per-head thresholds keeping 20% of the causal blocks of each
+    head (computed from a first pass at tau = 0.5). ``q``/``k`` are device tensors.
+
+    Returns ``(gate, taus)``; call ``gate(q, k, threshold=taus, force_diagonal=True)``.
+    """
+    from tasft_amd.modules import AttnGate
+
+    shape = CONFIG_SHAPES[2]
+    gate = AttnGate(num_heads=shape.q_heads, head_dim=shape.head_dim, block_size=shape.block,
+                    gate_hidden_dim=128)
+    gate.load_state_dict(gate_params(128, shape.head_dim, 3002))
+    gate = gate.to(device).requires_grad_(False)
+    with torch.no_grad():
+        probe = gate(q, k, threshold=0.5)
+    return gate, per_head_threshold(probe.soft_scores, keep_causal=0.20)
+
+
 __all__ = [
     "BLOCK",
     "CONFIG_SHAPES",
     "HEAD_DIM",
     "Shape",
     "bernoulli_causal_mask",
+    "config2_gate",
     "decode_mask",
     "gate_params",
     "per_head_threshold",

@@ -4,9 +4,15 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-# Parity bar for bf16 kernels against an fp32 reference on identical bf16-rounded inputs.
+# Parity bar for bf16 kernels against an fp32 reference on identical bf16-rounded inputs:
+# the absolute bound of the specification (max-abs 2e-2, mean-abs 2e-3) and, next to it, a
+# relative one (max-abs error <= 2e-2 * max|ref|, mean-abs error <= 2e-2 * mean|ref|), so
+# that outputs of small magnitude are held to the same 2% as outputs of order one.
 MAX_ABS_TOL = 2e-2
 MEAN_ABS_TOL = 2e-3
+REL_TOL = 2e-2
+# Floor of the relative bound (outputs that are all exactly zero).
+_REL_FLOOR = 1e-6
 
 
 def to_np(t: torch.Tensor) -> np.ndarray:
@@ -14,15 +20,50 @@ def to_np(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy()
 
 
+def parity_errors(actual: np.ndarray, expected: np.ndarray) -> dict[str, float]:
+    """Absolute and relative error figures of ``actual`` against ``expected``."""
+    err = np.abs(actual.astype(np.float64) - expected.astype(np.float64))
+    ref = np.abs(expected.astype(np.float64))
+    if err.size == 0:
+        return {"max": 0.0, "mean": 0.0, "ref_max": 0.0, "ref_mean": 0.0}
+    return {"max": float(err.max()), "mean": float(err.mean()),
+            "ref_max": float(ref.max()), "ref_mean": float(ref.mean())}
+
+
+def parity_failure(actual: np.ndarray, expected: np.ndarray, max_abs: float = MAX_ABS_TOL,
+                   mean_abs: float = MEAN_ABS_TOL, rel: float | None = REL_TOL) -> str | None:
+    """None if ``actual`` meets the bar against ``expected``, else a description."""
+    if actual.shape != expected.shape:
+        return f"shape {actual.shape} != {expected.shape}"
+    if not np.isfinite(actual).all():
+        return "non-finite values"
+    e = parity_errors(actual, expected)
+    bad = []
+    if e["max"] > max_abs:
+        bad.append(f"max-abs {e['max']:.3e} > {max_abs}")
+    if e["mean"] > mean_abs:
+        bad.append(f"mean-abs {e['mean']:.3e} > {mean_abs}")
+    if rel is not None:
+        if e["max"] > rel * e["ref_max"] + _REL_FLOOR:
+            bad.append(f"max-abs {e['max']:.3e} > {rel} * max|ref| ({e['ref_max']:.3e})")
+        if e["mean"] > rel * e["ref_mean"] + _REL_FLOOR:
+            bad.append(f"mean-abs {e['mean']:.3e} > {rel} * mean|ref| ({e['ref_mean']:.3e})")
+    return "; ".join(bad) or None
+
+
 def assert_close_bf16(actual: torch.Tensor | np.ndarray, expected: np.ndarray, what: str,
-                      max_abs: float = MAX_ABS_TOL, mean_abs: float = MEAN_ABS_TOL) -> None:
+                      max_abs: float = MAX_ABS_TOL, mean_abs: float = MEAN_ABS_TOL,
+                      rel: float | None = REL_TOL) -> None:
     a = to_np(actual) if isinstance(actual, torch.Tensor) else np.asarray(actual, dtype=np.float32)
-    assert a.shape == expected.shape, f"{what}: shape {a.shape} != {expected.shape}"
-    assert np.isfinite(a).all(), f"{what}: non-finite values in kernel output"
-    err = np.abs(a.astype(np.float64) - expected.astype(np.float64))
-    mx, mn = float(err.max()) if err.size else 0.0, float(err.mean()) if err.size else 0.0
-    assert mx <= max_abs and mn <= mean_abs, (
-        f"{what}: max-abs {mx:.3e} (tol {max_abs}), mean-abs {mn:.3e} (tol {mean_abs})")
+    fail = parity_failure(a, np.asarray(expected), max_abs, mean_abs, rel)
+    assert fail is None, f"{what}: {fail}"
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bf16 (ties to even), returned as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
 
 
 def require_gpu() -> torch.device:

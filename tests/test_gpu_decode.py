@@ -7,10 +7,11 @@ import numpy as np
 import pytest
 import torch
 
+import attn_inputs as ai
 from helpers import assert_close_bf16, require_gpu, to_np
 from oracle import tasft_oracle as orc
 from tasft_amd import workloads as wl
-from tasft_amd.kernels import BlockSparseFlashAttention
+from tasft_amd.kernels import BlockSparseFlashAttention, default_decode_splits
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +53,27 @@ def test_decode_matches_oracle(B, Hq, Hkv, S, D, bs, density, splits):
     assert_close_bf16(out, ref, f"decode {B}x{Hq}/{Hkv}x{S} bs={bs} splits={splits}")
 
 
+@pytest.mark.parametrize("kind", ("unit", "peaky"))
+@pytest.mark.parametrize("case", ai.DECODE_CASES, ids=ai.case_id)
+def test_decode_discriminating_inputs(case, kind):
+    """Scores far from uniform: pins QK^T, the exp2 scale, per-wave max tracking, the lazy
+    rescale and the merge of waves and splits (one split with direct writes, and several
+    with the combine kernel)."""
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs, _dens, splits = case
+    print(f"decode discriminating {case} {kind}", flush=True)
+    q, kc, vc, mask = ai.decode_case_inputs(case, kind)
+    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), bs, num_splits=splits)
+    assert (out[0, 0].cpu() == 0).all()
+    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), bs)
+    assert_close_bf16(out, ref, f"decode {case} {kind}")
+    lens = torch.randint(1, S + 1, (B,), generator=torch.Generator().manual_seed(S))
+    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), bs,
+                  kv_lens=lens.to(torch.int32).to(dev), num_splits=splits)
+    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), bs, kv_lens=lens.numpy())
+    assert_close_bf16(out, ref, f"decode {case} {kind} kv_lens")
+
+
 def test_decode_kv_lens():
     dev = require_gpu()
     B, Hq, Hkv, S, D, bs = 4, 8, 2, 700, 128, 64
@@ -85,18 +107,44 @@ def test_decode_equals_prefill_last_row():
     assert float(diff.max()) <= 1e-2, f"decode vs prefill last row: {float(diff.max())}"
 
 
-def test_config3_geometry_shared_kv_selection():
-    """Config-3 selection (51 of 512 blocks per KV head, sink + recent kept) at B=4."""
+def test_config3_full_size_default_splits():
+    """Config 3 as benchmarked: B=64, S_kv=32768, 32/8 heads, 51 of 512 blocks per KV head
+    (sink and recent kept), the default split count (one split per (b, KV head), direct
+    writes, 512 workgroups). K/V are drawn on the device as the bench does; sampled
+    (b, h) pairs are compared with the oracle on slices copied back. The same launch runs
+    again on unit-scale Q/K/V."""
     dev = require_gpu()
-    shape = wl.Shape(4, 32, 8, 32768)
-    q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1003)
-    kc = wl.randn_bf16((shape.batch, shape.kv_heads, shape.seq, shape.head_dim), 1004)
-    vc = wl.randn_bf16((shape.batch, shape.kv_heads, shape.seq, shape.head_dim), 1005)
+    shape = wl.CONFIG_SHAPES[3]
+    bsfa = BlockSparseFlashAttention(block_size=shape.block, min_sparsity_for_speedup=0.0)
+    nb = shape.nb
+    assert default_decode_splits(shape.batch, shape.kv_heads, nb) == 1
+    grp = shape.q_heads // shape.kv_heads
+    gen = torch.Generator(device=dev).manual_seed(1003)
+    kv_shape = (shape.batch, shape.kv_heads, shape.seq, shape.head_dim)
+    kc = torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16)
     mask = wl.decode_mask(shape, 51, 2003)
     assert int(mask[0, 0, 0].sum()) == 51 and bool(mask[0, 0, 0, 0]) and bool(mask[0, 0, 0, -1])
-    out = _decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), shape.block)
-    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), shape.block)
-    assert_close_bf16(out, ref, "config-3 geometry")
+    md = mask.to(dev)
+    pairs = [(0, 0), (17, 9), (40, 22), (63, 31)]
+    for kind in ("base", "unit"):
+        print(f"config 3 B=64 {kind}", flush=True)
+        if kind == "base":
+            q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1003)
+            kd = kc * (1.0 / math.sqrt(shape.head_dim))
+            vd = vc * (1.0 / math.sqrt(shape.head_dim))
+        else:
+            q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1013, scale=1.0)
+            kd, vd = kc, vc
+        out = _decode(q.to(dev), kd, vd, md, shape.block).cpu()
+        assert torch.isfinite(out.float()).all()
+        for b, h in pairs:
+            kvh = h // grp
+            ref = orc.sparse_decode(to_np(q[b:b + 1, h:h + 1]), to_np(kd[b:b + 1, kvh:kvh + 1]),
+                                    to_np(vd[b:b + 1, kvh:kvh + 1]), mask[b:b + 1, h:h + 1].numpy(),
+                                    shape.block)
+            assert_close_bf16(out[b:b + 1, h:h + 1], ref, f"config 3 {kind} ({b},{h})")
+        del kd, vd
 
 
 # ----------------------------------------------------------------------------- paged cache
@@ -145,6 +193,25 @@ def test_decode_paged_equals_contiguous_and_oracle(B, Hq, Hkv, S, D, bs, ps, spl
     ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),
                                   mask.numpy(), bs)
     assert_close_bf16(paged, ref, f"paged decode ps={ps}")
+
+
+@pytest.mark.parametrize("kind", ("unit", "peaky"))
+@pytest.mark.parametrize("case", ai.PAGED_CASES, ids=ai.case_id)
+def test_decode_paged_discriminating_inputs(case, kind):
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs, ps, splits = case
+    print(f"paged decode discriminating {case} {kind}", flush=True)
+    q, k, v, kp, vp, table, lens, mask = ai.paged_case_inputs(case, kind)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    paged = bsfa.forward_decode_paged(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                      lens.to(dev), mask.to(dev), num_splits=splits)
+    contig = bsfa.forward_decode(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                 kv_lens=lens.to(dev), num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(paged, contig)
+    ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),
+                                  mask.numpy(), bs)
+    assert_close_bf16(paged, ref, f"paged decode {case} {kind}")
 
 
 def test_decode_paged_block_indices_equals_mask():

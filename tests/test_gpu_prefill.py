@@ -13,6 +13,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+import attn_inputs as ai
 from helpers import assert_close_bf16, require_gpu, to_np
 from oracle import tasft_oracle as orc
 from tasft_amd import workloads as wl
@@ -144,14 +145,45 @@ def _sampled_parity(cfg, mask, seed, heads, rows=None):
     assert torch.isfinite(out.float()).all()
 
 
-def test_config2_full_size_sampled_heads():
+def test_config2_gate_chain_full_size_sampled_heads():
+    """The launch the bench times: the config-2 gate with per-head tau (80% causal
+    sparsity) and the diagonal forced on, then the prefill under its mask. The mask is
+    checked against the oracle's threshold of the kernel's own logits (every head), the
+    prefill against the oracle on sampled heads, on the benchmark inputs and again on
+    unit-scale inputs under the same mask."""
+    dev = require_gpu()
     shape = wl.CONFIG_SHAPES[2]
-    g = torch.Generator().manual_seed(2002)
     nb = shape.nb
-    # 80% causal sparsity with the diagonal on (the mask the gate produces at config 2).
-    keep = torch.rand((shape.batch, shape.q_heads, nb, nb), generator=g) < 0.187
-    mask = (keep & torch.ones(nb, nb, dtype=torch.bool).tril(-1)) | torch.eye(nb, dtype=torch.bool)
-    _sampled_parity(2, mask, 1002, heads=[(0, 0), (1, 13), (3, 31)])
+    q, k, v = wl.qkv(shape, 1002)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    gate, taus = wl.config2_gate(dev, qd, kd)
+    with torch.no_grad():
+        g = gate(qd, kd, threshold=taus, force_diagonal=True, return_logits=True)
+    torch.cuda.synchronize()
+    logits = to_np(g.logits)
+    t = taus.cpu().numpy()
+    soft_ref, hard_ref = orc.threshold_mask(logits, t, True)
+    hard_ref = hard_ref | np.eye(nb, dtype=bool)
+    decisive = (np.abs(soft_ref - t.reshape(1, -1, 1, 1)) > 1e-6) | np.eye(nb, dtype=bool)
+    hard = g.hard_mask.cpu().numpy()
+    assert np.array_equal(hard[decisive], hard_ref[decisive])
+    n_exec = int(np.count_nonzero(hard & np.tril(np.ones((nb, nb), dtype=bool))))
+    n_causal = shape.batch * shape.q_heads * nb * (nb + 1) // 2
+    assert abs((1.0 - n_exec / n_causal) - 0.8) < 0.005
+    mask = g.hard_mask
+    heads = [(0, 0), (1, 13), (3, 31)]
+    out = _run(qd, kd, vd, mask, shape.block, True).cpu()
+    ref = orc.attention_block_gather(to_np(q), to_np(k), to_np(v), hard, shape.block, True, heads=heads)
+    for b, h in heads:
+        assert_close_bf16(out[b, h], ref[b, h], f"config 2 head ({b},{h})")
+    assert torch.isfinite(out.float()).all()
+    del out
+    qu, ku, vu = ai.qkv("unit", tuple(q.shape), tuple(k.shape), 4002, shape.block)
+    out = _run(qu.to(dev), ku.to(dev), vu.to(dev), mask, shape.block, True).cpu()
+    ref = orc.attention_block_gather(to_np(qu), to_np(ku), to_np(vu), hard, shape.block, True,
+                                     heads=heads)
+    for b, h in heads:
+        assert_close_bf16(out[b, h], ref[b, h], f"config 2 unit-scale head ({b},{h})")
 
 
 def test_config4_full_size_sampled_heads():
@@ -160,35 +192,80 @@ def test_config4_full_size_sampled_heads():
     _sampled_parity(4, mask, 1004, heads=[(0, 0), (1, 27)])
 
 
-@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "bs"), [
-    (2, 16, 4, 2048, 64),   # 8 KV groups: per-XCD partitions
-    (2, 6, 3, 1500, 64),    # 6 KV groups: one partition, ragged
-    (1, 8, 2, 1024, 128),   # generic kernel
-])
-def test_persistent_queue_is_bit_identical(B, Hq, Hkv, S, bs):
-    """The persistent work queue (workspace given) must not change any output bit."""
+def _prefill_capi(q, k, v, mask, bs, causal, workspace=None):
+    """tasft_bsfa_prefill_fwd called directly (``workspace`` None: one workgroup per row)."""
     import ctypes
 
     from tasft_amd import _native
 
+    B, Hq, S, D = q.shape
+    lib = _native.load_library()
+    out = torch.empty_like(q)
+    m8 = mask.view(torch.uint8)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel())
+    rc = lib.tasft_bsfa_prefill_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), m8.data_ptr(), ws_ptr, ws_bytes,
+        B, Hq, k.shape[1], S, D, bs, _native.strides(q), _native.strides(k), _native.strides(v),
+        _native.strides(out), _native.strides(m8), ctypes.c_float(1.0 / math.sqrt(D)),
+        1 if causal else 0, _native.stream_handle(q.device))
+    _native.check(rc, "tasft_bsfa_prefill_fwd")
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kind", ("unit", "peaky"))
+@pytest.mark.parametrize("case", ai.PREFILL_CASES, ids=ai.case_id)
+def test_prefill_discriminating_inputs(case, kind):
+    """Scores far from uniform (unit scale; peaky keys that move the running maximum):
+    pins QK^T, the exp2 scale, max tracking and the lazy rescale of every prefill kernel.
+    The four-wave kernel runs with its persistent queue (the Python path) and without."""
     dev = require_gpu()
-    q, k, v = _inputs(B, Hq, Hkv, S, 128, 4242 + S)
-    shape = wl.Shape(B, Hq, Hkv, S, 128, bs)
+    B, Hq, Hkv, S, D, bs, causal, _dens, variant = case
+    print(f"prefill discriminating {case} {kind}", flush=True)
+    q, k, v, mask = ai.prefill_case_inputs(case, kind)
+    ref = orc.attention_block_gather(to_np(q), to_np(k), to_np(v), mask.numpy(), bs, causal)
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    out = _run(qd, kd, vd, md, bs, causal)
+    assert_close_bf16(out, ref, f"prefill {variant} {kind}")
+    if variant == "4w":
+        direct = _prefill_capi(qd, kd, vd, md, bs, causal)
+        assert_close_bf16(direct, ref, f"prefill {variant} {kind} (no work queue)")
+        assert torch.equal(direct, out)
+
+
+@pytest.mark.parametrize("kind", ("unit", "peaky"))
+@pytest.mark.parametrize("case", ai.VARLEN_CASES, ids=ai.case_id)
+def test_prefill_varlen_discriminating_inputs(case, kind):
+    dev = require_gpu()
+    lens, Hq, Hkv, D, bs, causal, _dens = case
+    print(f"varlen discriminating {case} {kind}", flush=True)
+    q, k, v, cu, mask = ai.varlen_case_inputs(case, kind)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward_varlen(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                              torch.tensor(cu, dtype=torch.int32), causal=causal)
+    torch.cuda.synchronize()
+    ref = orc.attention_varlen(to_np(q), to_np(k), to_np(v), cu, mask.numpy(), bs, causal)
+    assert_close_bf16(out, ref, f"varlen {lens} {kind}")
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs"), [
+    (2, 16, 4, 2048, 64, 64),    # 8 KV groups: per-XCD partitions of the work queue
+    (2, 6, 3, 1500, 64, 64),     # 6 KV groups: one partition, ragged
+    (2, 16, 4, 2048, 128, 64),   # two-wave kernel: the workspace is left unused
+    (1, 8, 2, 1024, 128, 128),   # generic kernel
+])
+def test_persistent_queue_is_bit_identical(B, Hq, Hkv, S, D, bs):
+    """The persistent work queue (workspace given; block 64 with head dim 64) must not
+    change any output bit against one workgroup per row."""
+    dev = require_gpu()
+    q, k, v = ai.qkv("unit", (B, Hq, S, D), (B, Hkv, S, D), 4242 + S + D, bs)
+    shape = wl.Shape(B, Hq, Hkv, S, D, bs)
     mask = wl.bernoulli_causal_mask(shape, 0.15, 5151 + S)
     mask[0, 1, -3:, :] = True   # whole rows lit, as a gate can produce
     mask[B - 1, Hq - 1, 5, :] = True
     q, k, v, mask = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
     out_ws = _run(q, k, v, mask, bs, True)  # the Python path passes a workspace
-    lib = _native.load_library()
-    out = torch.empty_like(q)
-    m8 = mask.view(torch.uint8)
-    rc = lib.tasft_bsfa_prefill_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), m8.data_ptr(), None, 0,
-        B, Hq, Hkv, S, 128, bs, _native.strides(q), _native.strides(k), _native.strides(v),
-        _native.strides(out), _native.strides(m8), ctypes.c_float(1.0 / math.sqrt(128)), 1,
-        _native.stream_handle(dev))
-    _native.check(rc, "tasft_bsfa_prefill_fwd")
-    torch.cuda.synchronize()
+    out = _prefill_capi(q, k, v, mask, bs, True)
     assert torch.equal(out, out_ws)
     ref = orc.attention_block_gather(to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu()),
                                      mask.cpu().numpy(), bs, True)

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace_sizes():
     lib = _native.load_library()
-    assert lib.tasft_abi_version() == 4
+    assert lib.tasft_abi_version() == 5
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 8192, 64) == 256
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 0, 64) == 0
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
@@ -83,14 +83,17 @@ def test_invalid_arguments_return_errors_without_launch():
                                            64, _i64([8, 8, 2]), st3, st3, st3, st, 1.0, 1, None)
     assert rc == -1 and b"contiguous" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 128, 16, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 128, 16, 100, 4, st, st, st, st, st, 64, 1.0, None)
     assert rc == -2 and b"block_size" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 64, 12, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 64, 12, 100, 4, st, st, st, st, st, 64, 1.0, None)
     assert rc == -2 and b"page_size" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 64, 16, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 64, 16, 100, 4, st, st, st, st, st, 64, 1.0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 1 << 20, 1, 32,
+                                         8, 1024, 128, 64, 16, 0, 4, st, st, st, st, st, 64, 1.0, None)
+    assert rc == -1 and b"positive" in lib.tasft_last_error()
 
 
 def test_check_raises_kernel_error_with_message():
