@@ -196,16 +196,22 @@ int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float*
  * TASFTObjective.compute_gate_target (tasft/training/objectives.py:128-185).
  *
  * target [B, Hq, NB, NB] fp32 contiguous receives the block maxima of
- * q.k^T*scale (causal: -inf above the diagonal and for key > query), then, when
- * normalize is 0, a softmax over the flat NB*NB grid of each (b, h) (the reference);
+ * q.k^T*scale (+ attn_mask) (causal: -inf above the diagonal and for key > query), then,
+ * when normalize is 0, a softmax over the flat NB*NB grid of each (b, h) (the reference);
  * 1, a softmax over the key blocks of each row; 2, no normalisation (raw maxima).
  * Before the softmax, finite maxima are clamped to [-clamp, clamp] when clamp > 0
  * and divided by temperature (the variant of tasft/modules/tasft_attention.py:272-290).
+ * attn_mask: NULL, or the additive mask of tasft_attention.py:445-449 as fp32 with
+ * element (b, h, query, key) at attn_mask[b*s0 + h*s1 + query*s2 + key] for
+ * mask_strides = {s0, s1, s2} (0 broadcasts a dim: a key-padding row has s1 = s2 = 0).
+ * It must be addressable for every query and key below NB*block_size (values past
+ * seq_len are ignored), 16-byte aligned, strides non-negative multiples of 4.
  */
-int tasft_gate_target_fwd(const void* q, const void* k, float* target, int64_t batch,
-                          int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
-                          int64_t head_dim, int64_t block_size, const int64_t* q_strides,
-                          const int64_t* k_strides, float scale, int causal, int normalize,
+int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask, float* target,
+                          int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                          int64_t seq_len, int64_t head_dim, int64_t block_size,
+                          const int64_t* q_strides, const int64_t* k_strides,
+                          const int64_t* mask_strides, float scale, int causal, int normalize,
                           float temperature, float clamp, void* stream);
 
 /*

@@ -302,11 +302,13 @@ def gate_target_from_scores(scores: np.ndarray, bs: int) -> np.ndarray:
 
 
 def block_max(q, k, bs: int, causal: bool = True, scale: float | None = None,
-              dtype: type = np.float32) -> np.ndarray:
-    """Raw pooled maxima of ``QK^T*scale (+ triu(-inf))``, ``[B,Hq,NB,NB]``.
+              dtype: type = np.float32, attn_mask: np.ndarray | None = None) -> np.ndarray:
+    """Raw pooled maxima of ``QK^T*scale (+ triu(-inf)) (+ attn_mask)``, ``[B,Hq,NB,NB]``.
 
-    The scores are those of tasft_attention.py:426-443 (K head h // G for query head h);
-    pooling as objectives.py:170-178. Computed one query block at a time.
+    The scores are those of tasft_attention.py:426-449 (K head h // G for query head h):
+    the causal ``triu(-inf, 1)`` term, then the additive ``attn_mask`` — ``[B, S]`` is
+    broadcast as ``[:, None, None, :]`` (:446-448), a 4-D mask broadcasts to
+    ``[B, Hq, S, S]``. Pooling as objectives.py:170-178. One query block at a time.
     """
     b_, hq, s, d = q.shape
     g = hq // k.shape[1]
@@ -314,12 +316,18 @@ def block_max(q, k, bs: int, causal: bool = True, scale: float | None = None,
     sc = dtype(scale if scale is not None else 1.0 / math.sqrt(d))
     out = np.full((b_, hq, nb, nb), -np.inf, dtype=dtype)
     pad = nb * bs - s
+    am = None
+    if attn_mask is not None:
+        am = attn_mask[:, None, None, :] if attn_mask.ndim == 2 else attn_mask
+        am = np.broadcast_to(am.astype(dtype), (b_, hq, s, s))
     for b in range(b_):
         for h in range(hq):
             kh = k[b, h // g].astype(dtype)
             for i in range(nb):
                 q0, q1 = i * bs, min((i + 1) * bs, s)
                 sco = (q[b, h, q0:q1].astype(dtype) @ kh.T) * sc
+                if am is not None:
+                    sco = sco + am[b, h, q0:q1]
                 if causal:
                     sco = np.where(np.arange(s)[None, :] <= np.arange(q0, q1)[:, None], sco, -np.inf)
                 if pad:
@@ -351,9 +359,10 @@ def normalize_block_max(pooled: np.ndarray, normalize: str = "flat", temperature
 
 def gate_target_from_qk(q, k, bs: int, causal: bool = True, normalize: str = "flat",
                         temperature: float = 1.0, clamp: float | None = None,
-                        scale: float | None = None) -> np.ndarray:
+                        scale: float | None = None, attn_mask: np.ndarray | None = None) -> np.ndarray:
     """``normalize_block_max(block_max(q, k))`` — the score producer plus compute_gate_target."""
-    return normalize_block_max(block_max(q, k, bs, causal, scale), normalize, temperature, clamp)
+    return normalize_block_max(block_max(q, k, bs, causal, scale, attn_mask=attn_mask), normalize,
+                               temperature, clamp)
 
 
 # ----------------------------------------------------------------------------- stats

@@ -77,7 +77,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "tasft_gate_target_fwd": (
         _I,
-        [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _F, _I, _I, _F, _F, _P],
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _F, _I, _I,
+         _F, _F, _P],
     ),
     "tasft_mask_compact_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "tasft_mask_compact": (
@@ -128,6 +129,11 @@ def strides(t: torch.Tensor) -> ctypes.Array:
     return (ctypes.c_int64 * t.dim())(*t.stride())
 
 
+def strides_array(values) -> ctypes.Array:
+    """A list of element strides as a C int64 array."""
+    return (ctypes.c_int64 * len(values))(*values)
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -145,4 +151,4 @@ def check(status: int, what: str, context: dict[str, object] | None = None) -> N
 
 
 __all__ = ["EXPORTED_SYMBOLS", "LIB_PATH", "check", "is_available", "load_library", "ptr",
-           "stream_handle", "strides"]
+           "stream_handle", "strides", "strides_array"]

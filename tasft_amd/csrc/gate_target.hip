@@ -4,10 +4,11 @@
 //   scores = Q K^T * scale + triu(-inf, 1)            (tasft/modules/tasft_attention.py:426-443)
 //   pooled = max_pool2d(pad(scores, -inf), bs, bs)    (tasft/training/objectives.py:170-178)
 //   target = softmax(pooled over the flat NB_q*NB_k grid)  (objectives.py:181-185)
-// plus two options: a per-row softmax over key blocks (the "softmax over k-blocks" reading
-// of the target that the benchmark configuration uses) and the clamp(+-50) / temperature
-// variant of
-// tasft/modules/tasft_attention.py:272-290.
+// plus the additive attention mask of tasft_attention.py:445-449 (scores + mask before
+// the max-pool; a key-padding row [B, S] broadcast as [:, None, None, :], or a full
+// [B, 1|H, S, S] mask), and two options: a per-row softmax over key blocks (the "softmax
+// over k-blocks" reading of the target that the benchmark configuration uses) and the
+// clamp(+-50) / temperature variant of tasft/modules/tasft_attention.py:272-290.
 //
 // Kernel 1 computes each block maximum with the same S^T = K . Q^T bf16 MFMA tiling as
 // the prefill kernel (v_mfma_f32_32x32x16_bf16, fp32 accumulation) and keeps only the
@@ -21,7 +22,11 @@ struct GateTargetParams {
   const uint16_t* q;
   const uint16_t* k;
   float* out;  // [B, Hq, NB, NB] contiguous
-  int64_t sq[3], sk[3];
+  // Additive fp32 mask (masked kernels only): element (b, h, query, key) at
+  // amask[b * sam[0] + h * sam[1] + query * sam[2] + key], addressable for every query and
+  // key below NB * block; strides are multiples of 4 and the base is 16-byte aligned.
+  const float* amask;
+  int64_t sq[3], sk[3], sam[3];
   int B, Hq, Hkv, G, S, NB;
   float scale;
   int causal;
@@ -33,7 +38,9 @@ __device__ __forceinline__ void gt_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TASFT_LDS void*)dst, 16, voff, 0, 0, 0);
 }
 
-template <int BS, int D>
+// Without a mask (MASKED false) the raw maxima are scaled once at the end (scale > 0
+// commutes with max); with one, each score is scaled and the mask added before the max.
+template <int BS, int D, bool MASKED>
 __global__ void __launch_bounds__(BS / 32 * kWave)
 gate_target_blockmax_kernel(const GateTargetParams p) {
   constexpr int WAVES = BS / 32;
@@ -65,9 +72,12 @@ gate_target_blockmax_kernel(const GateTargetParams p) {
   const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
   float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NB + qb) * p.NB;
+  const float post_scale = MASKED ? 1.f : p.scale;
 
   const int qrow = qb * BS + wave * 32 + col;
   const bool qvalid = qrow < p.S;
+  const float* mrow = MASKED ? p.amask + b * p.sam[0] + h * p.sam[1] + (int64_t)qrow * p.sam[2]
+                             : nullptr;
   bf16x8_t qf[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -87,7 +97,7 @@ gate_target_blockmax_kernel(const GateTargetParams p) {
       float mx = red[(kb - 1) & 1][0];
 #pragma unroll
       for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[(kb - 1) & 1][w]);
-      orow[kb - 1] = mx * p.scale;
+      orow[kb - 1] = mx * post_scale;
     }
 #pragma unroll
     for (int c = tid; c < BS * D / 8; c += THREADS) {
@@ -112,8 +122,9 @@ gate_target_blockmax_kernel(const GateTargetParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float x = s[r];
+        const int key = key0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if constexpr (MASKED) x = x * p.scale + mrow[key];
         if (need_mask) {
-          const int key = key0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           if (!qvalid || key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
         }
         mloc = fmaxf(mloc, x);
@@ -127,7 +138,7 @@ gate_target_blockmax_kernel(const GateTargetParams p) {
     float mx = red[(kb_end - 1) & 1][0];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[(kb_end - 1) & 1][w]);
-    orow[kb_end - 1] = mx * p.scale;
+    orow[kb_end - 1] = mx * post_scale;
   }
 }
 
@@ -176,7 +187,11 @@ __device__ __forceinline__ int gt_swz(int r, int cc) {
   return cc ^ (D == 128 ? (r & 15) : ((r >> 1) & 7));
 }
 
-template <int D, int HPW, int WPH = 2>
+//
+// MASKED adds the caller's additive mask: each wave loads the mask values of its 32 x 64
+// sub-tile (float4 per lane and 4-key group) before it issues the next block's DMA, so the
+// fixed DMA wait also covers them, and adds them to the scaled scores before the max.
+template <int D, int HPW, bool MASKED, int WPH = 2>
 __global__ void __launch_bounds__(HPW * WPH * 64)
 gate_target_bs64_kernel(const GateTargetParams p) {
   constexpr int BS = 64;
@@ -228,6 +243,9 @@ gate_target_bs64_kernel(const GateTargetParams p) {
 
   const int qrow = qb * BS + rh * 32 + col;
   const bool qvalid = qrow < p.S;
+  const float* mrow = MASKED ? p.amask + b * p.sam[0] + h * p.sam[1] + (int64_t)qrow * p.sam[2]
+                             : nullptr;
+  const float post_scale = MASKED ? 1.f : p.scale;
   bf16x8_t qf[KSTEPS];
   auto load_q = [&]() {
 #pragma unroll
@@ -263,6 +281,17 @@ gate_target_bs64_kernel(const GateTargetParams p) {
   const int krow_l = kh * 32 + col;
   // One block from stage kt: this wave's 32 x 32 (or 32 x 64) sub-tile maximum.
   constexpr int NKT = WPH == 4 ? 1 : 2;  // 32-key tiles per wave
+  using f32x4_t = float __attribute__((ext_vector_type(4)));
+  f32x4_t mv[NKT][4];  // mask values of this lane's keys (MASKED)
+  auto load_mask = [&](int kb) {
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int t = 0; t < NKT; ++t)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+          mv[t][g4] = *(const f32x4_t*)(mrow + kb * BS + kh * 32 + 32 * t + 8 * g4 + 4 * half);
+    }
+  };
   auto block_max = [&](const uint8_t* kt, int kb) {
     f32x16_t s[NKT];
 #pragma unroll
@@ -278,6 +307,12 @@ gate_target_bs64_kernel(const GateTargetParams p) {
       }
     }
     const int key0 = kb * BS;
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int t = 0; t < NKT; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) s[t][rr] = s[t][rr] * p.scale + mv[t][rr >> 2][rr & 3];
+    }
     if ((p.causal && kb == qb) || (key0 + BS > p.S) || qb * BS + BS > p.S) {
 #pragma unroll
       for (int t = 0; t < NKT; ++t)
@@ -306,7 +341,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
       float m = rm[0];
 #pragma unroll
       for (int i = 1; i < WPH; ++i) m = fmaxf(m, rm[i]);
-      orow[kb] = m * p.scale;
+      orow[kb] = m * post_scale;
     }
   };
 
@@ -322,6 +357,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
     __builtin_amdgcn_s_waitcnt(kWaitBlock);  // this wave's DMA of block kb landed
     asm volatile("s_barrier" ::: "memory");  // every wave's; stage nxt free; red slot final
     if (kb > 0) store(kb - 1);
+    load_mask(kb);
     issue(nxt, min(kb + 2, kb_end - 1));
     const float m = block_max(cur, kb);
     if (lane == 0) red[kb & 1][hw][w4] = m;
@@ -344,38 +380,50 @@ gate_target_bs64_kernel(const GateTargetParams p) {
   store(kb_end - 1);
 }
 
-template <int D>
+template <int D, bool MASKED>
 static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t stream) {
   const int hpw = (p.G % 4 == 0) ? 4 : (p.G % 2 == 0 ? 2 : 1);
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq / hpw;
   if (hpw == 4)
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4>), dim3((unsigned)grid), dim3(4 * 128), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4, MASKED>), dim3((unsigned)grid), dim3(4 * 128), 0, stream, p);
   else if (hpw == 2)
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2>), dim3((unsigned)grid), dim3(2 * 128), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2, MASKED>), dim3((unsigned)grid), dim3(2 * 128), 0, stream, p);
   else
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1>), dim3((unsigned)grid), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1, MASKED>), dim3((unsigned)grid), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 
-template <int BS, int D>
+template <int BS, int D, bool MASKED>
 static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
-  hipLaunchKernelGGL((gate_target_blockmax_kernel<BS, D>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gate_target_blockmax_kernel<BS, D, MASKED>), dim3((unsigned)grid),
                      dim3(BS / 32 * kWave), 0, stream, p);
   return hipGetLastError();
+}
+
+template <bool MASKED>
+static hipError_t dispatch_blockmax(const GateTargetParams& p, int64_t block_size,
+                                    int64_t head_dim, hipStream_t s) {
+  if (block_size == 64 && head_dim == 128) return launch_blockmax_bs64<128, MASKED>(p, s);
+  if (block_size == 64 && head_dim == 64) return launch_blockmax_bs64<64, MASKED>(p, s);
+  if (block_size == 32 && head_dim == 128) return launch_blockmax<32, 128, MASKED>(p, s);
+  if (block_size == 32 && head_dim == 64) return launch_blockmax<32, 64, MASKED>(p, s);
+  if (block_size == 128 && head_dim == 128) return launch_blockmax<128, 128, MASKED>(p, s);
+  return launch_blockmax<128, 64, MASKED>(p, s);
 }
 
 }  // namespace tasft
 
 using namespace tasft;
 
-extern "C" int tasft_gate_target_fwd(const void* q, const void* k, float* target, int64_t batch,
-                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
-                                     int64_t head_dim, int64_t block_size,
-                                     const int64_t* q_strides, const int64_t* k_strides,
+extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask,
+                                     float* target, int64_t batch, int64_t num_q_heads,
+                                     int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                                     int64_t block_size, const int64_t* q_strides,
+                                     const int64_t* k_strides, const int64_t* mask_strides,
                                      float scale, int causal, int normalize, float temperature,
                                      float clamp, void* stream) {
-  if (!q || !k || !target || !q_strides || !k_strides)
+  if (!q || !k || !target || !q_strides || !k_strides || (attn_mask && !mask_strides))
     return set_error(kErrInvalidArgument, "gate_target: null pointer argument");
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0)
     return set_error(kErrInvalidArgument, "gate_target: batch, heads and seq_len must be positive");
@@ -401,6 +449,14 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, float* target
   }
   if ((((uintptr_t)q) & 15u) || (((uintptr_t)k) & 15u))
     return set_error(kErrInvalidArgument, "gate_target: tensors must be 16-byte aligned");
+  if (attn_mask) {
+    if (((uintptr_t)attn_mask) & 15u)
+      return set_error(kErrInvalidArgument, "gate_target: attn_mask must be 16-byte aligned");
+    for (int j = 0; j < 3; ++j)
+      if (mask_strides[j] < 0 || mask_strides[j] % 4 != 0)
+        return set_error(kErrInvalidArgument,
+                         "gate_target: attn_mask strides must be non-negative multiples of 4");
+  }
   const int64_t nb = (seq_len + block_size - 1) / block_size;
   if (nb * batch * num_q_heads > 0x7fffffffLL)
     return set_error(kErrUnsupported, "gate_target: problem too large for one launch");
@@ -409,9 +465,11 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, float* target
   p.q = (const uint16_t*)q;
   p.k = (const uint16_t*)k;
   p.out = target;
+  p.amask = attn_mask;
   for (int j = 0; j < 3; ++j) {
     p.sq[j] = q_strides[j];
     p.sk[j] = k_strides[j];
+    p.sam[j] = attn_mask ? mask_strides[j] : 0;
   }
   p.B = (int)batch;
   p.Hq = (int)num_q_heads;
@@ -423,13 +481,8 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, float* target
   p.causal = causal ? 1 : 0;
 
   hipStream_t s = (hipStream_t)stream;
-  hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_blockmax_bs64<128>(p, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_blockmax_bs64<64>(p, s);
-  else if (block_size == 32 && head_dim == 128) err = launch_blockmax<32, 128>(p, s);
-  else if (block_size == 32 && head_dim == 64) err = launch_blockmax<32, 64>(p, s);
-  else if (block_size == 128 && head_dim == 128) err = launch_blockmax<128, 128>(p, s);
-  else err = launch_blockmax<128, 64>(p, s);
+  hipError_t err = attn_mask ? dispatch_blockmax<true>(p, block_size, head_dim, s)
+                             : dispatch_blockmax<false>(p, block_size, head_dim, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate_target: block-max launch failed: %s", hipGetErrorString(err));
 

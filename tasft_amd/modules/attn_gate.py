@@ -5,19 +5,26 @@ same constructor and defaults, the same parameters and state-dict keys
 (``gate_proj_in.weight/.bias``, ``gate_proj_out.weight``) created and initialised in the
 same order, the same validation order and messages, and the same ``GateOutput`` fields.
 
-Inference (no autograd) runs the fused HIP kernels of ``libtasft_amd.so``: one pass over
-Q and K for the pooling (GQA-native, K pooled per KV head) and one pairwise kernel that
-keeps logits, sigmoid and threshold in fp32 — gate scores cluster within ~1e-3 of 0.5,
-below one bf16 ulp, so the reference's bf16 cast of the gate would move mask bits.
+Inference on bf16 GPU tensors (no autograd) runs the fused HIP kernels of
+``libtasft_amd.so``: one pass over Q and K for the pooling (GQA-native, K pooled per KV
+head) and one pairwise kernel that keeps logits, sigmoid and threshold in fp32 — gate
+scores cluster within ~1e-3 of 0.5, below one bf16 ulp, so the reference's bf16 cast of
+the gate would move mask bits. Those ``soft_scores`` are fp32 whatever the module dtype,
+and ``sparsity_ratio`` is read from a device counter on first access instead of a sync
+inside ``forward``.
+
+Everything else the reference gate accepts — CPU tensors, fp16 or fp32 Q/K, and calls that
+need gradients (gate training) — evaluates the reference formula itself with torch
+operations in the promoted dtype of the inputs and parameters, returning ``soft_scores`` in
+that dtype as the reference does. It uses ``W_in . cat(x, y) = W_q x + W_k y`` (the exact
+algebra of ``attn_gate.py:250-257``) so no ``[B,H,NB,NB,2D]`` tensor is built. This is the
+gate's own formulation on the devices and dtypes the kernel does not serve, not a second
+backend of the HIP path: a bf16 GPU call without autograd never takes it, and fails with
+``KernelError`` if the library is missing.
 
 Additive, keyword-compatible extensions: ``k`` may have ``Hkv`` heads (``Hq % Hkv == 0``);
-``threshold`` may be a per-head tensor ``[Hq]``; ``return_logits=True`` adds fp32 logits.
-Differences: ``soft_scores`` are fp32 whatever the module dtype; ``sparsity_ratio`` is
-computed from a device counter on first access instead of a sync inside ``forward``.
-
-When autograd is needed (gate training), ``forward`` evaluates the same formula with
-differentiable torch operations on the GPU; that path is the training side, not the
-inference kernel path.
+``threshold`` may be a per-head tensor ``[Hq]``; ``return_logits=True`` adds the logits;
+``force_diagonal=True`` keeps every diagonal block.
 """
 from __future__ import annotations
 
@@ -37,13 +44,13 @@ class GateOutput:
     """Gate result (reference ``attn_gate.py:30-46``); immutable after construction.
 
     Attributes:
-        soft_scores: ``[B, H, NB_q, NB_k]`` fp32 scores in [0, 1] (0 above the block
-            diagonal when causal).
+        soft_scores: ``[B, H, NB_q, NB_k]`` scores in [0, 1] (0 above the block diagonal
+            when causal): fp32 from the HIP kernel, the computation dtype otherwise.
         hard_mask: ``[B, H, NB_q, NB_k]`` bool, ``soft_scores >= threshold``.
         sparsity_ratio: fraction of False entries over the full grid (reference
             ``attn_gate.py:277``); read lazily from a device counter.
         num_blocks_q, num_blocks_k: block grid size.
-        logits: fp32 pre-sigmoid logits when requested, else None.
+        logits: pre-sigmoid logits (same dtype as ``soft_scores``) when requested, else None.
     """
 
     __slots__ = ("soft_scores", "hard_mask", "num_blocks_q", "num_blocks_k", "logits",
@@ -191,12 +198,18 @@ class AttnGate(nn.Module):
         """
         tau = threshold if threshold is not None else self.default_threshold
         self._validate(q, k)
-        if not q.is_cuda or not k.is_cuda:
-            raise KernelError("AttnGate runs on a ROCm device; got a CPU tensor",
-                              context={"device": str(q.device)})
-        if self._needs_grad(q, k):
-            return self._forward_autograd(q, k, tau, return_logits, force_diagonal)
-        return self._forward_hip(q, k, tau, return_logits, force_diagonal)
+        if q.device != k.device:
+            raise ValidationError(f"Q and K must be on the same device, got {q.device} vs {k.device}",
+                                  context={"q_device": str(q.device), "k_device": str(k.device)})
+        if self._kernel_applies(q, k):
+            return self._forward_hip(q, k, tau, return_logits, force_diagonal)
+        return self._forward_torch(q, k, tau, return_logits, force_diagonal)
+
+    def _kernel_applies(self, q: torch.Tensor, k: torch.Tensor) -> bool:
+        """The HIP kernel serves bf16 GPU tensors without autograd (head_dim multiple of 8,
+        at most 256); every other call evaluates the formula with torch operations."""
+        return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
+                and not self._needs_grad(q, k) and q.shape[-1] % 8 == 0 and q.shape[-1] <= 256)
 
     def _thresholds(self, tau: float | torch.Tensor, device: torch.device) -> torch.Tensor:
         if isinstance(tau, torch.Tensor):
@@ -248,29 +261,36 @@ class AttnGate(nn.Module):
         return GateOutput(soft_scores=soft, hard_mask=mask.view(torch.bool), num_blocks_q=nb,
                           num_blocks_k=nb, logits=logits, active_count=active)
 
-    def _forward_autograd(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
-                          return_logits: bool, force_diagonal: bool) -> GateOutput:
-        """Differentiable evaluation of the same formula for gate training.
+    def _forward_torch(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
+                       return_logits: bool, force_diagonal: bool) -> GateOutput:
+        """The reference formula (``attn_gate.py:241-277``) with torch operations.
 
-        Uses ``W_in . cat(x, y) = W_q x + W_k y`` so no ``[B,H,NB,NB,2D]`` tensor is built.
+        Computes in the promoted dtype of Q, K and the parameters (fp32 parameters with
+        bf16 inputs compute in fp32) and returns ``soft_scores`` in that dtype; the
+        causal zeroing, threshold and full-grid sparsity are the reference's. Gradients
+        flow to the parameters (and to Q/K if they require them).
         """
         B, H, S, D = q.shape
         Hkv = k.shape[1]
-        w = self.gate_proj_in.weight.float()
-        qb = self._pool_to_blocks(q.float())
-        kb = self._pool_to_blocks(k.float())
+        w_in = self.gate_proj_in.weight
+        dt = torch.promote_types(torch.promote_types(q.dtype, k.dtype), w_in.dtype)
+        w = w_in.to(dt)
+        qb = self._pool_to_blocks(q.to(dt))
+        kb = self._pool_to_blocks(k.to(dt))
         if Hkv != H:
             kb = kb.repeat_interleave(H // Hkv, dim=1)
-        uq = qb @ w[:, :D].t() + self.gate_proj_in.bias.float()
+        uq = qb @ w[:, :D].t() + self.gate_proj_in.bias.to(dt)
         uk = kb @ w[:, D:].t()
         hidden = F.relu(uq.unsqueeze(3) + uk.unsqueeze(2))
-        logits = (hidden @ self.gate_proj_out.weight.float().t()).squeeze(-1)
+        logits = (hidden @ self.gate_proj_out.weight.to(dt).t()).squeeze(-1)
         soft = torch.sigmoid(logits)
         nb = soft.shape[2]
         if self.is_causal:
             soft = soft * torch.ones(nb, nb, dtype=torch.bool, device=soft.device).tril()
-        taus = self._thresholds(tau, soft.device).view(1, H, 1, 1)
-        hard = soft >= taus
+        if isinstance(tau, torch.Tensor):
+            hard = soft >= self._thresholds(tau, soft.device).to(dt).view(1, H, 1, 1)
+        else:
+            hard = soft >= tau
         if force_diagonal:
             hard = hard | torch.eye(nb, dtype=torch.bool, device=soft.device)
         active = hard.sum().reshape(1)

@@ -8,10 +8,11 @@ Two entry points:
   ``max_pool2d``, softmax over the flat block grid.
 * ``gate_target_from_qk(q, k, ...)`` is the MI355X kernel path: it takes Q and K and never
   forms the score tensor. The HIP kernel computes each 64x64 block maximum of
-  ``Q K^T * scale`` with bf16 MFMA (causal: -inf above the diagonal), then normalises.
-  It replaces the score producer ``tasft/modules/tasft_attention.py:426-458`` followed by
-  ``compute_gate_target``; ``normalize="row"`` gives the per-row variant and
-  ``temperature``/``clamp`` the variant of ``tasft/modules/tasft_attention.py:272-290``.
+  ``Q K^T * scale`` with bf16 MFMA (causal: -inf above the diagonal; plus the caller's
+  additive ``attention_mask``), then normalises. It replaces the score producer
+  ``tasft/modules/tasft_attention.py:426-458`` followed by ``compute_gate_target``;
+  ``normalize="row"`` gives the per-row variant and ``temperature``/``clamp`` the variant
+  of ``tasft/modules/tasft_attention.py:272-290``.
 """
 from __future__ import annotations
 
@@ -68,12 +69,19 @@ def gate_target_from_qk(
     normalize: str = "flat",
     temperature: float = 1.0,
     clamp: float | None = None,
+    attention_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Gate target ``[B, Hq, NB, NB]`` fp32 from ``q [B,Hq,S,D]`` and ``k [B,Hkv,S,D]`` (bf16).
 
     Args:
         block_size: pooling block (32, 64 or 128).
         causal: add the ``triu(-inf, 1)`` mask of ``tasft_attention.py:434-443``.
+        attention_mask: optional additive mask added to the scaled scores before the
+            max-pool, as ``tasft_attention.py:445-449`` does: ``[B, S]`` is broadcast as
+            ``[:, None, None, :]`` (a key-padding row), a 4-D mask must broadcast to
+            ``[B, Hq, S, S]`` (e.g. HF's ``[B, 1, S, S]``). Any float or integer dtype; the
+            values are added as they are. NaN or +inf raises ``NaNDetectedError`` (the
+            scores would then hold them, which ``compute_gate_target`` rejects).
         scale: score scale, default ``1/sqrt(D)`` (``tasft_attention.py:427``).
         normalize: ``"flat"`` softmax over all NB*NB blocks of a head (reference trainer),
             ``"row"`` over the key blocks of each query block, ``"none"`` raw block maxima.
@@ -98,16 +106,52 @@ def gate_target_from_qk(
     q = q if (q.stride(-1) == 1 and all(s % 8 == 0 for s in q.stride()[:-1])) else q.contiguous()
     k = k if (k.stride(-1) == 1 and all(s % 8 == 0 for s in k.stride()[:-1])) else k.contiguous()
     nb = math.ceil(S / block_size)
+    mask_buf, mask_strides = None, None
+    if attention_mask is not None:
+        mask_buf, mask_strides = _padded_attention_mask(attention_mask, B, H, S, nb * block_size, q.device)
     out = torch.empty((B, H, nb, nb), dtype=torch.float32, device=q.device)
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
     status = lib.tasft_gate_target_fwd(
-        q.data_ptr(), k.data_ptr(), out.data_ptr(), B, H, k.shape[1], S, D, block_size,
-        _native.strides(q), _native.strides(k), sc, 1 if causal else 0, _NORMALIZE[normalize],
-        float(temperature), float(clamp) if clamp is not None else 0.0,
+        q.data_ptr(), k.data_ptr(), _native.ptr(mask_buf), out.data_ptr(), B, H, k.shape[1], S, D,
+        block_size, _native.strides(q), _native.strides(k), mask_strides, sc, 1 if causal else 0,
+        _NORMALIZE[normalize], float(temperature), float(clamp) if clamp is not None else 0.0,
         _native.stream_handle(q.device),
     )
     _native.check(status, "tasft_gate_target_fwd", {"shape": [B, H, S, D]})
     return out
+
+
+def _padded_attention_mask(mask: torch.Tensor, B: int, H: int, S: int, padded: int,
+                           device: torch.device):
+    """The kernel's form of an additive mask: fp32 ``[B|1, H|1, padded|1, padded]`` with the
+    caller's values in the leading ``S`` rows/columns (broadcast dims keep size 1 and get
+    stride 0), and its (b, h, query) element strides."""
+    ext = mask[:, None, None, :] if mask.ndim == 2 else mask
+    if ext.ndim != 4:
+        raise KernelError(f"attention_mask must be 2-D [B, S] or 4-D, got {mask.ndim}-D",
+                          context={"attention_mask": list(mask.shape)})
+    want = (B, H, S, S)
+    if ext.shape[3] != S or any(ext.shape[i] not in (1, want[i]) for i in range(3)):
+        raise KernelError(
+            f"attention_mask shape {tuple(mask.shape)} does not broadcast to {want}",
+            context={"attention_mask": list(mask.shape), "scores": list(want)},
+        )
+    ext = ext.to(device=device, dtype=torch.float32)
+    has_nan = bool(torch.isnan(ext).any())
+    has_pos_inf = bool((ext == float("inf")).any())
+    if has_nan or has_pos_inf:
+        raise NaNDetectedError(
+            f"Non-finite values detected in attn_scores: NaN={has_nan}, Inf={has_pos_inf}",
+            context={"tensor_name": "attention_mask", "has_nan": has_nan, "has_inf": has_pos_inf,
+                     "shape": list(mask.shape), "dtype": str(mask.dtype)},
+        )
+    rows = padded if ext.shape[2] > 1 else 1
+    buf = torch.zeros((ext.shape[0], ext.shape[1], rows, padded), dtype=torch.float32, device=device)
+    buf[:, :, : ext.shape[2], :S] = ext
+    st = buf.stride()
+    strides = [st[0] if buf.shape[0] > 1 else 0, st[1] if buf.shape[1] > 1 else 0,
+               st[2] if rows > 1 else 0]
+    return buf, _native.strides_array(strides)
 
 
 __all__ = ["TASFTObjective", "gate_target_from_qk"]

@@ -86,3 +86,67 @@ def test_config5_full_size_sampled_heads():
     for b, h in [(0, 0), (3, 31)]:
         ref = orc.gate_target_from_qk(to_np(q[b : b + 1, h : h + 1]), to_np(k[b : b + 1, h // 4 : h // 4 + 1]), 64)
         np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)
+
+
+MASK_CASES = [
+    # B, Hq, Hkv, S, D, bs, form
+    (2, 8, 2, 700, 128, 64, "padding_2d"),    # four heads per workgroup, ragged, key padding
+    (2, 4, 2, 640, 64, 64, "binary_2d"),      # two heads per workgroup; the reference adds 1/0
+    (2, 3, 3, 333, 128, 64, "hf_4d"),         # one head per workgroup, HF [B, 1, S, S] mask
+    (1, 4, 2, 300, 128, 32, "per_head_4d"),   # generic kernel, full per-head mask
+    (2, 2, 1, 400, 64, 128, "padding_2d"),    # generic kernel, block 128
+]
+
+
+def _attention_mask(form, B, Hq, S, seed):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.tensor([S] + [int(S * 0.6)] * (B - 1))
+    keep = torch.arange(S)[None, :] < lens[:, None]
+    if form == "padding_2d":
+        return torch.zeros(B, S).masked_fill(~keep, float("-inf"))
+    if form == "binary_2d":
+        return keep.to(torch.int64)  # HF's 1 = attend / 0 = pad, added as-is by the reference
+    if form == "hf_4d":
+        causal = torch.ones(S, S, dtype=torch.bool).tril()
+        allowed = causal[None] & keep[:, None, :]
+        return torch.zeros(B, 1, S, S).masked_fill(~allowed[:, None], torch.finfo(torch.float32).min)
+    return torch.randn(B, Hq, S, S, generator=g)
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "form"), MASK_CASES)
+def test_attention_mask_matches_oracle(B, Hq, Hkv, S, D, bs, form):
+    """Padded batches: the additive attention_mask of tasft_attention.py:445-449 is added to
+    the scaled scores before the max-pool (raw maxima, flat and row targets)."""
+    dev = require_gpu()
+    print(f"gate target mask {form} B={B} Hq={Hq} S={S} D={D} bs={bs}", flush=True)
+    q, k, _ = wl.qkv(wl.Shape(B, Hq, Hkv, S, D), 500 + S)
+    q = (q.float() * math.sqrt(D)).to(torch.bfloat16)  # unit-scale scores
+    mask = _attention_mask(form, B, Hq, S, 600 + S)
+    qd, kd, md = q.to(dev), k.to(dev), mask.to(dev)
+    m_np = mask.double().numpy()
+    raw_ref = orc.block_max(to_np(q), to_np(k), bs, True, dtype=np.float64, attn_mask=m_np)
+    raw = to_np(_gt(qd, kd, bs, normalize="none", attention_mask=md))
+    assert np.array_equal(np.isneginf(raw), np.isneginf(raw_ref))
+    fin = np.isfinite(raw_ref)
+    np.testing.assert_allclose(raw[fin], raw_ref[fin], rtol=RAW_RTOL, atol=1e-5)
+    for norm in ("flat", "row"):
+        got = to_np(_gt(qd, kd, bs, normalize=norm, attention_mask=md))
+        ref = orc.normalize_block_max(raw_ref, norm)
+        np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-7)
+    if form == "padding_2d":
+        # The padded rows' targets differ from the unmasked ones (the mask matters).
+        plain = to_np(_gt(qd, kd, bs))
+        assert not np.allclose(plain[1], orc.normalize_block_max(raw_ref, "flat")[1], atol=1e-4)
+
+
+def test_attention_mask_rejects_nan_and_bad_shapes():
+    from tasft_amd.exceptions import KernelError, NaNDetectedError
+
+    dev = require_gpu()
+    q, k, _ = (t.to(dev) for t in wl.qkv(wl.Shape(1, 4, 2, 128, 128), 7))
+    bad = torch.zeros(1, 128, device=dev)
+    bad[0, 5] = float("nan")
+    with pytest.raises(NaNDetectedError):
+        gate_target_from_qk(q, k, 64, attention_mask=bad)
+    with pytest.raises(KernelError, match="broadcast"):
+        gate_target_from_qk(q, k, 64, attention_mask=torch.zeros(1, 1, 128, 100, device=dev))

@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import dataclasses
 
+import numpy as np
 import pytest
 import torch
 
@@ -167,10 +168,92 @@ class TestAttnGateHost:
         with pytest.raises(ValidationError, match=msg):
             g(torch.randn(q), torch.randn(k))
 
-    def test_cpu_tensors_rejected(self):
+    def test_cpu_fp32_matches_reference_concat_formula(self):
+        """CPU fp32 runs the reference formula: logits equal the materialised-concat
+        Linear-ReLU-Linear of the oracle (attn_gate.py:248-257), masks follow from them."""
+        from oracle import tasft_oracle as orc
+
+        torch.manual_seed(3)
         g = AttnGate(num_heads=4, head_dim=32, block_size=8)
-        with pytest.raises(KernelError, match="ROCm device"):
-            g(torch.randn(1, 4, 64, 32), torch.randn(1, 4, 64, 32))
+        q, k = torch.randn(2, 4, 60, 32), torch.randn(2, 4, 60, 32)
+        out = g(q, k, threshold=0.5, return_logits=True)
+        w_in, b_in = g.gate_proj_in.weight.detach().numpy(), g.gate_proj_in.bias.detach().numpy()
+        w_out = g.gate_proj_out.weight.detach().numpy()
+        qb = orc.pool_to_blocks(q.double().numpy(), 8)
+        kb = orc.pool_to_blocks(k.double().numpy(), 8)
+        ref = orc.gate_logits_concat(qb, kb, w_in.astype(np.float64), b_in.astype(np.float64),
+                                     w_out.astype(np.float64))
+        np.testing.assert_allclose(out.logits.detach().numpy(), ref, rtol=1e-5, atol=1e-6)
+        assert out.soft_scores.dtype == torch.float32
+        soft = out.soft_scores.detach()
+        assert (soft[..., torch.ones(8, 8, dtype=torch.bool).triu(1)] == 0).all()
+        assert torch.equal(out.hard_mask, soft >= 0.5)
+        assert out.sparsity_ratio == pytest.approx(1.0 - out.hard_mask.float().mean().item())
+
+    # The shapes, ranges and edge cases of the reference's own CPU tests
+    # (tests/unit/test_attn_gate.py:123-141, 160-236, 244-278, 289-318).
+    @pytest.mark.parametrize(("B", "H", "S", "D", "bs"), [
+        (1, 4, 64, 32, 8), (2, 8, 128, 64, 16), (4, 16, 256, 128, 32), (1, 32, 2048, 128, 64)])
+    def test_cpu_output_shapes(self, B, H, S, D, bs):
+        g = AttnGate(num_heads=H, head_dim=D, block_size=bs)
+        out = g(torch.randn(B, H, S, D), torch.randn(B, H, S, D))
+        nb = (S + bs - 1) // bs
+        assert isinstance(out, GateOutput)
+        assert out.soft_scores.shape == (B, H, nb, nb) and out.hard_mask.shape == (B, H, nb, nb)
+        assert out.hard_mask.dtype == torch.bool
+        assert (out.num_blocks_q, out.num_blocks_k) == (nb, nb)
+
+    @pytest.mark.parametrize("scale", [1.0, 1000.0, 0.0])
+    def test_cpu_scores_in_unit_interval(self, scale):
+        g = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        out = g(torch.randn(2, 4, 64, 32) * scale, torch.randn(2, 4, 64, 32) * scale)
+        s = out.soft_scores
+        assert not s.isnan().any() and not s.isinf().any()
+        assert s.min() >= 0.0 and s.max() <= 1.0
+
+    def test_cpu_sparsity_edges_and_compute_sparsity(self):
+        g = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        q, k = torch.randn(1, 4, 64, 32), torch.randn(1, 4, 64, 32)
+        out0 = g(q, k, threshold=0.0)
+        assert out0.sparsity_ratio == pytest.approx(0.0, abs=1e-6) and out0.hard_mask.all()
+        out1 = g(q, k, threshold=1.0 + 1e-6)
+        assert out1.sparsity_ratio == pytest.approx(1.0, abs=1e-6) and not out1.hard_mask.any()
+        out = g(q, k, threshold=0.5)
+        assert g.compute_sparsity(out.soft_scores, 0.5) == pytest.approx(out.sparsity_ratio, abs=1e-6)
+
+    def test_cpu_bf16_and_fp16_modules(self):
+        for dt in (torch.bfloat16, torch.float16):
+            g = AttnGate(num_heads=8, head_dim=64, block_size=16).to(dt)
+            out = g(torch.randn(2, 8, 256, 64, dtype=dt), torch.randn(2, 8, 256, 64, dtype=dt))
+            assert out.soft_scores.dtype == dt  # the module dtype, as the reference returns
+            assert not out.soft_scores.isnan().any() and not out.soft_scores.isinf().any()
+            assert out.soft_scores.min() >= 0.0 and out.soft_scores.max() <= 1.0
+        g32 = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        g16 = AttnGate(num_heads=4, head_dim=32, block_size=8).to(torch.bfloat16)
+        q = torch.randn(1, 4, 64, 32)
+        assert g32(q, q).soft_scores.shape == g16(q.bfloat16(), q.bfloat16()).soft_scores.shape
+
+    @pytest.mark.parametrize(("S", "bs"), [(65, 64), (100, 64), (127, 64), (33, 16), (1, 8), (7, 8), (9, 8)])
+    def test_cpu_non_divisible_seq_len(self, S, bs):
+        g = AttnGate(num_heads=4, head_dim=32, block_size=bs)
+        out = g(torch.randn(1, 4, S, 32), torch.randn(1, 4, S, 32))
+        nb = (S + bs - 1) // bs
+        assert out.num_blocks_q == nb and out.soft_scores.shape == (1, 4, nb, nb)
+
+    def test_cpu_gqa_and_per_head_threshold(self):
+        g = AttnGate(num_heads=8, head_dim=32, block_size=8)
+        q, k = torch.randn(1, 8, 64, 32), torch.randn(1, 2, 64, 32)
+        a = g(q, k, threshold=torch.full((8,), 0.5))
+        b = g(q, k.repeat_interleave(4, dim=1), threshold=0.5)
+        torch.testing.assert_close(a.soft_scores, b.soft_scores)
+        assert torch.equal(a.hard_mask, b.hard_mask)
+
+    def test_cpu_gradients_reach_gate_parameters(self):
+        g = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        out = g(torch.randn(1, 4, 64, 32), torch.randn(1, 4, 64, 32))
+        out.soft_scores.sum().backward()
+        for name, p in g.named_parameters():
+            assert p.grad is not None and torch.isfinite(p.grad).all() and p.grad.abs().sum() > 0, name
 
     def test_gate_output_frozen_and_lazy(self):
         out = GateOutput(soft_scores=torch.zeros(1, 1, 2, 2), hard_mask=torch.zeros(1, 1, 2, 2, dtype=torch.bool),

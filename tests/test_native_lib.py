@@ -100,6 +100,7 @@ def test_check_raises_kernel_error_with_message():
     from tasft_amd.exceptions import KernelError
     lib = _native.load_library()
     st = _i64([0, 0, 0, 1])
-    rc = lib.tasft_gate_target_fwd(None, None, None, 1, 1, 1, 64, 128, 64, st, st, 1.0, 1, 0, 1.0, 0.0, None)
+    rc = lib.tasft_gate_target_fwd(None, None, None, None, 1, 1, 1, 64, 128, 64, st, st, None, 1.0, 1, 0,
+                                   1.0, 0.0, None)
     with pytest.raises(KernelError, match="null pointer"):
         _native.check(rc, "tasft_gate_target_fwd")

@@ -329,6 +329,46 @@ def test_block_max_equals_explicit_scores(causal):
     np.testing.assert_allclose(row.sum(-1), 1.0, rtol=1e-12)
 
 
+@pytest.mark.parametrize("form", ["padding_2d", "binary_2d", "hf_4d", "per_head_4d"])
+def test_block_max_with_attention_mask_equals_reference_composition(form):
+    """Scores built as tasft_attention.py:426-449 does (torch: matmul * scale, + triu(-inf),
+    + attention_mask with a 2-D mask broadcast as [:, None, None, :]), then the reference
+    pooling path, against the oracle's fused block maxima."""
+    rng = np.random.default_rng(12)
+    B, H, Hkv, S, D, bs = 2, 4, 2, 45, 8, 16
+    q = rng.standard_normal((B, H, S, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    sc = 0.3
+    lens = [45, 30]
+    if form == "padding_2d":
+        mask = np.zeros((B, S), dtype=np.float32)
+        mask[1, 30:] = -np.inf
+    elif form == "binary_2d":
+        mask = (np.arange(S)[None, :] < np.array(lens)[:, None]).astype(np.float32)  # 1 keep, 0 pad
+    elif form == "hf_4d":
+        fmin = np.finfo(np.float32).min
+        allowed = (np.arange(S)[None, None, :] <= np.arange(S)[None, :, None]) & \
+                  (np.arange(S)[None, None, :] < np.array(lens)[:, None, None])
+        mask = np.where(allowed, 0.0, fmin).astype(np.float32)[:, None]  # [B, 1, S, S]
+    else:
+        mask = rng.standard_normal((B, H, S, S)).astype(np.float32)
+    qt, kt = torch.from_numpy(q).double(), torch.from_numpy(k).double().repeat_interleave(2, dim=1)
+    weights = torch.matmul(qt, kt.transpose(-2, -1)) * sc
+    weights = weights + torch.triu(torch.full((S, S), float("-inf"), dtype=torch.float64), 1)[None, None]
+    ext = torch.from_numpy(mask).double()
+    if ext.ndim == 2:
+        ext = ext[:, None, None, :]
+    weights = weights + ext
+    ref = orc.gate_target_from_scores(weights.numpy(), bs)
+    got = orc.gate_target_from_qk(q, k, bs, causal=True, scale=sc, attn_mask=mask)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-9)
+    raw = orc.block_max(q, k, bs, True, sc, attn_mask=mask)
+    nb = raw.shape[-1]
+    pooled = torch.nn.functional.max_pool2d(
+        torch.nn.functional.pad(weights, (0, nb * bs - S, 0, nb * bs - S), value=-math.inf), bs, bs)
+    np.testing.assert_allclose(raw, pooled.numpy(), rtol=1e-5, atol=1e-6)
+
+
 def test_gate_target_clamp_temperature_variant():
     pooled = np.array([[[[100.0, -np.inf], [3.0, -70.0]]]])
     got = orc.normalize_block_max(pooled, "flat", temperature=2.0, clamp=50.0)
