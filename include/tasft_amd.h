@@ -132,6 +132,32 @@ int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cach
                           void* stream);
 
 /*
+ * tasft_bsfa_decode_fwd without a workspace: the variant that allocates nothing.
+ * No counterpart in the reference. It is for callers that cannot allocate device memory
+ * or take a caller-sized workspace: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.
+ *
+ * Arguments and results are those of tasft_bsfa_decode_fwd minus the workspace. The split
+ * partials go to a static device array of TASFT_DECODE_NOALLOC_MAX_BYTES bytes inside the
+ * library (one per GPU, held until the process ends; its address is looked up on the
+ * first call on each device, with the stream's device current). A call whose
+ * tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits) exceeds it
+ * returns TASFT_ERR_WORKSPACE without launching. With num_splits == 1 the array is not
+ * touched. Every call on one GPU shares the array: calls that overlap on one GPU (on
+ * different streams, or from different threads without ordering) race and give wrong
+ * results; calls ordered on one stream are safe.
+ */
+#define TASFT_DECODE_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+int tasft_bsfa_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                  void* out, const uint8_t* block_mask, const int32_t* kv_lens,
+                                  int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                  int64_t kv_len_max, int64_t head_dim, int64_t block_size,
+                                  int64_t num_splits, const int64_t* q_strides,
+                                  const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* o_strides, const int64_t* mask_strides,
+                                  float scale, void* stream);
+
+/*
  * Split-K block-sparse decode over a paged KV cache (vLLM's block-table layout).
  * Stands in for the paged dense decode that tasft/inference/vllm_patch.py:189-196 and
  * :215-252 hand to vLLM's PagedAttention; its result equals tasft_bsfa_decode_fwd on the

@@ -17,6 +17,7 @@ from tasft_amd.exceptions import KernelError
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtasft_amd.so"
 
 # Every symbol the header include/tasft_amd.h declares.
+DECODE_NOALLOC_MAX_BYTES = 16 << 20  # TASFT_DECODE_NOALLOC_MAX_BYTES
 EXPORTED_SYMBOLS = (
     "tasft_last_error",
     "tasft_abi_version",
@@ -26,6 +27,7 @@ EXPORTED_SYMBOLS = (
     "tasft_bsfa_decode_workspace_bytes",
     "tasft_bsfa_decode_fwd",
     "tasft_bsfa_decode_paged_fwd",
+    "tasft_bsfa_decode_fwd_noalloc",
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
     "tasft_gate_target_fwd",
@@ -68,6 +70,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64, _F, _P],
+    ),
+    "tasft_bsfa_decode_fwd_noalloc": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _P],
     ),
     "tasft_gate_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_fwd": (

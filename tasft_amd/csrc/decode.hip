@@ -22,6 +22,10 @@
 // second kernel merges them.
 #include "common.h"
 
+#include <mutex>
+
+#include "../../include/tasft_amd.h"
+
 namespace tasft {
 
 constexpr int kDecodeMaxG = 8;    // query heads per KV head handled by one workgroup
@@ -625,14 +629,14 @@ extern "C" size_t tasft_bsfa_decode_workspace_bytes(int64_t batch, int64_t num_q
   return (size_t)(batch * num_q_heads * num_splits) * (size_t)(head_dim + 2) * sizeof(float);
 }
 
-extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
-                                     void* out, const uint8_t* block_mask, const int32_t* kv_lens,
-                                     void* workspace, size_t workspace_bytes, int64_t batch,
-                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t kv_len_max,
-                                     int64_t head_dim, int64_t block_size, int64_t num_splits,
-                                     const int64_t* q_strides, const int64_t* k_strides,
-                                     const int64_t* v_strides, const int64_t* o_strides,
-                                     const int64_t* mask_strides, float scale, void* stream) {
+static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, void* out,
+                      const uint8_t* block_mask, const int32_t* kv_lens, void* workspace,
+                      size_t workspace_bytes, int64_t batch, int64_t num_q_heads,
+                      int64_t num_kv_heads, int64_t kv_len_max, int64_t head_dim,
+                      int64_t block_size, int64_t num_splits, const int64_t* q_strides,
+                      const int64_t* k_strides, const int64_t* v_strides,
+                      const int64_t* o_strides, const int64_t* mask_strides, float scale,
+                      void* stream) {
   if (!q || !k_cache || !v_cache || !out || !block_mask || !workspace || !q_strides ||
       !k_strides || !v_strides || !o_strides || !mask_strides)
     return set_error(kErrInvalidArgument, "decode: null pointer argument");
@@ -718,6 +722,75 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
   if (err != hipSuccess)
     return set_error(kErrLaunch, "decode: launch failed: %s", hipGetErrorString(err));
   return kOk;
+}
+
+extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
+                                     void* out, const uint8_t* block_mask, const int32_t* kv_lens,
+                                     void* workspace, size_t workspace_bytes, int64_t batch,
+                                     int64_t num_q_heads, int64_t num_kv_heads, int64_t kv_len_max,
+                                     int64_t head_dim, int64_t block_size, int64_t num_splits,
+                                     const int64_t* q_strides, const int64_t* k_strides,
+                                     const int64_t* v_strides, const int64_t* o_strides,
+                                     const int64_t* mask_strides, float scale, void* stream) {
+  return decode_fwd(q, k_cache, v_cache, out, block_mask, kv_lens, workspace, workspace_bytes,
+                    batch, num_q_heads, num_kv_heads, kv_len_max, head_dim, block_size,
+                    num_splits, q_strides, k_strides, v_strides, o_strides, mask_strides, scale,
+                    stream);
+}
+
+// ---------------------------------------------------------------------------- no allocation
+// Static device scratch for tasft_bsfa_decode_fwd_noalloc: the split partials (the
+// workspace of tasft_bsfa_decode_fwd) of every call on a GPU live in this one array, which
+// each GPU the library runs on holds until the process ends. Its device address is taken
+// once per device with hipGetSymbolAddress (the name itself is a host-side stand-in).
+constexpr size_t kDecodeScratchBytes = TASFT_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+
+// Device address of `scratch` on the current device (looked up on the first call there).
+static int decode_scratch_ptr(void** out) {
+  static std::mutex mu;
+  static void* ptrs[kMaxScratchDevices] = {};
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(kErrUnsupported, "decode_noalloc: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return set_error(kErrLaunch, "decode_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(err));
+    ptrs[dev] = ptr;
+  }
+  *out = ptrs[dev];
+  return kOk;
+}
+
+extern "C" int tasft_bsfa_decode_fwd_noalloc(
+    const void* q, const void* k_cache, const void* v_cache, void* out, const uint8_t* block_mask,
+    const int32_t* kv_lens, int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t kv_len_max, int64_t head_dim, int64_t block_size, int64_t num_splits,
+    const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+    const int64_t* o_strides, const int64_t* mask_strides, float scale, void* stream) {
+  const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+  if (need > kDecodeScratchBytes)
+    return set_error(kErrWorkspace,
+                     "decode_noalloc: %lld splits of %lld x %lld heads need %zu bytes of partials, "
+                     "more than the %zu-byte static scratch (use fewer splits, or "
+                     "tasft_bsfa_decode_fwd with a workspace)",
+                     (long long)num_splits, (long long)batch, (long long)num_q_heads, need,
+                     kDecodeScratchBytes);
+  void* ws = nullptr;
+  const int rc = decode_scratch_ptr(&ws);
+  if (rc != kOk) return rc;
+  return decode_fwd(q, k_cache, v_cache, out, block_mask, kv_lens, ws, kDecodeScratchBytes, batch,
+                    num_q_heads, num_kv_heads, kv_len_max, head_dim, block_size, num_splits,
+                    q_strides, k_strides, v_strides, o_strides, mask_strides, scale, stream);
 }
 
 extern "C" int tasft_bsfa_decode_paged_fwd(
