@@ -7,8 +7,8 @@ diagonal forced on). Inputs are resident in HBM before timing. ``value`` is toke
 the step. The same run also measures, as extra figures, the split-K decode (config 3:
 B=64, S_kv=32768, 51 of 512 blocks per KV head) in HBM GB/s, with the same tokens also
 read from a 16-token paged cache (checked bit-identical), the Qwen-2.5-7B prefill
-(config 4) and the gate target (config 5), plus a CPU baseline of the oracle on a bounded
-sample of config 2.
+(config 4) and the gate target (config 5), plus the reference CPU path (fp32 torch) of
+config 2 on a bounded sample of its (batch, head) chunks.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--extras decode,qwen,gate_target|none]
                        [--no-extras] [--no-cpu-baseline] [--copy-probe MIB]
@@ -248,43 +248,70 @@ def bench_gate_target(torch, dev, steps, warmup):
 
 
 def cpu_baseline(res, budget_s: float = 20.0):
-    """Oracle (numpy) gate + block-sparse attention on a sample of config-2 heads."""
-    import numpy as np
+    """The reference CPU path of one config-2 step, timed on the host cores.
 
-    from oracle import tasft_oracle as orc
+    The reference has no CPU block-sparse attention (its CPU attention is dense SDPA that
+    ignores the mask, tasft/kernels/block_sparse_fa.py:572), so this is the fp32 torch
+    restatement the benchmark plan defines, per (batch, head) chunk:
+      * gate: the reference formula as written (tasft/modules/attn_gate.py:241-277): zero-
+        padded block means, the materialised [NB, NB, 2D] pair concat, Linear -> ReLU ->
+        Linear -> sigmoid -> causal zero -> the head's tau, diagonal forced on;
+      * attention: masked dense attention, the block mask expanded to a token mask and
+        AND-ed with the causal mask, empty rows 0 (block_sparse_fa.py:192-258).
+    Chunks run in a seeded random order until ``budget_s`` is spent; the time is scaled
+    linearly to all chunks.
+    """
+    import random
 
-    try:
-        import threadpoolctl
-        threads = max((i.get("num_threads", 1) for i in threadpoolctl.threadpool_info()), default=1)
-    except Exception:  # noqa: BLE001
-        threads = os.cpu_count() or 1
+    import torch
+    import torch.nn.functional as F
+
     shape = res["shape"]
-    q, k, v = (t.float().numpy() for t in res["host"])
+    threads = torch.get_num_threads()
+    q, k, v = (t.float() for t in res["host"])
     gate = res["gate"]
-    w_in = gate.gate_proj_in.weight.detach().float().cpu().numpy()
-    b_in = gate.gate_proj_in.bias.detach().float().cpu().numpy()
-    w_out = gate.gate_proj_out.weight.detach().float().cpu().numpy()
-    taus = res["taus"].cpu().numpy()
+    w_in = gate.gate_proj_in.weight.detach().float().cpu()
+    b_in = gate.gate_proj_in.bias.detach().float().cpu()
+    w_out = gate.gate_proj_out.weight.detach().float().cpu()
+    taus = res["taus"].float().cpu()
+    bs, nb, S = shape.block, shape.nb, shape.seq
     grp = shape.q_heads // shape.kv_heads
+    causal_blocks = torch.ones(nb, nb, dtype=torch.bool).tril()
+    causal_tokens = torch.ones(S, S, dtype=torch.bool).tril()
+    scale = 1.0 / math.sqrt(shape.head_dim)
+
+    def one_chunk(b, h):
+        qh, kh, vh = q[b, h], k[b, h // grp], v[b, h // grp]
+        pad = nb * bs - S
+        qb = F.pad(qh, (0, 0, 0, pad)).view(nb, bs, -1).mean(1)
+        kb = F.pad(kh, (0, 0, 0, pad)).view(nb, bs, -1).mean(1)
+        cat = torch.cat([qb[:, None, :].expand(nb, nb, -1), kb[None, :, :].expand(nb, nb, -1)], dim=-1)
+        logits = F.linear(F.relu(F.linear(cat, w_in, b_in)), w_out).squeeze(-1)
+        soft = torch.sigmoid(logits) * causal_blocks
+        hard = (soft >= taus[h]) | torch.eye(nb, dtype=torch.bool)
+        tok = hard.repeat_interleave(bs, 0).repeat_interleave(bs, 1)[:S, :S] & causal_tokens
+        scores = (qh @ kh.T) * scale
+        scores = scores.masked_fill(~tok, float("-inf"))
+        p = torch.softmax(scores, dim=-1).nan_to_num(0.0)
+        return p @ vh
+
     order = [(b, h) for b in range(shape.batch) for h in range(shape.q_heads)]
-    rng = np.random.default_rng(0)
-    rng.shuffle(order)
+    random.Random(0).shuffle(order)
     done, t0 = 0, time.perf_counter()
-    for b, h in order:
-        qh, kh, vh = q[b : b + 1, h : h + 1], k[b : b + 1, h // grp : h // grp + 1], v[b : b + 1, h // grp : h // grp + 1]
-        logits = orc.gate_logits(qh, kh, w_in, b_in, w_out, shape.block)
-        _, hard = orc.threshold_mask(logits, float(taus[h]), True)
-        hard = hard | np.eye(shape.nb, dtype=bool)
-        orc.attention_block_gather(qh, kh, vh, hard, shape.block, True)
-        done += 1
-        if time.perf_counter() - t0 > budget_s or done >= 32:
-            break
-    per_head = (time.perf_counter() - t0) / done
-    total_s = per_head * len(order)
-    return {"value": shape.batch * shape.seq / total_s, "unit": "tokens/s", "cores": int(threads),
+    with torch.no_grad():
+        for b, h in order:
+            one_chunk(b, h)
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    elapsed = time.perf_counter() - t0
+    total_s = elapsed / done * len(order)
+    return {"value": round(shape.batch * shape.seq / total_s, 1), "unit": "tokens/s", "cores": int(threads),
             "kind": "port",
-            "sample": f"oracle gate + block-gather attention (numpy fp32) on {done} of {len(order)} "
-                      f"(batch, head) pairs of config 2, scaled linearly to all heads"}
+            "os_cpu_count": os.cpu_count(), "torch_num_threads": int(threads),
+            "sample": f"reference gate formula (materialised pair concat) + masked dense attention, "
+                      f"torch fp32, on {done} of {len(order)} (batch, head) chunks of config 2 "
+                      f"({elapsed:.1f} s), scaled linearly to all chunks"}
 
 
 def copy_probe(torch, dev, mib: int) -> int:
