@@ -33,7 +33,7 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (5). */
+/* ABI version of this library (6). */
 int tasft_abi_version(void);
 
 /*
@@ -201,6 +201,10 @@ size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t nu
  * contiguous: soft_scores fp32 (sigmoid of the logit, exactly 0 above the block
  * diagonal when causal), logits fp32 (may be NULL), hard_mask bytes (soft >= tau).
  * active_count: one uint64 in device memory receiving the number of set mask bytes.
+ * q_means [B, Hq, NB, D], k_means [B, Hkv, NB, D] fp32 (each may be NULL) receive the
+ * zero-padded block means (what tasft_gate_bwd's caller needs for the W_in gradient).
+ * The workspace afterwards holds u = W_q qbar + b_in [B, Hq, NB, hidden] followed by
+ * v = W_k kbar [B, Hkv, NB, hidden] (fp32), the input of tasft_gate_bwd.
  * flags: TASFT_GATE_CAUSAL (zero the upper block triangle, reference is_causal) |
  * TASFT_GATE_FORCE_DIAGONAL (set the diagonal blocks in hard_mask regardless of tau).
  * head_dim a multiple of 8, at most 256; any block_size >= 1.
@@ -209,11 +213,35 @@ size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t nu
 #define TASFT_GATE_FORCE_DIAGONAL 2
 int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float* b_in,
                    const float* w_out, const float* thresholds, float* soft_scores, float* logits,
-                   uint8_t* hard_mask, unsigned long long* active_count, void* workspace,
-                   size_t workspace_bytes, int64_t batch, int64_t num_q_heads,
-                   int64_t num_kv_heads, int64_t seq_len, int64_t head_dim, int64_t block_size,
-                   int64_t hidden, const int64_t* q_strides, const int64_t* k_strides, int flags,
-                   void* stream);
+                   uint8_t* hard_mask, unsigned long long* active_count, float* q_means,
+                   float* k_means, void* workspace, size_t workspace_bytes, int64_t batch,
+                   int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
+                   int64_t block_size, int64_t hidden, const int64_t* q_strides,
+                   const int64_t* k_strides, int flags, void* stream);
+
+/*
+ * Backward of the gate's pairwise MLP, for gate training: the gradient the reference gets
+ * from autograd through AttnGate.forward (tasft/modules/attn_gate.py:248-273), without the
+ * [B, H, NB, NB, hidden] activations.
+ *
+ * soft_scores and grad_soft [B, Hq, NB, NB] fp32 contiguous (the forward's soft scores and
+ * dL/dsoft); fwd_workspace: the workspace of the tasft_gate_fwd call that produced them.
+ * With g = grad_soft * soft * (1 - soft) (0 where the causal zero applied) and
+ * pre[i][j][c] = u[i][c] + v[j][c], partials (>= tasft_gate_bwd_workspace_bytes, fp32)
+ * receives, for T = ceil(NB / 32) tiles:
+ *   du_part [T][B][Hq][NB][hidden]: sum over the keys of key tile t of g * (pre > 0),
+ *   dv_part [T][B][Hq][NB][hidden]: sum over the queries of query tile t of g * (pre > 0),
+ *   dw_part [B*Hq*T*T][hidden]: sum over the tile's pairs of g * relu(pre).
+ * Then dL/dw_out = sum(dw_part), dL/du = w_out * sum_t du_part, dL/dv = w_out * (sum_t
+ * dv_part, summed over the query heads of each KV head), and dL/dW_in, dL/db_in follow from
+ * u and v's definitions (plain GEMMs with the block means). flags: TASFT_GATE_CAUSAL.
+ */
+size_t tasft_gate_bwd_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t seq_len,
+                                      int64_t block_size, int64_t hidden);
+int tasft_gate_bwd(const float* soft_scores, const float* grad_soft, const void* fwd_workspace,
+                   size_t fwd_workspace_bytes, float* partials, size_t partials_bytes,
+                   int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                   int64_t block_size, int64_t hidden, int flags, void* stream);
 
 /*
  * Gate target from Q and K, without the [B, H, S, S] score tensor.
@@ -239,6 +267,20 @@ int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask, 
                           const int64_t* q_strides, const int64_t* k_strides,
                           const int64_t* mask_strides, float scale, int causal, int normalize,
                           float temperature, float clamp, void* stream);
+
+/*
+ * KL gate loss: replaces TASFTObjective.compute_gate_loss (tasft/training/objectives.py:187-221),
+ * KL(target || gate) with the gate scores normalised over each (b, h) grid and reduced
+ * with "batchmean". Together with tasft_gate_target_fwd it is the per-layer gate term of
+ * TASFTObjective.compute (objectives.py:316-346) without the [B, H, S, S] scores.
+ *
+ * gate_scores, target [B, H, NBq, NBk] fp32 contiguous. loss_partials [B*H] receives each
+ * (b, h)'s KL sum (the loss is their sum divided by B); grad_scores (NULL allowed) receives
+ * d(loss)/d(gate_scores).
+ */
+int tasft_gate_kl_fwd(const float* gate_scores, const float* target, int64_t batch,
+                      int64_t num_heads, int64_t num_blocks_q, int64_t num_blocks_k,
+                      float* loss_partials, float* grad_scores, void* stream);
 
 /*
  * Block mask -> compressed rows (CSR) of its active blocks.

@@ -26,6 +26,8 @@ asks for float64. How each function is pinned (checked independently of itself):
   test_numerical_correctness.py:119-157 and :714-721; torch max_pool2d + softmax.
 * ``block_max`` / ``gate_target_from_qk``: equal ``gate_target_from_scores`` applied to
   explicitly built scores.
+* ``gate_kl_loss``: torch ``F.kl_div(..., reduction="batchmean")`` composed as the reference
+  does (tests/test_oracle.py); ``gate_kl_grad``: torch autograd of that composition.
 * ``sparsity_stats`` / ``estimate_speedup``: literal values of tests/unit/test_kernel.py.
 * ``mask_to_csr`` / ``indices_to_mask``: a hand-checked literal example and the round
   trip dense -> CSR -> dense (numpy ``nonzero`` / fancy-index scatter).
@@ -363,6 +365,39 @@ def gate_target_from_qk(q, k, bs: int, causal: bool = True, normalize: str = "fl
     """``normalize_block_max(block_max(q, k))`` — the score producer plus compute_gate_target."""
     return normalize_block_max(block_max(q, k, bs, causal, scale, attn_mask=attn_mask), normalize,
                                temperature, clamp)
+
+
+# ----------------------------------------------------------------------------- gate loss
+KL_EPS = 1e-8  # objectives.py:39
+
+
+def gate_kl_loss(soft: np.ndarray, target: np.ndarray) -> float:
+    """KL(target || gate) with "batchmean" (objectives.py:187-221).
+
+    Per (b, h) the scores are normalised over the flat NB_q*NB_k grid, ``g / (sum g + eps)``,
+    then ``log(. + eps)``; entries with ``target == 0`` contribute 0; the sum over (b, h) is
+    divided by B.
+    """
+    b, h = soft.shape[:2]
+    g = soft.reshape(b, h, -1).astype(np.float64)
+    t = target.reshape(b, h, -1).astype(np.float64)
+    dist = g / (g.sum(-1, keepdims=True) + KL_EPS)
+    logg = np.log(dist + KL_EPS)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        terms = np.where(t > 0, t * (np.log(np.where(t > 0, t, 1.0)) - logg), 0.0)
+    return float(terms.sum() / b)
+
+
+def gate_kl_grad(soft: np.ndarray, target: np.ndarray) -> np.ndarray:
+    """d gate_kl_loss / d soft: with Z = sum g + eps and u = g / Z + eps per (b, h),
+    ``(-t_k / u_k + (sum_i t_i g_i / u_i) / Z) / (Z * B)``."""
+    b, h = soft.shape[:2]
+    g = soft.reshape(b, h, -1).astype(np.float64)
+    t = target.reshape(b, h, -1).astype(np.float64)
+    z = g.sum(-1, keepdims=True) + KL_EPS
+    u = g / z + KL_EPS
+    s2 = (t * g / u).sum(-1, keepdims=True)
+    return ((-t / u + s2 / z) / (z * b)).reshape(soft.shape)
 
 
 # ----------------------------------------------------------------------------- stats

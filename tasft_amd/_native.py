@@ -30,7 +30,10 @@ EXPORTED_SYMBOLS = (
     "tasft_bsfa_decode_fwd_noalloc",
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
+    "tasft_gate_bwd_workspace_bytes",
+    "tasft_gate_bwd",
     "tasft_gate_target_fwd",
+    "tasft_gate_kl_fwd",
     "tasft_mask_compact_workspace_bytes",
     "tasft_mask_compact",
     "tasft_mask_from_indices",
@@ -79,9 +82,15 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_gate_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_fwd": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64,
          _I64, _I64, _I64P, _I64P, _I, _P],
     ),
+    "tasft_gate_bwd_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "tasft_gate_bwd": (
+        _I,
+        [_P, _P, _P, _SZ, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
+    ),
+    "tasft_gate_kl_fwd": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "tasft_gate_target_fwd": (
         _I,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _F, _I, _I,

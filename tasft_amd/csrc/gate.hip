@@ -33,6 +33,8 @@ struct GatePoolParams {
   const float* b_in;  // [hidden]
   float* uq;          // [B, Hq, NB, hidden]
   float* uk;          // [B, Hkv, NB, hidden]
+  float* qmeans;      // [B, Hq, NB, D] block means of Q, or null
+  float* kmeans;      // [B, Hkv, NB, D] block means of K, or null
   unsigned long long* counter;
   int64_t sq[3], sk[3];
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
@@ -89,6 +91,11 @@ gate_pool_project_kernel(const GatePoolParams p) {
       pooled[bi][d] = sum * inv_bs;
     }
     __syncthreads();
+  }
+  float* mdst = is_q ? p.qmeans : p.kmeans;
+  if (mdst) {
+    mdst += (bh * p.NB + blk0) * (int64_t)p.D;
+    for (int i = tid; i < nblk * p.D; i += 256) mdst[i] = pooled[i / p.D][i % p.D];
   }
 
   // Project: u[blk][c] = sum_d pooled[blk][d] * W_in[c][off + d] (+ b_in[c] for queries).
@@ -202,6 +209,11 @@ gate_pool_proj64_kernel(const GatePoolParams p) {
     red[0][bi][d] = ((red[0][bi][d] + red[1][bi][d]) + (red[2][bi][d] + red[3][bi][d])) * inv_bs;
   }
   __syncthreads();
+  float* mdst = is_q ? p.qmeans : p.kmeans;
+  if (mdst) {
+    mdst += (bh * p.NB + blk0) * (int64_t)D;
+    for (int e = tid; e < nblk * D; e += 256) mdst[e] = red[0][e / D][e % D];
+  }
 
   // u[blk][c] = sum_d mean[blk][d] * W_in[c][off + d] (+ b_in[c] for query rows). Thread t
   // takes unit c0 + t % 128 of blocks 8 * (t / 128) .. +7; the mean reads are broadcasts.
@@ -405,6 +417,158 @@ gate_pairwise_kernel(const GatePairParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Backward of the pairwise MLP (gate training).
+//
+// With u_i = W_q qbar_i + b_in, v_j = W_k kbar_j, pre_ijc = u_ic + v_jc and
+// soft_ij = sigmoid(w . relu(pre_ij)) (0 above the block diagonal when causal), the
+// gradient G = dL/dsoft gives g_ij = G_ij soft_ij (1 - soft_ij) (0 where soft was zeroed),
+// and
+//   dL/dw_c   = sum_ij g_ij relu(pre_ijc)
+//   dL/du_ic  = w_c sum_j g_ij [pre_ijc > 0]
+//   dL/dv_jc  = w_c sum_i g_ij [pre_ijc > 0].
+// A workgroup takes a 32 x 32 tile of pairs of one (batch, head) and writes the tile's
+// partial sums without the w_c factor: S_u[i][c] = sum over the tile's j, S_v[j][c] over
+// its i, S_w[c] over the tile. Partial buffers (fp32, every element written, zeros for
+// tiles wholly above the diagonal):
+//   du_part [tiles][B][Hq][NB][hidden]  (indexed by the key tile)
+//   dv_part [tiles][B][Hq][NB][hidden]  (indexed by the query tile)
+//   dw_part [B * Hq * tiles * tiles][hidden]
+// The caller sums them and applies w (deterministic: no atomics).
+// ---------------------------------------------------------------------------------------
+constexpr int kBwdTile = 32;
+constexpr int kBwdHC = 64;  // hidden units staged per round
+
+struct GateBwdParams {
+  const float* uq;
+  const float* uk;
+  const float* soft;       // [B, Hq, NB, NB]
+  const float* grad_soft;  // [B, Hq, NB, NB]
+  float* du_part;
+  float* dv_part;
+  float* dw_part;
+  int B, Hq, Hkv, G, NB, hidden, causal, tiles;
+};
+
+__global__ void __launch_bounds__(256)
+gate_pairwise_bwd_kernel(const GateBwdParams p) {
+  __shared__ float g_t[kBwdTile][kBwdTile + 1];
+  __shared__ float uq_s[kBwdTile][kBwdHC + 1];
+  __shared__ float uk_s[kBwdTile][kBwdHC + 1];
+
+  const int tid = threadIdx.x;
+  const int per_head = p.tiles * p.tiles;
+  const int64_t bh = blockIdx.x / per_head;
+  const int t2 = (int)(blockIdx.x % per_head);
+  const int it = t2 / p.tiles, jt = t2 % p.tiles;
+  const int i0 = it * kBwdTile, j0 = jt * kBwdTile;
+  const int b = (int)(bh / p.Hq);
+  const int h = (int)(bh % p.Hq);
+  const int kvh = h / p.G;
+  const int64_t plane = (int64_t)p.B * p.Hq * p.NB * p.hidden;
+  float* du_out = p.du_part + jt * plane + (bh * p.NB) * (int64_t)p.hidden;
+  float* dv_out = p.dv_part + it * plane + (bh * p.NB) * (int64_t)p.hidden;
+  float* dw_out = p.dw_part + (int64_t)blockIdx.x * p.hidden;
+  const int rows_i = min(kBwdTile, p.NB - i0), rows_j = min(kBwdTile, p.NB - j0);
+
+  if (p.causal && j0 > i0 + kBwdTile - 1) {
+    // Wholly above the diagonal: every g is zero.
+    for (int e = tid; e < rows_i * p.hidden; e += 256) du_out[(int64_t)i0 * p.hidden + e] = 0.f;
+    for (int e = tid; e < rows_j * p.hidden; e += 256) dv_out[(int64_t)j0 * p.hidden + e] = 0.f;
+    for (int e = tid; e < p.hidden; e += 256) dw_out[e] = 0.f;
+    return;
+  }
+  const int64_t sbase = bh * (int64_t)p.NB * p.NB;
+  for (int e = tid; e < kBwdTile * kBwdTile; e += 256) {
+    const int ii = e / kBwdTile, jj = e % kBwdTile;
+    const int i = i0 + ii, j = j0 + jj;
+    float g = 0.f;
+    if (i < p.NB && j < p.NB && !(p.causal && j > i)) {
+      const int64_t o = sbase + (int64_t)i * p.NB + j;
+      const float sv = p.soft[o];
+      g = p.grad_soft[o] * sv * (1.f - sv);
+    }
+    g_t[ii][jj] = g;
+  }
+
+  const float* uq = p.uq + (bh * p.NB) * (int64_t)p.hidden;
+  const float* uk = p.uk + (((int64_t)b * p.Hkv + kvh) * p.NB) * (int64_t)p.hidden;
+  const int r = tid % kBwdTile;       // row (pass A) / column (pass B) of this thread
+  const int ug = tid / kBwdTile;      // unit group: units 8*ug .. 8*ug+7 of a staged round
+  for (int c0 = 0; c0 < p.hidden; c0 += kBwdHC) {
+    const int hc = min(kBwdHC, p.hidden - c0);
+    __syncthreads();  // g_t written (first round); previous round's reads done
+    for (int e = tid; e < kBwdTile * kBwdHC; e += 256) {
+      const int rr = e / kBwdHC, cc = e % kBwdHC;
+      const bool okc = cc < hc;
+      uq_s[rr][cc] = (okc && rr < rows_i) ? uq[(int64_t)(i0 + rr) * p.hidden + c0 + cc] : 0.f;
+      uk_s[rr][cc] = (okc && rr < rows_j) ? uk[(int64_t)(j0 + rr) * p.hidden + c0 + cc] : 0.f;
+    }
+    __syncthreads();
+    // Pass A: row i = i0 + r, units c0 + 8ug ..: S_u over the tile's keys and S_w.
+    float a[8], su[8], sw[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = uq_s[r][8 * ug + e];
+      su[e] = 0.f;
+      sw[e] = 0.f;
+    }
+    for (int jj = 0; jj < kBwdTile; ++jj) {
+      const float g = g_t[r][jj];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pre = a[e] + uk_s[jj][8 * ug + e];
+        su[e] += pre > 0.f ? g : 0.f;
+        sw[e] = fmaf(g, fmaxf(pre, 0.f), sw[e]);
+      }
+    }
+    if (r < rows_i) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + 8 * ug + e;
+        if (c < p.hidden) du_out[(int64_t)(i0 + r) * p.hidden + c] = su[e];
+      }
+    }
+    // S_w: sum over the 32 rows, held by the 32 consecutive lanes of this unit group.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = sw[e];
+#pragma unroll
+      for (int off = 1; off < kBwdTile; off <<= 1) x += __shfl_xor(x, off, kWave);
+      sw[e] = x;
+    }
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + 8 * ug + e;
+        if (c < p.hidden) dw_out[c] = sw[e];
+      }
+    }
+    // Pass B: column j = j0 + r: S_v over the tile's queries.
+    float bv[8], sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bv[e] = uk_s[r][8 * ug + e];
+      sv[e] = 0.f;
+    }
+    for (int ii = 0; ii < kBwdTile; ++ii) {
+      const float g = g_t[ii][r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pre = uq_s[ii][8 * ug + e] + bv[e];
+        sv[e] += pre > 0.f ? g : 0.f;
+      }
+    }
+    if (r < rows_j) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + 8 * ug + e;
+        if (c < p.hidden) dv_out[(int64_t)(j0 + r) * p.hidden + c] = sv[e];
+      }
+    }
+  }
+}
+
 }  // namespace tasft
 
 using namespace tasft;
@@ -424,6 +588,7 @@ extern "C" size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads,
 extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float* b_in,
                               const float* w_out, const float* thresholds, float* soft_scores,
                               float* logits, uint8_t* hard_mask, unsigned long long* active_count,
+                              float* q_means, float* k_means,
                               void* workspace, size_t workspace_bytes, int64_t batch,
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
                               int64_t head_dim, int64_t block_size, int64_t hidden,
@@ -466,6 +631,8 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   pp.b_in = b_in;
   pp.uq = (float*)workspace;
   pp.uk = pp.uq + batch * num_q_heads * nb * hidden;
+  pp.qmeans = q_means;
+  pp.kmeans = k_means;
   pp.counter = active_count;
   for (int j = 0; j < 3; ++j) {
     pp.sq[j] = q_strides[j];
@@ -521,5 +688,65 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   hipLaunchKernelGGL(gate_pairwise_kernel, dim3((unsigned)grid2), dim3(256), 0, s, qp);
   if ((err = hipGetLastError()) != hipSuccess)
     return set_error(kErrLaunch, "gate: pairwise launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}
+
+extern "C" size_t tasft_gate_bwd_workspace_bytes(int64_t batch, int64_t num_q_heads,
+                                                 int64_t seq_len, int64_t block_size,
+                                                 int64_t hidden) {
+  if (batch <= 0 || num_q_heads <= 0 || seq_len <= 0 || block_size <= 0 || hidden <= 0) return 0;
+  const int64_t nb = (seq_len + block_size - 1) / block_size;
+  const int64_t tiles = (nb + kBwdTile - 1) / kBwdTile;
+  const int64_t plane = batch * num_q_heads * nb * hidden;
+  return (size_t)(2 * tiles * plane + batch * num_q_heads * tiles * tiles * hidden) * sizeof(float);
+}
+
+extern "C" int tasft_gate_bwd(const float* soft_scores, const float* grad_soft,
+                              const void* fwd_workspace, size_t fwd_workspace_bytes,
+                              float* partials, size_t partials_bytes, int64_t batch,
+                              int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
+                              int64_t block_size, int64_t hidden, int flags, void* stream) {
+  if (!soft_scores || !grad_soft || !fwd_workspace || !partials)
+    return set_error(kErrInvalidArgument, "gate_bwd: null pointer argument");
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0 || block_size <= 0 ||
+      hidden <= 0)
+    return set_error(kErrInvalidArgument, "gate_bwd: sizes must be positive");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument, "gate_bwd: num_q_heads must be a multiple of num_kv_heads");
+  const size_t fwd_need = tasft_gate_workspace_bytes(batch, num_q_heads, num_kv_heads, seq_len, 8,
+                                                     block_size, hidden);
+  if (fwd_workspace_bytes < fwd_need)
+    return set_error(kErrWorkspace, "gate_bwd: forward workspace too small: need %zu bytes, got %zu",
+                     fwd_need, fwd_workspace_bytes);
+  const size_t need = tasft_gate_bwd_workspace_bytes(batch, num_q_heads, seq_len, block_size, hidden);
+  if (partials_bytes < need)
+    return set_error(kErrWorkspace, "gate_bwd: partials buffer too small: need %zu bytes, got %zu",
+                     need, partials_bytes);
+  const int64_t nb = (seq_len + block_size - 1) / block_size;
+  const int64_t tiles = (nb + kBwdTile - 1) / kBwdTile;
+  if (batch * num_q_heads * tiles * tiles > 0x7fffffffLL)
+    return set_error(kErrUnsupported, "gate_bwd: problem too large for one launch");
+  GateBwdParams bp;
+  bp.uq = (const float*)fwd_workspace;
+  bp.uk = bp.uq + batch * num_q_heads * nb * hidden;
+  bp.soft = soft_scores;
+  bp.grad_soft = grad_soft;
+  const int64_t plane = batch * num_q_heads * nb * hidden;
+  bp.du_part = partials;
+  bp.dv_part = partials + tiles * plane;
+  bp.dw_part = partials + 2 * tiles * plane;
+  bp.B = (int)batch;
+  bp.Hq = (int)num_q_heads;
+  bp.Hkv = (int)num_kv_heads;
+  bp.G = (int)(num_q_heads / num_kv_heads);
+  bp.NB = (int)nb;
+  bp.hidden = (int)hidden;
+  bp.causal = (flags & 1) ? 1 : 0;
+  bp.tiles = (int)tiles;
+  hipLaunchKernelGGL(gate_pairwise_bwd_kernel, dim3((unsigned)(batch * num_q_heads * tiles * tiles)),
+                     dim3(256), 0, (hipStream_t)stream, bp);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "gate_bwd: launch failed: %s", hipGetErrorString(err));
   return kOk;
 }

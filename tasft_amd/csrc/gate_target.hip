@@ -412,6 +412,59 @@ static hipError_t dispatch_blockmax(const GateTargetParams& p, int64_t block_siz
   return launch_blockmax<128, 64, MASKED>(p, s);
 }
 
+// KL gate loss (reference TASFTObjective.compute_gate_loss, objectives.py:187-221) of one
+// (batch, head) per workgroup, on its flattened NB_q * NB_k scores g and target t:
+//   Z = sum_i g_i + eps,  u_i = g_i / Z + eps,
+//   L = sum_i t_i (log t_i - log u_i)            (entries with t_i = 0 contribute 0),
+//   dL/dg_k = (-t_k / u_k + (sum_i t_i g_i / u_i) / Z) / Z.
+// loss_part[bh] receives L; grad (optional) receives inv_batch * dL/dg (the reference
+// reduces with "batchmean": the sum over (b, h) divided by B).
+constexpr float kKlEps = 1e-8f;
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ void __launch_bounds__(256)
+gate_kl_kernel(const float* soft, const float* target, int64_t n, float inv_batch,
+               float* loss_part, float* grad) {
+  __shared__ float red[4];
+  const int64_t bh = blockIdx.x;
+  const float* g = soft + bh * n;
+  const float* t = target + bh * n;
+  const int tid = threadIdx.x;
+  float z = 0.f;
+  for (int64_t i = tid; i < n; i += 256) z += g[i];
+  z = block_sum256(z, red) + kKlEps;
+  const float inv_z = 1.f / z;
+  float l = 0.f, s2 = 0.f;
+  for (int64_t i = tid; i < n; i += 256) {
+    const float ti = t[i];
+    if (ti > 0.f) {
+      const float gi = g[i];
+      const float u = gi * inv_z + kKlEps;
+      l += ti * (logf(ti) - logf(u));
+      s2 += ti * gi / u;
+    }
+  }
+  l = block_sum256(l, red);
+  s2 = block_sum256(s2, red);
+  if (tid == 0) loss_part[bh] = l;
+  if (grad) {
+    float* gr = grad + bh * n;
+    const float c = s2 * inv_z;
+    for (int64_t i = tid; i < n; i += 256) {
+      const float ti = t[i];
+      const float u = g[i] * inv_z + kKlEps;
+      gr[i] = inv_batch * inv_z * (c - ti / u);
+    }
+  }
+}
+
 }  // namespace tasft
 
 using namespace tasft;
@@ -494,5 +547,23 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
     if ((err = hipGetLastError()) != hipSuccess)
       return set_error(kErrLaunch, "gate_target: normalize launch failed: %s", hipGetErrorString(err));
   }
+  return kOk;
+}
+
+extern "C" int tasft_gate_kl_fwd(const float* gate_scores, const float* target, int64_t batch,
+                                 int64_t num_heads, int64_t num_blocks_q, int64_t num_blocks_k,
+                                 float* loss_partials, float* grad_scores, void* stream) {
+  if (!gate_scores || !target || !loss_partials)
+    return set_error(kErrInvalidArgument, "gate_kl: null pointer argument");
+  if (batch <= 0 || num_heads <= 0 || num_blocks_q <= 0 || num_blocks_k <= 0)
+    return set_error(kErrInvalidArgument, "gate_kl: sizes must be positive");
+  if (batch * num_heads > 0x7fffffffLL)
+    return set_error(kErrUnsupported, "gate_kl: problem too large for one launch");
+  hipLaunchKernelGGL(gate_kl_kernel, dim3((unsigned)(batch * num_heads)), dim3(256), 0,
+                     (hipStream_t)stream, gate_scores, target, num_blocks_q * num_blocks_k,
+                     1.f / (float)batch, loss_partials, grad_scores);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "gate_kl: launch failed: %s", hipGetErrorString(err));
   return kOk;
 }

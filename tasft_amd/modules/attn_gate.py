@@ -202,14 +202,18 @@ class AttnGate(nn.Module):
             raise ValidationError(f"Q and K must be on the same device, got {q.device} vs {k.device}",
                                   context={"q_device": str(q.device), "k_device": str(k.device)})
         if self._kernel_applies(q, k):
-            return self._forward_hip(q, k, tau, return_logits, force_diagonal)
+            if not self._needs_grad(q, k):
+                return self._forward_hip(q, k, tau, return_logits, force_diagonal)
+            if not return_logits:
+                return self._forward_hip_train(q, k, tau, force_diagonal)
         return self._forward_torch(q, k, tau, return_logits, force_diagonal)
 
     def _kernel_applies(self, q: torch.Tensor, k: torch.Tensor) -> bool:
-        """The HIP kernel serves bf16 GPU tensors without autograd (head_dim multiple of 8,
-        at most 256); every other call evaluates the formula with torch operations."""
+        """The HIP kernels serve bf16 GPU tensors (head_dim a multiple of 8, at most 256):
+        inference, and training through the HIP backward; every other call (CPU, fp16 or
+        fp32 inputs, or gradients of the logits) evaluates the formula with torch."""
         return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
-                and not self._needs_grad(q, k) and q.shape[-1] % 8 == 0 and q.shape[-1] <= 256)
+                and q.shape[-1] % 8 == 0 and q.shape[-1] <= 256)
 
     def _thresholds(self, tau: float | torch.Tensor, device: torch.device) -> torch.Tensor:
         if isinstance(tau, torch.Tensor):
@@ -225,41 +229,24 @@ class AttnGate(nn.Module):
 
     def _forward_hip(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
                      return_logits: bool, force_diagonal: bool) -> GateOutput:
-        B, H, S, D = q.shape
-        Hkv = k.shape[1]
-        for name, t in (("q", q), ("k", k)):
-            if t.dtype != torch.bfloat16:
-                raise KernelError(f"AttnGate kernel reads bfloat16; {name} is {t.dtype}",
-                                  context={"tensor": name, "dtype": str(t.dtype)})
-        if D % 8 != 0 or D > 256:
-            raise KernelError(f"AttnGate kernel supports head_dim multiple of 8 up to 256, got {D}",
-                              context={"head_dim": D})
-        lib = _native.load_library()
-        dev = q.device
-        q = q if (q.stride(-1) == 1 and all(s % 8 == 0 for s in q.stride()[:-1])) else q.contiguous()
-        k = k if (k.stride(-1) == 1 and all(s % 8 == 0 for s in k.stride()[:-1])) else k.contiguous()
-        w_in = self.gate_proj_in.weight.detach().to(device=dev, dtype=torch.float32).contiguous()
-        b_in = self.gate_proj_in.bias.detach().to(device=dev, dtype=torch.float32).contiguous()
-        w_out = self.gate_proj_out.weight.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
-        taus = self._thresholds(tau, dev)
-        nb = math.ceil(S / self.block_size)
-        hidden = self.gate_hidden_dim
-        soft = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev)
-        mask = torch.empty((B, H, nb, nb), dtype=torch.uint8, device=dev)
-        logits = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev) if return_logits else None
-        active = torch.empty((1,), dtype=torch.int64, device=dev)
-        ws_bytes = lib.tasft_gate_workspace_bytes(B, H, Hkv, S, D, self.block_size, hidden)
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        status = lib.tasft_gate_fwd(
-            q.data_ptr(), k.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(),
-            taus.data_ptr(), soft.data_ptr(), _native.ptr(logits), mask.data_ptr(),
-            active.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, Hkv, S, D,
-            self.block_size, hidden, _native.strides(q), _native.strides(k),
-            (1 if self.is_causal else 0) | (2 if force_diagonal else 0), _native.stream_handle(dev),
-        )
-        _native.check(status, "tasft_gate_fwd", {"shape": [B, H, S, D]})
+        r = _launch_gate(self, q, k, self._thresholds(tau, q.device), return_logits,
+                         force_diagonal, keep=False)
+        return GateOutput(soft_scores=r["soft"], hard_mask=r["mask"].view(torch.bool),
+                          num_blocks_q=r["nb"], num_blocks_k=r["nb"], logits=r["logits"],
+                          active_count=r["active"])
+
+    def _forward_hip_train(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
+                           force_diagonal: bool) -> GateOutput:
+        """HIP forward plus HIP backward (``tasft_gate_bwd``) through autograd: the soft
+        scores carry gradients to the gate parameters (and to Q/K if they require them)
+        without materialising the ``[B, H, NB, NB, hidden]`` activations."""
+        taus = self._thresholds(tau, q.device)
+        soft, mask, active = _HipGateFunction.apply(
+            q, k, self.gate_proj_in.weight, self.gate_proj_in.bias, self.gate_proj_out.weight,
+            self, taus, force_diagonal)
+        nb = soft.shape[-1]
         return GateOutput(soft_scores=soft, hard_mask=mask.view(torch.bool), num_blocks_q=nb,
-                          num_blocks_k=nb, logits=logits, active_count=active)
+                          num_blocks_k=nb, logits=None, active_count=active)
 
     def _forward_torch(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
                        return_logits: bool, force_diagonal: bool) -> GateOutput:
@@ -313,6 +300,104 @@ class AttnGate(nn.Module):
             f"default_threshold={self.default_threshold}, "
             f"is_causal={self.is_causal}, params={self.num_parameters}"
         )
+
+
+def _kernel_layout(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1])) else t.contiguous()
+
+
+def _launch_gate(gate: AttnGate, q: torch.Tensor, k: torch.Tensor, taus: torch.Tensor,
+                 return_logits: bool, force_diagonal: bool, keep: bool) -> dict:
+    """Run ``tasft_gate_fwd``; with ``keep`` also return the block means and the workspace
+    (the projected units) that the backward needs."""
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    lib = _native.load_library()
+    dev = q.device
+    q = _kernel_layout(q.detach())
+    k = _kernel_layout(k.detach())
+    w_in = gate.gate_proj_in.weight.detach().to(device=dev, dtype=torch.float32).contiguous()
+    b_in = gate.gate_proj_in.bias.detach().to(device=dev, dtype=torch.float32).contiguous()
+    w_out = gate.gate_proj_out.weight.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    nb = math.ceil(S / gate.block_size)
+    hidden = gate.gate_hidden_dim
+    soft = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev)
+    mask = torch.empty((B, H, nb, nb), dtype=torch.uint8, device=dev)
+    logits = torch.empty((B, H, nb, nb), dtype=torch.float32, device=dev) if return_logits else None
+    active = torch.empty((1,), dtype=torch.int64, device=dev)
+    qm = torch.empty((B, H, nb, D), dtype=torch.float32, device=dev) if keep else None
+    km = torch.empty((B, Hkv, nb, D), dtype=torch.float32, device=dev) if keep else None
+    ws_bytes = lib.tasft_gate_workspace_bytes(B, H, Hkv, S, D, gate.block_size, hidden)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    status = lib.tasft_gate_fwd(
+        q.data_ptr(), k.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(),
+        taus.data_ptr(), soft.data_ptr(), _native.ptr(logits), mask.data_ptr(), active.data_ptr(),
+        _native.ptr(qm), _native.ptr(km), workspace.data_ptr(), ws_bytes, B, H, Hkv, S, D,
+        gate.block_size, hidden, _native.strides(q), _native.strides(k),
+        (1 if gate.is_causal else 0) | (2 if force_diagonal else 0), _native.stream_handle(dev),
+    )
+    _native.check(status, "tasft_gate_fwd", {"shape": [B, H, S, D]})
+    return {"soft": soft, "mask": mask, "logits": logits, "active": active, "nb": nb,
+            "q_means": qm, "k_means": km, "workspace": workspace, "w_in": w_in, "w_out": w_out}
+
+
+class _HipGateFunction(torch.autograd.Function):
+    """AttnGate forward/backward on the HIP kernels (gate training).
+
+    Backward, with g = dL/dsoft * soft * (1 - soft) (0 where the causal zero applied) and
+    pre_ijc = u_ic + v_jc (u = W_q qbar + b_in, v = W_k kbar): ``tasft_gate_bwd`` reduces
+    the pairwise terms; the rest are plain GEMMs on [B, H, NB, .] tensors:
+      dL/dw_out = sum g relu(pre);  dL/du = w_out * sum_j g [pre > 0];
+      dL/dv = w_out * sum_i g [pre > 0] (summed over the query heads of each KV head);
+      dL/db_in = sum du;  dL/dW_in = [du^T qbar, dv^T kbar];
+      dL/dqbar = du W_q, dL/dkbar = dv W_k, spread over each block's tokens / block size.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, w_in, b_in, w_out, gate, taus, force_diagonal):
+        r = _launch_gate(gate, q, k, taus, False, force_diagonal, keep=True)
+        ctx.gate_cfg = (gate.block_size, gate.gate_hidden_dim, gate.is_causal)
+        ctx.shapes = (tuple(q.shape), tuple(k.shape))
+        ctx.dtypes = (q.dtype, k.dtype, w_in.dtype, b_in.dtype, w_out.dtype)
+        ctx.save_for_backward(r["soft"], r["workspace"], r["q_means"], r["k_means"], r["w_in"],
+                              r["w_out"])
+        ctx.mark_non_differentiable(r["mask"], r["active"])
+        return r["soft"], r["mask"], r["active"]
+
+    @staticmethod
+    def backward(ctx, grad_soft, _grad_mask, _grad_active):
+        soft, workspace, qm, km, w_in, w_out = ctx.saved_tensors
+        bs, hidden, causal = ctx.gate_cfg
+        (B, H, S, D), (_, Hkv, _, _) = ctx.shapes
+        nb = soft.shape[-1]
+        lib = _native.load_library()
+        dev = soft.device
+        gs = grad_soft.to(torch.float32).contiguous()
+        pbytes = lib.tasft_gate_bwd_workspace_bytes(B, H, S, bs, hidden)
+        partials = torch.empty(pbytes // 4, dtype=torch.float32, device=dev)
+        status = lib.tasft_gate_bwd(soft.data_ptr(), gs.data_ptr(), workspace.data_ptr(),
+                                    workspace.numel(), partials.data_ptr(), pbytes, B, H, Hkv, S,
+                                    bs, hidden, 1 if causal else 0, _native.stream_handle(dev))
+        _native.check(status, "tasft_gate_bwd", {"shape": [B, H, S, D]})
+        tiles = (nb + 31) // 32
+        plane = B * H * nb * hidden
+        du = partials[: tiles * plane].view(tiles, B, H, nb, hidden).sum(0) * w_out
+        dv = (partials[tiles * plane: 2 * tiles * plane].view(tiles, B, Hkv, H // Hkv, nb, hidden)
+              .sum((0, 3)) * w_out)
+        dw_out = partials[2 * tiles * plane:].view(-1, hidden).sum(0)
+        db_in = du.sum((0, 1, 2))
+        dw_q = du.reshape(-1, hidden).t() @ qm.reshape(-1, D)
+        dw_k = dv.reshape(-1, hidden).t() @ km.reshape(-1, D)
+        dw_in = torch.cat([dw_q, dw_k], dim=1)
+        gq = gk = None
+        if ctx.needs_input_grad[0]:
+            dqbar = (du @ w_in[:, :D]) / bs
+            gq = dqbar.repeat_interleave(bs, dim=2)[:, :, :S].to(ctx.dtypes[0])
+        if ctx.needs_input_grad[1]:
+            dkbar = (dv @ w_in[:, D:]) / bs
+            gk = dkbar.repeat_interleave(bs, dim=2)[:, :, :S].to(ctx.dtypes[1])
+        return (gq, gk, dw_in.to(ctx.dtypes[2]), db_in.to(ctx.dtypes[3]),
+                dw_out.view(1, -1).to(ctx.dtypes[4]), None, None, None)
 
 
 __all__ = ["AttnGate", "GateOutput"]

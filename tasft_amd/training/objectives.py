@@ -27,8 +27,25 @@ from tasft_amd.exceptions import KernelError, NaNDetectedError
 _NORMALIZE = {"flat": 0, "row": 1, "none": 2}
 
 
+_EPS = 1e-8  # reference objectives.py:39
+
+
+def _check_finite(tensor: torch.Tensor, name: str) -> None:
+    """NaN/Inf guard with the reference's message and context (objectives.py:67-87)."""
+    if not bool(torch.isfinite(tensor).all()):
+        has_nan = bool(torch.isnan(tensor).any())
+        has_inf = bool(torch.isinf(tensor).any())
+        raise NaNDetectedError(
+            f"Non-finite values detected in {name}: NaN={has_nan}, Inf={has_inf}",
+            context={"tensor_name": name, "has_nan": has_nan, "has_inf": has_inf,
+                     "shape": list(tensor.shape), "dtype": str(tensor.dtype)},
+        )
+
+
 class TASFTObjective:
-    """Holder of the gate-target operator (the loss algebra of the reference is out of scope)."""
+    """The gate terms of the reference objective (``tasft/training/objectives.py:128-235``):
+    the gate target, the KL gate loss and the sparsity loss. The task loss, the Kahan sums
+    and the trainer around them are outside the hot path."""
 
     @staticmethod
     def compute_gate_target(attn_scores: torch.Tensor, block_size: int) -> torch.Tensor:
@@ -57,6 +74,24 @@ class TASFTObjective:
         nb_q, nb_k = pooled.shape[2], pooled.shape[3]
         target = F.softmax(pooled.reshape(b, h, nb_q * nb_k), dim=-1)
         return target.reshape(b, h, nb_q, nb_k)
+
+    @staticmethod
+    def compute_gate_loss(gate_soft_scores: torch.Tensor, gate_target: torch.Tensor) -> torch.Tensor:
+        """KL(target || gate), "batchmean" (reference ``objectives.py:187-221``), in torch."""
+        _check_finite(gate_soft_scores, "gate_soft_scores")
+        _check_finite(gate_target, "gate_target")
+        b, h, nb_q, nb_k = gate_soft_scores.shape
+        gate_flat = gate_soft_scores.reshape(b, h, nb_q * nb_k)
+        gate_dist = gate_flat / (gate_flat.sum(dim=-1, keepdim=True) + _EPS)
+        target_flat = gate_target.reshape(b, h, nb_q * nb_k)
+        log_gate = torch.log(gate_dist + _EPS)
+        return F.kl_div(log_gate, target_flat, reduction="batchmean", log_target=False)
+
+    @staticmethod
+    def compute_sparsity_loss(gate_soft_scores: torch.Tensor, tau_target: float) -> torch.Tensor:
+        """``(mean(gate_soft_scores) - tau_target) ** 2`` (reference ``objectives.py:223-240``)."""
+        _check_finite(gate_soft_scores, "gate_soft_scores")
+        return (gate_soft_scores.mean() - tau_target) ** 2
 
 
 def gate_target_from_qk(
@@ -154,4 +189,67 @@ def _padded_attention_mask(mask: torch.Tensor, B: int, H: int, S: int, padded: i
     return buf, _native.strides_array(strides)
 
 
-__all__ = ["TASFTObjective", "gate_target_from_qk"]
+class _GateKL(torch.autograd.Function):
+    """KL gate loss on the GPU (``tasft_gate_kl_fwd``): the loss and d(loss)/d(gate scores)
+    come from one kernel; backward scales the saved gradient."""
+
+    @staticmethod
+    def forward(ctx, gate_soft: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        b, h, nbq, nbk = gate_soft.shape
+        g = gate_soft.detach().to(torch.float32).contiguous()
+        t = target.detach().to(torch.float32).contiguous()
+        partial = torch.empty(b * h, dtype=torch.float32, device=g.device)
+        grad = torch.empty_like(g) if ctx.needs_input_grad[0] else None
+        lib = _native.load_library()
+        status = lib.tasft_gate_kl_fwd(g.data_ptr(), t.data_ptr(), b, h, nbq, nbk, partial.data_ptr(),
+                                       _native.ptr(grad), _native.stream_handle(g.device))
+        _native.check(status, "tasft_gate_kl_fwd", {"shape": [b, h, nbq, nbk]})
+        ctx.save_for_backward(grad)
+        ctx.in_dtype = gate_soft.dtype
+        return partial.sum() / b
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        (grad,) = ctx.saved_tensors
+        if grad is None:
+            return None, None
+        return (grad * grad_out).to(ctx.in_dtype), None
+
+
+def gate_loss_from_qk(
+    gate_soft_scores: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    block_size: int = 64,
+    *,
+    causal: bool = True,
+    scale: float | None = None,
+    attention_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The per-layer gate term ``compute_gate_loss(gate, compute_gate_target(scores))`` of
+    ``TASFTObjective.compute`` (reference ``objectives.py:316-346``) from Q and K, without the
+    ``[B, H, S, S]`` score tensor the reference's score producer stores
+    (``tasft/modules/tasft_attention.py:426-458``).
+
+    The target comes from ``gate_target_from_qk`` (bf16 MFMA block maxima, flat softmax) and
+    is a constant of the loss, as the reference's detached scores are; the KL and its
+    gradient with respect to ``gate_soft_scores`` come from one HIP kernel, so
+    ``loss.backward()`` reaches the gate (and, through ``AttnGate``'s HIP backward, its
+    parameters). NaN or Inf in ``gate_soft_scores`` raises ``NaNDetectedError``.
+    """
+    if gate_soft_scores.ndim != 4:
+        raise KernelError("gate_soft_scores must be [B, H, NB, NB]",
+                          context={"shape": list(gate_soft_scores.shape)})
+    if not gate_soft_scores.is_cuda:
+        raise KernelError("Tensors must be on CUDA device", context={"device": str(gate_soft_scores.device)})
+    target = gate_target_from_qk(q, k, block_size, causal=causal, scale=scale,
+                                 attention_mask=attention_mask)
+    if tuple(target.shape) != tuple(gate_soft_scores.shape):
+        raise KernelError(
+            f"gate scores {tuple(gate_soft_scores.shape)} do not match the target grid {tuple(target.shape)}",
+            context={"gate": list(gate_soft_scores.shape), "target": list(target.shape)})
+    _check_finite(gate_soft_scores, "gate_soft_scores")
+    return _GateKL.apply(gate_soft_scores, target)
+
+
+__all__ = ["TASFTObjective", "gate_loss_from_qk", "gate_target_from_qk"]

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace_sizes():
     lib = _native.load_library()
-    assert lib.tasft_abi_version() == 5
+    assert lib.tasft_abi_version() == 6
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 8192, 64) == 256
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 0, 64) == 0
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4

@@ -369,6 +369,41 @@ def test_block_max_with_attention_mask_equals_reference_composition(form):
     np.testing.assert_allclose(raw, pooled.numpy(), rtol=1e-5, atol=1e-6)
 
 
+def _kl_case(seed):
+    rng = np.random.default_rng(seed)
+    soft = 1.0 / (1.0 + np.exp(-rng.standard_normal((2, 3, 5, 5))))
+    soft = soft * np.tril(np.ones((5, 5)))  # causal zeros, as the gate produces
+    target = orc.gate_target_from_scores(rng.standard_normal((2, 3, 20, 20)) * 3, 4)
+    target[0, 0, 1, :] = 0.0  # exact zeros in the target
+    target[0, 0] /= target[0, 0].sum()
+    return soft, target
+
+
+def test_gate_kl_loss_matches_reference_kl_div_composition():
+    """objectives.py:210-221 composed with torch: normalise, log(. + eps), F.kl_div batchmean."""
+    soft, target = _kl_case(21)
+    st = torch.from_numpy(soft)
+    tt = torch.from_numpy(target)
+    b, h = st.shape[:2]
+    flat = st.reshape(b, h, -1)
+    dist = flat / (flat.sum(-1, keepdim=True) + 1e-8)
+    ref = torch.nn.functional.kl_div(torch.log(dist + 1e-8), tt.reshape(b, h, -1),
+                                     reduction="batchmean", log_target=False)
+    assert orc.gate_kl_loss(soft, target) == pytest.approx(float(ref), rel=1e-12, abs=1e-14)
+
+
+def test_gate_kl_grad_matches_autograd():
+    soft, target = _kl_case(22)
+    st = torch.from_numpy(soft).requires_grad_(True)
+    b, h = st.shape[:2]
+    flat = st.reshape(b, h, -1)
+    dist = flat / (flat.sum(-1, keepdim=True) + 1e-8)
+    loss = torch.nn.functional.kl_div(torch.log(dist + 1e-8), torch.from_numpy(target).reshape(b, h, -1),
+                                      reduction="batchmean", log_target=False)
+    loss.backward()
+    np.testing.assert_allclose(orc.gate_kl_grad(soft, target), st.grad.numpy(), rtol=1e-9, atol=1e-12)
+
+
 def test_gate_target_clamp_temperature_variant():
     pooled = np.array([[[[100.0, -np.inf], [3.0, -70.0]]]])
     got = orc.normalize_block_max(pooled, "flat", temperature=2.0, clamp=50.0)
