@@ -220,6 +220,27 @@ int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float*
                    const int64_t* k_strides, int flags, void* stream);
 
 /*
+ * The pairwise stage of the gate on precomputed projected units, for query-block rows that
+ * need not start at block 0: a cached decode step's selection (one row) without pooling the
+ * KV cache again. With the units of tasft_gate_fwd's workspace (u for the rows, v for the
+ * key blocks) it gives exactly those rows of tasft_gate_fwd's output. No reference
+ * counterpart: the reference gate rejects S_q != S_k (tasft/modules/attn_gate.py:216-221).
+ *
+ * uq [B, Hq, rows, hidden] fp32 contiguous: u = W_q qbar + b_in of query blocks row0 ..
+ * row0 + rows - 1. uk: v = W_k kbar of key blocks 0 .. key_blocks - 1, block j of
+ * (b, KV head g) at uk[(b * Hkv + g) * uk_head_stride + j * hidden] (uk_head_stride >=
+ * key_blocks * hidden; it and hidden multiples of 4; 16-byte aligned). Outputs [B, Hq, rows,
+ * key_blocks] as in tasft_gate_fwd; the causal zero and TASFT_GATE_FORCE_DIAGONAL compare key
+ * block j with query block row0 + i. active_count is zeroed and counted by the call.
+ */
+int tasft_gate_rows_fwd(const float* uq, const float* uk, const float* w_out,
+                        const float* thresholds, float* soft_scores, float* logits,
+                        uint8_t* hard_mask, unsigned long long* active_count, int64_t batch,
+                        int64_t num_q_heads, int64_t num_kv_heads, int64_t rows,
+                        int64_t key_blocks, int64_t row0, int64_t hidden, int64_t uk_head_stride,
+                        int flags, void* stream);
+
+/*
  * Backward of the gate's pairwise MLP, for gate training: the gradient the reference gets
  * from autograd through AttnGate.forward (tasft/modules/attn_gate.py:248-273), without the
  * [B, H, NB, NB, hidden] activations.

@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "tasft_bsfa_decode_fwd_noalloc",
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
+    "tasft_gate_rows_fwd",
     "tasft_gate_bwd_workspace_bytes",
     "tasft_gate_bwd",
     "tasft_gate_target_fwd",
@@ -84,6 +85,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64,
          _I64, _I64, _I64P, _I64P, _I, _P],
+    ),
+    "tasft_gate_rows_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
     ),
     "tasft_gate_bwd_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_bwd": (

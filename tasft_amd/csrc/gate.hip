@@ -252,11 +252,15 @@ struct GatePairParams {
   const float* uk;
   const float* w_out;  // [hidden]
   const float* tau;    // [Hq]
-  float* soft;         // [B, Hq, NB, NB]
-  float* logits;       // [B, Hq, NB, NB] or null
-  uint8_t* mask;       // [B, Hq, NB, NB]
+  float* soft;         // [B, Hq, NBq, NBk]
+  float* logits;       // [B, Hq, NBq, NBk] or null
+  uint8_t* mask;       // [B, Hq, NBq, NBk]
   unsigned long long* counter;
-  int B, Hq, Hkv, G, NB, hidden, causal, force_diag, tiles;
+  // uq holds NBq query-block rows whose global block index is row0 + i (a decode step:
+  // one row); uk holds NBk key blocks. The causal zero and the forced diagonal compare
+  // key block j with the global query block row0 + i.
+  int B, Hq, Hkv, G, NBq, NBk, row0, hidden, causal, force_diag, tiles_q, tiles_k;
+  int64_t uk_bh_stride;  // elements between the key units of consecutive (b, KV head)
 };
 
 // Pairwise MLP: a workgroup evaluates a kPairTile x kPairTile tile of (query block,
@@ -287,19 +291,19 @@ gate_pairwise_kernel(const GatePairParams p) {
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
   const int tr = lane / 8, tc = lane % 8;
-  const int per_head = p.tiles * p.tiles;
+  const int per_head = p.tiles_q * p.tiles_k;
   const int64_t bh = blockIdx.x / per_head;
   const int t2 = (int)(blockIdx.x % per_head);
-  const int i0 = (t2 / p.tiles) * kPairTile;
-  const int j0 = (t2 % p.tiles) * kPairTile;
+  const int i0 = (t2 / p.tiles_k) * kPairTile;
+  const int j0 = (t2 % p.tiles_k) * kPairTile;
   const int b = (int)(bh / p.Hq);
   const int h = (int)(bh % p.Hq);
   const int kvh = h / p.G;
-  const float* uq = p.uq + (bh * p.NB) * (int64_t)p.hidden;
-  const float* uk = p.uk + (((int64_t)b * p.Hkv + kvh) * p.NB) * (int64_t)p.hidden;
+  const float* uq = p.uq + (bh * p.NBq) * (int64_t)p.hidden;
+  const float* uk = p.uk + ((int64_t)b * p.Hkv + kvh) * p.uk_bh_stride;
   // With causal=1 and no logits requested, a tile wholly above the diagonal is never
   // evaluated (its soft scores are exactly zero).
-  const bool skip = p.causal && p.logits == nullptr && j0 > i0 + kPairTile - 1;
+  const bool skip = p.causal && p.logits == nullptr && j0 > p.row0 + i0 + kPairTile - 1;
 
   if (!skip) {
     float acc[4][4];
@@ -321,8 +325,8 @@ gate_pairwise_kernel(const GatePairParams p) {
         // Whole run in range: 16-byte loads (hc is a multiple of 4 here).
 #pragma unroll
         for (int u = 0; u < SU; u += 4) {
-          const f32x4_t a = i < p.NB ? *(const f32x4_t*)(qrow + su + u) : (f32x4_t){};
-          const f32x4_t c = j < p.NB ? *(const f32x4_t*)(krow + su + u) : (f32x4_t){};
+          const f32x4_t a = i < p.NBq ? *(const f32x4_t*)(qrow + su + u) : (f32x4_t){};
+          const f32x4_t c = j < p.NBk ? *(const f32x4_t*)(krow + su + u) : (f32x4_t){};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float w = p.w_out[c0 + su + u + e];
@@ -336,8 +340,8 @@ gate_pairwise_kernel(const GatePairParams p) {
 #pragma unroll
         for (int u = 0; u < SU; ++u) {
           const int cc = su + u;
-          const float a = (cc < hc && i < p.NB) ? qrow[cc] : 0.f;
-          const float c = (cc < hc && j < p.NB) ? krow[cc] : 0.f;
+          const float a = (cc < hc && i < p.NBq) ? qrow[cc] : 0.f;
+          const float c = (cc < hc && j < p.NBk) ? krow[cc] : 0.f;
           const float w = cc < hc ? p.w_out[c0 + cc] : 0.f;
           uq_t[cc * kPairLd + sr] = a;
           uk_t[cc * kPairLd + sr] = c;
@@ -382,14 +386,14 @@ gate_pairwise_kernel(const GatePairParams p) {
   }
 
   const float tau = p.tau[h];
-  const int64_t obase = bh * (int64_t)p.NB * p.NB;
+  const int64_t obase = bh * (int64_t)p.NBq * p.NBk;
   unsigned int active = 0;
 #pragma unroll
   for (int k = 0; k < (kPairTile * kPairTile) / 256; ++k) {
     const int idx = tid + 256 * k;
     const int ii = idx / kPairTile, jj = idx % kPairTile;
     const int i = i0 + ii, j = j0 + jj;
-    if (i >= p.NB || j >= p.NB) continue;
+    if (i >= p.NBq || j >= p.NBk) continue;
     float logit = 0.f;
     if (!skip) {
       const int o = ii * kPairLd + jj;
@@ -398,10 +402,10 @@ gate_pairwise_kernel(const GatePairParams p) {
       logit = 0.5f * ((ab[0][ii] + ab[1][jj]) + sabs);
     }
     float soft = 1.f / (1.f + expf(-logit));
-    if (p.causal && j > i) soft = 0.f;
-    const bool on = soft >= tau || (p.force_diag && i == j);
+    if (p.causal && j > p.row0 + i) soft = 0.f;
+    const bool on = soft >= tau || (p.force_diag && p.row0 + i == j);
     active += on ? 1u : 0u;
-    const int64_t o = obase + (int64_t)i * p.NB + j;
+    const int64_t o = obase + (int64_t)i * p.NBk + j;
     p.soft[o] = soft;
     p.mask[o] = on ? 1 : 0;
     if (p.logits) p.logits[o] = logit;
@@ -415,6 +419,10 @@ gate_pairwise_kernel(const GatePairParams p) {
     const unsigned int t = (wave_count[0] + wave_count[1]) + (wave_count[2] + wave_count[3]);
     if (t) atomicAdd(p.counter, (unsigned long long)t);
   }
+}
+
+__global__ void gate_counter_reset_kernel(unsigned long long* counter) {
+  if (threadIdx.x == 0) *counter = 0ull;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -679,11 +687,15 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   qp.Hq = pp.Hq;
   qp.Hkv = pp.Hkv;
   qp.G = (int)(num_q_heads / num_kv_heads);
-  qp.NB = pp.NB;
+  qp.NBq = pp.NB;
+  qp.NBk = pp.NB;
+  qp.row0 = 0;
   qp.hidden = pp.hidden;
   qp.causal = (flags & 1) ? 1 : 0;
   qp.force_diag = (flags & 2) ? 1 : 0;
-  qp.tiles = (int)tiles;
+  qp.tiles_q = (int)tiles;
+  qp.tiles_k = (int)tiles;
+  qp.uk_bh_stride = nb * hidden;
   const int64_t grid2 = batch * num_q_heads * tiles * tiles;
   hipLaunchKernelGGL(gate_pairwise_kernel, dim3((unsigned)grid2), dim3(256), 0, s, qp);
   if ((err = hipGetLastError()) != hipSuccess)
@@ -748,5 +760,60 @@ extern "C" int tasft_gate_bwd(const float* soft_scores, const float* grad_soft,
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate_bwd: launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}
+
+extern "C" int tasft_gate_rows_fwd(const float* uq, const float* uk, const float* w_out,
+                                   const float* thresholds, float* soft_scores, float* logits,
+                                   uint8_t* hard_mask, unsigned long long* active_count,
+                                   int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                   int64_t rows, int64_t key_blocks, int64_t row0, int64_t hidden,
+                                   int64_t uk_head_stride, int flags, void* stream) {
+  if (!uq || !uk || !w_out || !thresholds || !soft_scores || !hard_mask || !active_count)
+    return set_error(kErrInvalidArgument, "gate_rows: null pointer argument");
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || rows <= 0 || key_blocks <= 0 ||
+      hidden <= 0 || row0 < 0)
+    return set_error(kErrInvalidArgument, "gate_rows: sizes must be positive (row0 >= 0)");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument, "gate_rows: num_q_heads must be a multiple of num_kv_heads");
+  if ((((uintptr_t)uq) & 15u) || (((uintptr_t)uk) & 15u))
+    return set_error(kErrInvalidArgument, "gate_rows: uq and uk must be 16-byte aligned");
+  if (uk_head_stride < key_blocks * hidden || uk_head_stride % 4 != 0 || hidden % 4 != 0)
+    return set_error(kErrInvalidArgument,
+                     "gate_rows: uk_head_stride must be >= key_blocks * hidden, and it and hidden "
+                     "multiples of 4");
+  const int64_t tq = (rows + kPairTile - 1) / kPairTile;
+  const int64_t tk = (key_blocks + kPairTile - 1) / kPairTile;
+  if (batch * num_q_heads * tq * tk > 0x7fffffffLL || row0 + rows > 0x7fffffffLL)
+    return set_error(kErrUnsupported, "gate_rows: problem too large for one launch");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(gate_counter_reset_kernel, dim3(1), dim3(64), 0, s, active_count);
+  GatePairParams qp;
+  qp.uq = uq;
+  qp.uk = uk;
+  qp.w_out = w_out;
+  qp.tau = thresholds;
+  qp.soft = soft_scores;
+  qp.logits = logits;
+  qp.mask = hard_mask;
+  qp.counter = active_count;
+  qp.B = (int)batch;
+  qp.Hq = (int)num_q_heads;
+  qp.Hkv = (int)num_kv_heads;
+  qp.G = (int)(num_q_heads / num_kv_heads);
+  qp.NBq = (int)rows;
+  qp.NBk = (int)key_blocks;
+  qp.row0 = (int)row0;
+  qp.hidden = (int)hidden;
+  qp.causal = (flags & 1) ? 1 : 0;
+  qp.force_diag = (flags & 2) ? 1 : 0;
+  qp.tiles_q = (int)tq;
+  qp.tiles_k = (int)tk;
+  qp.uk_bh_stride = uk_head_stride;
+  hipLaunchKernelGGL(gate_pairwise_kernel, dim3((unsigned)(batch * num_q_heads * tq * tk)), dim3(256),
+                     0, s, qp);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "gate_rows: launch failed: %s", hipGetErrorString(err));
   return kOk;
 }

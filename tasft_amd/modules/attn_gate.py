@@ -190,13 +190,30 @@ class AttnGate(nn.Module):
         *,
         return_logits: bool = False,
         force_diagonal: bool = False,
+        query_offset: int | None = None,
+        q_block_sum: torch.Tensor | None = None,
     ) -> GateOutput:
         """Block scores, hard mask and sparsity for ``q [B,H,S,D]``, ``k [B,H or Hkv,S,D]``.
 
         ``force_diagonal=True`` sets the diagonal blocks of ``hard_mask`` whatever their
         score (every query block then attends at least to itself).
+
+        ``query_offset`` (keyword extension for cached decoding, where S_q != S_k; without it
+        such a call raises as the reference does, ``attn_gate.py:216-221``): the queries are
+        tokens ``query_offset .. query_offset + S_q - 1`` of the sequence whose keys are
+        ``k``. The result holds the gate rows of the query blocks those tokens fall in,
+        ``[B, H, R, ceil(S_k / block)]``, with each row's block mean taken over its tokens
+        present in ``q`` plus ``q_block_sum`` (``[B, H, D]``, the sum of the queries of the
+        first row's block that precede ``query_offset``; default zero), divided by the block
+        size as the zero-padded pool does. For a decode step (S_q = 1, ``query_offset =
+        S_k - 1``) with ``q_block_sum`` given, the row equals the last row of this gate on
+        the whole sequence so far. Computed with torch operations (the serving path keeps
+        the projected key blocks across steps instead: ``tasft_amd.inference``).
         """
         tau = threshold if threshold is not None else self.default_threshold
+        if query_offset is not None:
+            return self._forward_rows(q, k, tau, return_logits, force_diagonal, int(query_offset),
+                                      q_block_sum)
         self._validate(q, k)
         if q.device != k.device:
             raise ValidationError(f"Q and K must be on the same device, got {q.device} vs {k.device}",
@@ -283,6 +300,65 @@ class AttnGate(nn.Module):
         active = hard.sum().reshape(1)
         return GateOutput(soft_scores=soft, hard_mask=hard, num_blocks_q=nb, num_blocks_k=nb,
                           logits=logits if return_logits else None, active_count=active)
+
+    def _forward_rows(self, q: torch.Tensor, k: torch.Tensor, tau: float | torch.Tensor,
+                      return_logits: bool, force_diagonal: bool, offset: int,
+                      q_block_sum: torch.Tensor | None) -> GateOutput:
+        """Gate rows for queries at ``offset ..`` against all of ``k`` (see ``forward``)."""
+        if q.ndim != 4 or k.ndim != 4:
+            raise ValidationError("Expected 4D Q and K tensors [B, H, S, D]",
+                                  context={"q_shape": list(q.shape), "k_shape": list(k.shape)})
+        B, H, Sq, D = q.shape
+        Sk = k.shape[2]
+        if (k.shape[0] != B or k.shape[3] != D or k.shape[1] <= 0 or H % k.shape[1] != 0
+                or Sq == 0 or offset < 0 or offset + Sq > Sk):
+            raise ValidationError(
+                f"query_offset {offset} with Q {tuple(q.shape)} does not fit K {tuple(k.shape)}",
+                context={"q_shape": list(q.shape), "k_shape": list(k.shape), "query_offset": offset})
+        if self.num_heads != H:
+            raise ValidationError(f"Expected {self.num_heads} heads, got {H}",
+                                  context={"expected_heads": self.num_heads, "actual_heads": H})
+        if self.head_dim != D:
+            raise ValidationError(f"Expected head_dim={self.head_dim}, got {D}",
+                                  context={"expected_dim": self.head_dim, "actual_dim": D})
+        bs = self.block_size
+        Hkv = k.shape[1]
+        w_in = self.gate_proj_in.weight
+        dt = torch.promote_types(torch.promote_types(q.dtype, k.dtype), w_in.dtype)
+        r0, r1 = offset // bs, (offset + Sq - 1) // bs
+        R = r1 - r0 + 1
+        front = offset - r0 * bs
+        qpad = F.pad(q.to(dt), (0, 0, front, R * bs - front - Sq))
+        qsum = qpad.view(B, H, R, bs, D).sum(3)
+        if q_block_sum is not None:
+            if tuple(q_block_sum.shape) != (B, H, D):
+                raise ValidationError(f"q_block_sum must have shape {(B, H, D)}, got {tuple(q_block_sum.shape)}",
+                                      context={"q_block_sum": list(q_block_sum.shape)})
+            qsum = qsum.clone()
+            qsum[:, :, 0] += q_block_sum.to(device=qsum.device, dtype=dt)
+        qb = qsum / bs
+        kb = self._pool_to_blocks(k.to(dt))
+        if Hkv != H:
+            kb = kb.repeat_interleave(H // Hkv, dim=1)
+        w = w_in.to(dt)
+        uq = qb @ w[:, :D].t() + self.gate_proj_in.bias.to(dt)
+        uk = kb @ w[:, D:].t()
+        logits = (F.relu(uq.unsqueeze(3) + uk.unsqueeze(2)) @ self.gate_proj_out.weight.to(dt).t()).squeeze(-1)
+        soft = torch.sigmoid(logits)
+        nbk = soft.shape[-1]
+        rows = torch.arange(r0, r1 + 1, device=soft.device)[:, None]
+        cols = torch.arange(nbk, device=soft.device)[None, :]
+        if self.is_causal:
+            soft = soft * (cols <= rows)
+        if isinstance(tau, torch.Tensor):
+            hard = soft >= self._thresholds(tau, soft.device).to(dt).view(1, H, 1, 1)
+        else:
+            hard = soft >= tau
+        if force_diagonal:
+            hard = hard | (cols == rows)
+        return GateOutput(soft_scores=soft, hard_mask=hard, num_blocks_q=R, num_blocks_k=nbk,
+                          logits=logits if return_logits else None,
+                          active_count=hard.sum().reshape(1))
 
     def compute_sparsity(self, soft_scores: torch.Tensor, threshold: float) -> float:
         """Fraction of scores below ``threshold`` (reference ``attn_gate.py:287-297``)."""

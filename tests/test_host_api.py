@@ -248,6 +248,30 @@ class TestAttnGateHost:
         torch.testing.assert_close(a.soft_scores, b.soft_scores)
         assert torch.equal(a.hard_mask, b.hard_mask)
 
+    def test_cached_decoding_rejected_without_query_offset(self):
+        """S_q != S_k raises as the reference does (pinned by its
+        tests/integration/test_model_families.py:915-948)."""
+        g = AttnGate(num_heads=4, head_dim=16, block_size=32)
+        with pytest.raises(ValidationError, match="Q and K must have same shape"):
+            g(torch.randn(1, 4, 8, 16), torch.randn(1, 4, 24, 16))
+
+    @pytest.mark.parametrize("t", [44, 40, 32, 0])
+    def test_query_offset_row_equals_full_gate_row(self, t):
+        """query_offset = t with the block's earlier queries as q_block_sum gives exactly
+        the row t // block of the gate on tokens 0 .. t."""
+        torch.manual_seed(1)
+        g = AttnGate(num_heads=4, head_dim=32, block_size=8)
+        q, k = torch.randn(2, 4, 45, 32), torch.randn(2, 2, 45, 32)
+        r = t // 8
+        row = g(q[:, :, t:t + 1], k[:, :, :t + 1], return_logits=True, query_offset=t,
+                q_block_sum=q[:, :, r * 8:t].sum(2))
+        full = g(q[:, :, :t + 1], k[:, :, :t + 1], return_logits=True)
+        assert row.soft_scores.shape == (2, 4, 1, r + 1)
+        torch.testing.assert_close(row.logits[:, :, 0], full.logits[:, :, r], rtol=0, atol=1e-6)
+        assert torch.equal(row.hard_mask[:, :, 0], full.hard_mask[:, :, r])
+        chunk = g(q[:, :, 16:45], k, return_logits=True, query_offset=16)
+        torch.testing.assert_close(chunk.logits, g(q, k, return_logits=True).logits[:, :, 2:], rtol=0, atol=1e-6)
+
     def test_cpu_gradients_reach_gate_parameters(self):
         g = AttnGate(num_heads=4, head_dim=32, block_size=8)
         out = g(torch.randn(1, 4, 64, 32), torch.randn(1, 4, 64, 32))
