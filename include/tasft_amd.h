@@ -4,8 +4,10 @@
  * Every function launches asynchronously on `stream` (a hipStream_t; pass the
  * caller's current stream) and never synchronises the device, allocates, frees or
  * retains a pointer beyond the call. Device buffers — inputs, outputs and
- * workspaces — are owned by the caller. Tensors are bf16 (as raw 16-bit words)
- * unless stated; each 4-D tensor is described by element strides for its dims
+ * workspaces — are owned by the caller. Q, K, V and outputs of attention are 16-bit
+ * (raw words) of the type named by the call's `dtype` argument: TASFT_DTYPE_BF16 or
+ * TASFT_DTYPE_F16 (scores, softmax and accumulation are fp32 either way); other tensors
+ * are as stated. Each 4-D tensor is described by element strides for its dims
  * (b, h, s, d) and the d stride must be 1. Return value: 0 on success, a negative
  * status on error, with the message available from tasft_last_error() on the
  * calling thread.
@@ -33,8 +35,14 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (6). */
+/* ABI version of this library (7). */
 int tasft_abi_version(void);
+
+/* Element types of the 16-bit tensors (the `dtype` argument). The reference kernel takes
+ * fp16 or bf16 (tasft/kernels/block_sparse_fa.py:228, :252 are dtype-generic) and its gate
+ * module fp16, bf16 or fp32 (tasft/modules/attn_gate.py:59). */
+#define TASFT_DTYPE_BF16 0
+#define TASFT_DTYPE_F16 1
 
 /*
  * Block-sparse flash-attention prefill.
@@ -46,7 +54,7 @@ int tasft_abi_version(void);
  * out[b,h,i,:] = softmax_j(q[b,h,i,:] . k[b,h/G,j,:] * scale + M[i,j]) v[b,h/G,j,:]
  * with M = 0 where block_mask[b,h,i/bs,j/bs] != 0 (AND j/bs <= i/bs when causal;
  * AND j <= i inside the diagonal block when causal) and j < seq_len, else -inf.
- * Rows with no admissible key are 0. P is rounded to bf16 before the PV product.
+ * Rows with no admissible key are 0. P is rounded to `dtype` before the PV product.
  * block_mask: [B, Hq, ceil(S/bs), ceil(S/bs)] bytes, strides in mask_strides (bytes).
  * head_dim in {64, 128}; block_size in {32, 64, 128}; strides of b/h/s multiples of 8.
  * workspace: NULL (one workgroup per query-block row), or >=
@@ -63,7 +71,8 @@ int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* ou
                            int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
                            int64_t block_size, const int64_t* q_strides, const int64_t* k_strides,
                            const int64_t* v_strides, const int64_t* o_strides,
-                           const int64_t* mask_strides, float scale, int causal, void* stream);
+                           const int64_t* mask_strides, float scale, int causal, int dtype,
+                           void* stream);
 
 /*
  * Block-sparse prefill of a packed batch of variable-length sequences, in one launch.
@@ -89,7 +98,7 @@ int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const void* v, v
                                   const int64_t* q_strides, const int64_t* k_strides,
                                   const int64_t* v_strides, const int64_t* o_strides,
                                   const int64_t* mask_strides, float scale, int causal,
-                                  void* stream);
+                                  int dtype, void* stream);
 
 /*
  * Bytes of the optional workspace of tasft_bsfa_prefill_fwd (work-queue counters).
@@ -129,7 +138,7 @@ int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cach
                           int64_t block_size, int64_t num_splits, const int64_t* q_strides,
                           const int64_t* k_strides, const int64_t* v_strides,
                           const int64_t* o_strides, const int64_t* mask_strides, float scale,
-                          void* stream);
+                          int dtype, void* stream);
 
 /*
  * tasft_bsfa_decode_fwd without a workspace: the variant that allocates nothing.
@@ -155,7 +164,7 @@ int tasft_bsfa_decode_fwd_noalloc(const void* q, const void* k_cache, const void
                                   int64_t num_splits, const int64_t* q_strides,
                                   const int64_t* k_strides, const int64_t* v_strides,
                                   const int64_t* o_strides, const int64_t* mask_strides,
-                                  float scale, void* stream);
+                                  float scale, int dtype, void* stream);
 
 /*
  * Split-K block-sparse decode over a paged KV cache (vLLM's block-table layout).
@@ -182,7 +191,8 @@ int tasft_bsfa_decode_paged_fwd(const void* q, const void* k_pages, const void* 
                                 int64_t num_pages, int64_t num_splits, const int64_t* q_strides,
                                 const int64_t* k_strides, const int64_t* v_strides,
                                 const int64_t* o_strides, const int64_t* mask_strides,
-                                int64_t block_table_stride, float scale, void* stream);
+                                int64_t block_table_stride, float scale, int dtype,
+                                void* stream);
 
 /* Bytes of workspace tasft_gate_fwd needs (projected block features; head_dim is checked
  * but does not change the size). */
@@ -217,7 +227,7 @@ int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float*
                    float* k_means, void* workspace, size_t workspace_bytes, int64_t batch,
                    int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
                    int64_t block_size, int64_t hidden, const int64_t* q_strides,
-                   const int64_t* k_strides, int flags, void* stream);
+                   const int64_t* k_strides, int flags, int dtype, void* stream);
 
 /*
  * The pairwise stage of the gate on precomputed projected units, for query-block rows that
@@ -287,7 +297,7 @@ int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask, 
                           int64_t seq_len, int64_t head_dim, int64_t block_size,
                           const int64_t* q_strides, const int64_t* k_strides,
                           const int64_t* mask_strides, float scale, int causal, int normalize,
-                          float temperature, float clamp, void* stream);
+                          float temperature, float clamp, int dtype, void* stream);
 
 /*
  * KL gate loss: replaces TASFTObjective.compute_gate_loss (tasft/training/objectives.py:187-221),

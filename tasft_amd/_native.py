@@ -57,34 +57,34 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_bsfa_prefill_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
+         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P],
     ),
     "tasft_bsfa_prefill_varlen_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
+         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P],
     ),
     "tasft_bsfa_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "tasft_bsfa_decode_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _P],
+         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
     ),
     "tasft_bsfa_decode_paged_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64, _F, _P],
+         _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64, _F, _I, _P],
     ),
     "tasft_bsfa_decode_fwd_noalloc": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _P],
+         _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _P],
     ),
     "tasft_gate_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64,
-         _I64, _I64, _I64P, _I64P, _I, _P],
+         _I64, _I64, _I64P, _I64P, _I, _I, _P],
     ),
     "tasft_gate_rows_fwd": (
         _I,
@@ -99,7 +99,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_gate_target_fwd": (
         _I,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _F, _I, _I,
-         _F, _F, _P],
+         _F, _F, _I, _P],
     ),
     "tasft_mask_compact_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "tasft_mask_compact": (
@@ -155,6 +155,23 @@ def strides_array(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(values))(*values)
 
 
+# Element types of the 16-bit tensors (TASFT_DTYPE_BF16 / TASFT_DTYPE_F16).
+DTYPE_BF16 = 0
+DTYPE_F16 = 1
+_DTYPE_CODES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
+KERNEL_DTYPES = tuple(_DTYPE_CODES)
+
+
+def dtype_code(dtype: torch.dtype, what: str) -> int:
+    """The C-ABI ``dtype`` argument for a torch dtype; raises ``KernelError`` for any other
+    than bf16 / fp16."""
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
+        raise KernelError(f"{what}: the HIP kernels take bf16 or fp16 tensors, got {dtype}",
+                          context={"dtype": str(dtype)})
+    return code
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -171,5 +188,6 @@ def check(status: int, what: str, context: dict[str, object] | None = None) -> N
         raise KernelError(f"{what} failed ({status}): {msg}", context={"status": status, **(context or {})})
 
 
-__all__ = ["EXPORTED_SYMBOLS", "LIB_PATH", "check", "is_available", "load_library", "ptr",
-           "stream_handle", "strides", "strides_array"]
+__all__ = ["DTYPE_BF16", "DTYPE_F16", "EXPORTED_SYMBOLS", "KERNEL_DTYPES", "LIB_PATH", "check",
+           "dtype_code", "is_available", "load_library", "ptr", "stream_handle", "strides",
+           "strides_array"]

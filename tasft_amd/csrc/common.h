@@ -1,6 +1,6 @@
 // Shared device/host helpers for the gfx950 block-sparse attention kernels.
 //
-// Everything here is CDNA4-specific: wave64, bf16 MFMA (v_mfma_f32_32x32x16_bf16),
+// Everything here is CDNA4-specific: wave64, bf16/fp16 MFMA (v_mfma_f32_32x32x16_{bf16,f16}),
 // and the 64-bank LDS of gfx950. No CUDA compatibility layer is used.
 #pragma once
 
@@ -66,6 +66,65 @@ __device__ __forceinline__ f32x16_t mfma_32x32x16_bf16(const bf16x8_t& a, const 
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// Element type of the 16-bit tensors (Q, K, V, out). The kernels move them as raw 16-bit
+// words; only the MFMA that multiplies them, the fp32 -> 16-bit rounding (P before the PV
+// product, the output) and the 16-bit -> fp32 unpack depend on it. Values match
+// TASFT_DTYPE_BF16 / TASFT_DTYPE_F16 of the C ABI.
+enum DType : int { kBf16 = 0, kF16 = 1 };
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// v_mfma_f32_32x32x16_{bf16,f16}: 8 elements per lane of A and B as raw words.
+template <int DT>
+__device__ __forceinline__ f32x16_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Round-to-nearest-even fp32 -> 16-bit of two values packed in one dword (lo in bits 0-15).
+template <int DT>
+__device__ __forceinline__ uint32_t pack16x2(float lo, float hi) {
+  if constexpr (DT == kF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, f16x2_t));
+  else
+    return pack_bf16x2(lo, hi);
+}
+
+// Unpack 8 16-bit values (as uint4) to 8 floats.
+template <int DT>
+__device__ __forceinline__ void unpack16x8(const u32x4_t& v, float* out) {
+  if constexpr (DT == kF16) {
+    const f16x8_t h = __builtin_bit_cast(f16x8_t, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)h[i];
+  } else {
+    unpack_bf16x8(v, out);
+  }
+}
+
+// Round-to-nearest-even fp32 -> one 16-bit value.
+template <int DT>
+__device__ __forceinline__ uint16_t f32_to16(float x) {
+  if constexpr (DT == kF16)
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  else
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+// One 16-bit value (low bits of `bits16`) to fp32.
+template <int DT>
+__device__ __forceinline__ float bits16_to_f32(uint32_t bits16) {
+  if constexpr (DT == kF16)
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+  else
+    return bf16_bits_to_f32(bits16);
 }
 
 // gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each group of 16 lanes,

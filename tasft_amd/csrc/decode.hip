@@ -16,7 +16,7 @@
 // the contiguous range of key blocks [s*NB/P, (s+1)*NB/P).) Its 4 waves take the
 // blocks round-robin. Each selected KV block is read from HBM once per KV
 // head, however many query heads chose it; all its K and V loads are issued together.
-// QK^T runs on MFMA (v_mfma_f32_32x32x16_bf16; K is loaded straight into the A-operand
+// QK^T runs on MFMA (v_mfma_f32_32x32x16_bf16, or _f16 for fp16 inputs; K is loaded straight into the A-operand
 // layout, the G query heads are the N columns), PV on the VALU. Partial
 // (max, sum, output) triples per (b, h, split) go to a caller-provided workspace and a
 // second kernel merges them.
@@ -80,7 +80,7 @@ __device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int voff
 // SUB keys (<= 64) of one KV block are processed at a time; a block of BS keys is
 // BS/SUB sub-blocks. MG >= G is the head count the loops are unrolled for (padding heads
 // carry zero probability).
-template <int BS, int D, int MG, bool PAGED = false>
+template <int BS, int D, int MG, bool PAGED, int DT>
 __global__ void __launch_bounds__(kDecodeWaves * kWave, 2)
 bsfa_decode_split_kernel(const DecodeParams p) {
   static_assert(!PAGED || BS <= 64, "paged caches use the one-sub-block path");
@@ -137,7 +137,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
 
   // Q^T as the MFMA B operand: lane (col, half) holds head h0+col, head dims
   // ks*16 + half*8 .. +7. Columns >= G are zero.
-  bf16x8_t qf[KSTEPS];
+  u32x4_t qf[KSTEPS];
   {
     const bool hv = col < G;
     const uint16_t* qrow = p.q + b * p.sq[0] + (int64_t)(h0 + (hv ? col : 0)) * p.sq[1];
@@ -145,7 +145,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     for (int ks = 0; ks < KSTEPS; ++ks) {
       u32x4_t val = {0u, 0u, 0u, 0u};
       if (hv) val = *(const u32x4_t*)(qrow + ks * 16 + half * 8);
-      qf[ks] = as_bf16x8(val);
+      qf[ks] = val;
     }
   }
   __syncthreads();
@@ -322,7 +322,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         sacc[t2] = (f32x16_t){};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
-          sacc[t2] = mfma_32x32x16_bf16(as_bf16x8(ka[t2][ks]), qf[ks], sacc[t2]);
+          sacc[t2] = mfma16<DT>(ka[t2][ks], qf[ks], sacc[t2]);
       }
       // The next block of this wave: its K loads go out now (the K registers are free).
       const int en = e + kDecodeWaves;
@@ -386,7 +386,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       for (int i = 0; i < VPL; ++i) {
         const int kk = kg + KG * i;
         float vf[8];
-        unpack_bf16x8(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
+        unpack16x8<DT>(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
 #pragma unroll
         for (int gg = 0; gg < MG; ++gg) {
           const float pv = pw[kk * MG + gg];
@@ -459,7 +459,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
           sacc[t2] = (f32x16_t){};
 #pragma unroll
           for (int ks = 0; ks < KSTEPS; ++ks)
-            sacc[t2] = mfma_32x32x16_bf16(as_bf16x8(ka[t2][ks]), qf[ks], sacc[t2]);
+            sacc[t2] = mfma16<DT>(ka[t2][ks], qf[ks], sacc[t2]);
         }
         // Register r of tile t2 holds key t2*32 + 8*(r/4) + 4*half + r%4 of head `col`.
         float mx = -INFINITY;
@@ -509,7 +509,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
         for (int i = 0; i < VPL; ++i) {
           const int kk = kg + KG * i;
           float vf[8];
-          unpack_bf16x8(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
+          unpack16x8<DT>(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
 #pragma unroll
           for (int gg = 0; gg < MG; ++gg) {
             const float pv = pw[kk * MG + gg];
@@ -562,8 +562,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     if (p.P == 1) {
       // One split: this is the whole row, written directly (no combine pass).
       const float r = L > 0.f ? O / L : 0.f;
-      const __bf16 rb = (__bf16)r;
-      p.o[b * p.so[0] + (int64_t)(h0 + gg) * p.so[1] + d] = __builtin_bit_cast(uint16_t, rb);
+      p.o[b * p.so[0] + (int64_t)(h0 + gg) * p.so[1] + d] = f32_to16<DT>(r);
     } else {
       const int64_t row = ((int64_t)b * p.Hq + h0 + gg) * p.P + s;
       p.ws_o[row * D + d] = O;
@@ -575,8 +574,8 @@ bsfa_decode_split_kernel(const DecodeParams p) {
   }
 }
 
-// Merge the P split partials of every (b, h) and write the bf16 output row.
-template <int D>
+// Merge the P split partials of every (b, h) and write the output row.
+template <int D, int DT>
 __global__ void __launch_bounds__(D)
 bsfa_decode_combine_kernel(const DecodeParams p) {
   const int64_t bh = blockIdx.x;
@@ -595,28 +594,33 @@ bsfa_decode_combine_kernel(const DecodeParams p) {
     O += os[(int64_t)sp * D + d] * f;
   }
   const float r = L > 0.f ? O / L : 0.f;
-  const __bf16 rb = (__bf16)r;
-  p.o[b * p.so[0] + h * p.so[1] + d] = __builtin_bit_cast(uint16_t, rb);
+  p.o[b * p.so[0] + h * p.so[1] + d] = f32_to16<DT>(r);
 }
 
-template <int BS, int D, int MG, bool PAGED = false>
+template <int BS, int D, int MG, bool PAGED, int DT>
 static hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.B * p.Hkv * p.P;
-  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG, PAGED>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG, PAGED, DT>), dim3((unsigned)grid),
                      dim3(kDecodeWaves * kWave), 0, stream, p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.P == 1) return err;
-  hipLaunchKernelGGL((bsfa_decode_combine_kernel<D>), dim3((unsigned)((int64_t)p.B * p.Hq)), dim3(D),
+  hipLaunchKernelGGL((bsfa_decode_combine_kernel<D, DT>), dim3((unsigned)((int64_t)p.B * p.Hq)), dim3(D),
                      0, stream, p);
   return hipGetLastError();
 }
 
+template <int BS, int D, bool PAGED, int DT>
+static hipError_t launch_decode_dt(const DecodeParams& p, hipStream_t stream) {
+  if (p.G <= 1) return launch_decode_g<BS, D, 1, PAGED, DT>(p, stream);
+  if (p.G <= 2) return launch_decode_g<BS, D, 2, PAGED, DT>(p, stream);
+  if (p.G <= 4) return launch_decode_g<BS, D, 4, PAGED, DT>(p, stream);
+  return launch_decode_g<BS, D, 8, PAGED, DT>(p, stream);
+}
+
 template <int BS, int D, bool PAGED = false>
-static hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
-  if (p.G <= 1) return launch_decode_g<BS, D, 1, PAGED>(p, stream);
-  if (p.G <= 2) return launch_decode_g<BS, D, 2, PAGED>(p, stream);
-  if (p.G <= 4) return launch_decode_g<BS, D, 4, PAGED>(p, stream);
-  return launch_decode_g<BS, D, 8, PAGED>(p, stream);
+static hipError_t launch_decode(const DecodeParams& p, int dtype, hipStream_t stream) {
+  return dtype == kF16 ? launch_decode_dt<BS, D, PAGED, kF16>(p, stream)
+                       : launch_decode_dt<BS, D, PAGED, kBf16>(p, stream);
 }
 
 }  // namespace tasft
@@ -636,10 +640,12 @@ static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, v
                       int64_t block_size, int64_t num_splits, const int64_t* q_strides,
                       const int64_t* k_strides, const int64_t* v_strides,
                       const int64_t* o_strides, const int64_t* mask_strides, float scale,
-                      void* stream) {
+                      int dtype, void* stream) {
   if (!q || !k_cache || !v_cache || !out || !block_mask || !workspace || !q_strides ||
       !k_strides || !v_strides || !o_strides || !mask_strides)
     return set_error(kErrInvalidArgument, "decode: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "decode: dtype must be bf16 (0) or fp16 (1), got %d", dtype);
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || kv_len_max <= 0 || num_splits <= 0)
     return set_error(kErrInvalidArgument, "decode: sizes must be positive");
   if (num_q_heads % num_kv_heads != 0)
@@ -713,12 +719,12 @@ static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, v
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128>(p, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64>(p, s);
-  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128>(p, s);
-  else if (block_size == 32 && head_dim == 64) err = launch_decode<32, 64>(p, s);
-  else if (block_size == 128 && head_dim == 128) err = launch_decode<128, 128>(p, s);
-  else err = launch_decode<128, 64>(p, s);
+  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128>(p, dtype, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64>(p, dtype, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128>(p, dtype, s);
+  else if (block_size == 32 && head_dim == 64) err = launch_decode<32, 64>(p, dtype, s);
+  else if (block_size == 128 && head_dim == 128) err = launch_decode<128, 128>(p, dtype, s);
+  else err = launch_decode<128, 64>(p, dtype, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "decode: launch failed: %s", hipGetErrorString(err));
   return kOk;
@@ -731,11 +737,12 @@ extern "C" int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const v
                                      int64_t head_dim, int64_t block_size, int64_t num_splits,
                                      const int64_t* q_strides, const int64_t* k_strides,
                                      const int64_t* v_strides, const int64_t* o_strides,
-                                     const int64_t* mask_strides, float scale, void* stream) {
+                                     const int64_t* mask_strides, float scale, int dtype,
+                                     void* stream) {
   return decode_fwd(q, k_cache, v_cache, out, block_mask, kv_lens, workspace, workspace_bytes,
                     batch, num_q_heads, num_kv_heads, kv_len_max, head_dim, block_size,
                     num_splits, q_strides, k_strides, v_strides, o_strides, mask_strides, scale,
-                    stream);
+                    dtype, stream);
 }
 
 // ---------------------------------------------------------------------------- no allocation
@@ -776,7 +783,10 @@ extern "C" int tasft_bsfa_decode_fwd_noalloc(
     const int32_t* kv_lens, int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
     int64_t kv_len_max, int64_t head_dim, int64_t block_size, int64_t num_splits,
     const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-    const int64_t* o_strides, const int64_t* mask_strides, float scale, void* stream) {
+    const int64_t* o_strides, const int64_t* mask_strides, float scale, int dtype, void* stream) {
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "decode_noalloc: dtype must be bf16 (0) or fp16 (1), got %d",
+                     dtype);
   const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
   if (need > kDecodeScratchBytes)
     return set_error(kErrWorkspace,
@@ -790,7 +800,8 @@ extern "C" int tasft_bsfa_decode_fwd_noalloc(
   if (rc != kOk) return rc;
   return decode_fwd(q, k_cache, v_cache, out, block_mask, kv_lens, ws, kDecodeScratchBytes, batch,
                     num_q_heads, num_kv_heads, kv_len_max, head_dim, block_size, num_splits,
-                    q_strides, k_strides, v_strides, o_strides, mask_strides, scale, stream);
+                    q_strides, k_strides, v_strides, o_strides, mask_strides, scale, dtype,
+                    stream);
 }
 
 extern "C" int tasft_bsfa_decode_paged_fwd(
@@ -800,10 +811,13 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
     int64_t head_dim, int64_t block_size, int64_t page_size, int64_t num_pages,
     int64_t num_splits, const int64_t* q_strides, const int64_t* k_strides,
     const int64_t* v_strides, const int64_t* o_strides, const int64_t* mask_strides,
-    int64_t block_table_stride, float scale, void* stream) {
+    int64_t block_table_stride, float scale, int dtype, void* stream) {
   if (!q || !k_pages || !v_pages || !out || !block_mask || !block_table || !kv_lens ||
       !workspace || !q_strides || !k_strides || !v_strides || !o_strides || !mask_strides)
     return set_error(kErrInvalidArgument, "decode_paged: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "decode_paged: dtype must be bf16 (0) or fp16 (1), got %d",
+                     dtype);
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || kv_len_max <= 0 || num_splits <= 0 ||
       num_pages <= 0)
     return set_error(kErrInvalidArgument, "decode_paged: sizes must be positive");
@@ -890,10 +904,10 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128, true>(p, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64, true>(p, s);
-  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128, true>(p, s);
-  else err = launch_decode<32, 64, true>(p, s);
+  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128, true>(p, dtype, s);
+  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64, true>(p, dtype, s);
+  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128, true>(p, dtype, s);
+  else err = launch_decode<32, 64, true>(p, dtype, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "decode_paged: launch failed: %s", hipGetErrorString(err));
   return kOk;

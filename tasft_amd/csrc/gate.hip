@@ -10,7 +10,7 @@
 // this computes u_i = W_q qbar_i + b_in once per query block and v_j = W_k kbar_j once
 // per key block, so each pair costs hidden x (add, max, fma) instead of a 2D-wide GEMV.
 //
-// Pooling streams Q and K from HBM exactly once (GQA-native: K is pooled per KV head,
+// Pooling streams Q and K (bf16 or fp16, accumulated in fp32) from HBM exactly once (GQA-native: K is pooled per KV head,
 // never expanded) in one kernel that also projects the block means (a streaming variant
 // for block size 64 and D in {64, 128}, a generic one otherwise). The pairwise kernel evaluates the MLP for the causal pairs in fp32, applies
 // sigmoid, the causal zero and the per-head threshold, and writes soft scores (fp32),
@@ -19,6 +19,8 @@
 #include <algorithm>
 
 #include "common.h"
+
+#include "../../include/tasft_amd.h"
 
 namespace tasft {
 
@@ -40,6 +42,7 @@ struct GatePoolParams {
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
 };
 
+template <int DT>
 __global__ void __launch_bounds__(256)
 gate_pool_project_kernel(const GatePoolParams p) {
   __shared__ float partial[256][8];  // per-thread 8-wide partial sums (row-group major)
@@ -76,7 +79,7 @@ gate_pool_project_kernel(const GatePoolParams p) {
         if (tok >= p.S) break;
         const u32x4_t v = *(const u32x4_t*)(src + tok * srow + dc * 8);
         float f[8];
-        unpack_bf16x8(v, f);
+        unpack16x8<DT>(v, f);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] += f[j];
       }
@@ -134,7 +137,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
-template <int D>
+template <int D, int DT>
 __global__ void __launch_bounds__(256)
 gate_pool_proj64_kernel(const GatePoolParams p) {
   constexpr int BSZ = 64;
@@ -183,7 +186,7 @@ gate_pool_proj64_kernel(const GatePoolParams p) {
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         float f[8];
-        unpack_bf16x8(v[bi][i], f);
+        unpack16x8<DT>(v[bi][i], f);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] += f[j];
       }
@@ -601,10 +604,12 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len,
                               int64_t head_dim, int64_t block_size, int64_t hidden,
                               const int64_t* q_strides, const int64_t* k_strides, int flags,
-                              void* stream) {
+                              int dtype, void* stream) {
   if (!q || !k || !w_in || !b_in || !w_out || !thresholds || !soft_scores || !hard_mask ||
       !active_count || !workspace || !q_strides || !k_strides)
     return set_error(kErrInvalidArgument, "gate: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "gate: dtype must be bf16 (0) or fp16 (1), got %d", dtype);
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0 || block_size <= 0 ||
       hidden <= 0)
     return set_error(kErrInvalidArgument, "gate: sizes must be positive");
@@ -662,13 +667,21 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   if (fast) {
     const int64_t fchunks = (nb + kFusePB - 1) / kFusePB;
     const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * fchunks;
-    if (head_dim == 128)
-      hipLaunchKernelGGL(gate_pool_proj64_kernel<128>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+    const dim3 g1((unsigned)grid1);
+    if (head_dim == 128 && dtype == kF16)
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16>), g1, dim3(256), 0, s, pp);
+    else if (head_dim == 128)
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kBf16>), g1, dim3(256), 0, s, pp);
+    else if (dtype == kF16)
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kF16>), g1, dim3(256), 0, s, pp);
     else
-      hipLaunchKernelGGL(gate_pool_proj64_kernel<64>, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kBf16>), g1, dim3(256), 0, s, pp);
   } else {
-    const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * chunks;
-    hipLaunchKernelGGL(gate_pool_project_kernel, dim3((unsigned)grid1), dim3(256), 0, s, pp);
+    const dim3 g1((unsigned)(batch * (num_q_heads + num_kv_heads) * chunks));
+    if (dtype == kF16)
+      hipLaunchKernelGGL(gate_pool_project_kernel<kF16>, g1, dim3(256), 0, s, pp);
+    else
+      hipLaunchKernelGGL(gate_pool_project_kernel<kBf16>, g1, dim3(256), 0, s, pp);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)

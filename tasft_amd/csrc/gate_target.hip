@@ -10,11 +10,13 @@
 // over k-blocks" reading of the target that the benchmark configuration uses) and the
 // clamp(+-50) / temperature variant of tasft/modules/tasft_attention.py:272-290.
 //
-// Kernel 1 computes each block maximum with the same S^T = K . Q^T bf16 MFMA tiling as
-// the prefill kernel (v_mfma_f32_32x32x16_bf16, fp32 accumulation) and keeps only the
-// maximum of every 64x64 tile, so the work is the QK^T half of a dense causal prefill
-// and nothing of size S^2 touches HBM. Kernel 2 normalises in place.
+// Kernel 1 computes each block maximum with the same S^T = K . Q^T MFMA tiling as the
+// prefill kernel (v_mfma_f32_32x32x16_bf16, or _f16 for fp16 inputs; fp32 accumulation)
+// and keeps only the maximum of every 64x64 tile, so the work is the QK^T half of a dense
+// causal prefill and nothing of size S^2 touches HBM. Kernel 2 normalises in place.
 #include "common.h"
+
+#include "../../include/tasft_amd.h"
 
 namespace tasft {
 
@@ -40,7 +42,7 @@ __device__ __forceinline__ void gt_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst,
 
 // Without a mask (MASKED false) the raw maxima are scaled once at the end (scale > 0
 // commutes with max); with one, each score is scaled and the mask added before the max.
-template <int BS, int D, bool MASKED>
+template <int BS, int D, bool MASKED, int DT>
 __global__ void __launch_bounds__(BS / 32 * kWave)
 gate_target_blockmax_kernel(const GateTargetParams p) {
   constexpr int WAVES = BS / 32;
@@ -78,12 +80,12 @@ gate_target_blockmax_kernel(const GateTargetParams p) {
   const bool qvalid = qrow < p.S;
   const float* mrow = MASKED ? p.amask + b * p.sam[0] + h * p.sam[1] + (int64_t)qrow * p.sam[2]
                              : nullptr;
-  bf16x8_t qf[KSTEPS];
+  u32x4_t qf[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
     u32x4_t val = {0u, 0u, 0u, 0u};
     if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
-    qf[ks] = as_bf16x8(val);
+    qf[ks] = val;
   }
 
   const int kb_end = p.causal ? qb + 1 : p.NB;
@@ -117,7 +119,7 @@ gate_target_blockmax_kernel(const GateTargetParams p) {
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
         const u32x4_t a = *(const u32x4_t*)(k_lds + (t * 32 + col) * KST + ks * 16 + half * 8);
-        s = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s);
+        s = mfma16<DT>(a, qf[ks], s);
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -191,7 +193,7 @@ __device__ __forceinline__ int gt_swz(int r, int cc) {
 // MASKED adds the caller's additive mask: each wave loads the mask values of its 32 x 64
 // sub-tile (float4 per lane and 4-key group) before it issues the next block's DMA, so the
 // fixed DMA wait also covers them, and adds them to the scaled scores before the max.
-template <int D, int HPW, bool MASKED, int WPH = 2>
+template <int D, int HPW, bool MASKED, int DT, int WPH = 2>
 __global__ void __launch_bounds__(HPW * WPH * 64)
 gate_target_bs64_kernel(const GateTargetParams p) {
   constexpr int BS = 64;
@@ -246,13 +248,13 @@ gate_target_bs64_kernel(const GateTargetParams p) {
   const float* mrow = MASKED ? p.amask + b * p.sam[0] + h * p.sam[1] + (int64_t)qrow * p.sam[2]
                              : nullptr;
   const float post_scale = MASKED ? 1.f : p.scale;
-  bf16x8_t qf[KSTEPS];
+  u32x4_t qf[KSTEPS];
   auto load_q = [&]() {
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       u32x4_t val = {0u, 0u, 0u, 0u};
       if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
-      qf[ks] = as_bf16x8(val);
+      qf[ks] = val;
     }
   };
   // DMA units of this wave: u = wave, wave + NWAVES, ...
@@ -303,7 +305,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
       for (int t = 0; t < NKT; ++t) {
         const int kr = krow_l + 32 * t;
         const u32x4_t a = *(const u32x4_t*)(kt + kr * ROWB + gt_swz<D>(kr, cc) * 16);
-        s[t] = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s[t]);
+        s[t] = mfma16<DT>(a, qf[ks], s[t]);
       }
     }
     const int key0 = kb * BS;
@@ -380,36 +382,43 @@ gate_target_bs64_kernel(const GateTargetParams p) {
   store(kb_end - 1);
 }
 
-template <int D, bool MASKED>
+template <int D, bool MASKED, int DT>
 static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t stream) {
   const int hpw = (p.G % 4 == 0) ? 4 : (p.G % 2 == 0 ? 2 : 1);
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq / hpw;
   if (hpw == 4)
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4, MASKED>), dim3((unsigned)grid), dim3(4 * 128), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4, MASKED, DT>), dim3((unsigned)grid), dim3(4 * 128), 0, stream, p);
   else if (hpw == 2)
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2, MASKED>), dim3((unsigned)grid), dim3(2 * 128), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 2, MASKED, DT>), dim3((unsigned)grid), dim3(2 * 128), 0, stream, p);
   else
-    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1, MASKED>), dim3((unsigned)grid), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL((gate_target_bs64_kernel<D, 1, MASKED, DT>), dim3((unsigned)grid), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 
-template <int BS, int D, bool MASKED>
+template <int BS, int D, bool MASKED, int DT>
 static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
-  hipLaunchKernelGGL((gate_target_blockmax_kernel<BS, D, MASKED>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gate_target_blockmax_kernel<BS, D, MASKED, DT>), dim3((unsigned)grid),
                      dim3(BS / 32 * kWave), 0, stream, p);
   return hipGetLastError();
 }
 
+template <bool MASKED, int DT>
+static hipError_t dispatch_blockmax_dt(const GateTargetParams& p, int64_t block_size,
+                                       int64_t head_dim, hipStream_t s) {
+  if (block_size == 64 && head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
+  if (block_size == 64 && head_dim == 64) return launch_blockmax_bs64<64, MASKED, DT>(p, s);
+  if (block_size == 32 && head_dim == 128) return launch_blockmax<32, 128, MASKED, DT>(p, s);
+  if (block_size == 32 && head_dim == 64) return launch_blockmax<32, 64, MASKED, DT>(p, s);
+  if (block_size == 128 && head_dim == 128) return launch_blockmax<128, 128, MASKED, DT>(p, s);
+  return launch_blockmax<128, 64, MASKED, DT>(p, s);
+}
+
 template <bool MASKED>
 static hipError_t dispatch_blockmax(const GateTargetParams& p, int64_t block_size,
-                                    int64_t head_dim, hipStream_t s) {
-  if (block_size == 64 && head_dim == 128) return launch_blockmax_bs64<128, MASKED>(p, s);
-  if (block_size == 64 && head_dim == 64) return launch_blockmax_bs64<64, MASKED>(p, s);
-  if (block_size == 32 && head_dim == 128) return launch_blockmax<32, 128, MASKED>(p, s);
-  if (block_size == 32 && head_dim == 64) return launch_blockmax<32, 64, MASKED>(p, s);
-  if (block_size == 128 && head_dim == 128) return launch_blockmax<128, 128, MASKED>(p, s);
-  return launch_blockmax<128, 64, MASKED>(p, s);
+                                    int64_t head_dim, int dtype, hipStream_t s) {
+  return dtype == kF16 ? dispatch_blockmax_dt<MASKED, kF16>(p, block_size, head_dim, s)
+                       : dispatch_blockmax_dt<MASKED, kBf16>(p, block_size, head_dim, s);
 }
 
 // KL gate loss (reference TASFTObjective.compute_gate_loss, objectives.py:187-221) of one
@@ -475,9 +484,12 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
                                      int64_t block_size, const int64_t* q_strides,
                                      const int64_t* k_strides, const int64_t* mask_strides,
                                      float scale, int causal, int normalize, float temperature,
-                                     float clamp, void* stream) {
+                                     float clamp, int dtype, void* stream) {
   if (!q || !k || !target || !q_strides || !k_strides || (attn_mask && !mask_strides))
     return set_error(kErrInvalidArgument, "gate_target: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "gate_target: dtype must be bf16 (0) or fp16 (1), got %d",
+                     dtype);
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0)
     return set_error(kErrInvalidArgument, "gate_target: batch, heads and seq_len must be positive");
   if (num_q_heads % num_kv_heads != 0)
@@ -534,8 +546,8 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
   p.causal = causal ? 1 : 0;
 
   hipStream_t s = (hipStream_t)stream;
-  hipError_t err = attn_mask ? dispatch_blockmax<true>(p, block_size, head_dim, s)
-                             : dispatch_blockmax<false>(p, block_size, head_dim, s);
+  hipError_t err = attn_mask ? dispatch_blockmax<true>(p, block_size, head_dim, dtype, s)
+                             : dispatch_blockmax<false>(p, block_size, head_dim, dtype, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate_target: block-max launch failed: %s", hipGetErrorString(err));
 

@@ -17,6 +17,8 @@
 // each wave writes its row's column indices in ascending order from the same ballots.
 #include "common.h"
 
+#include "../../include/tasft_amd.h"
+
 namespace tasft {
 
 struct MaskView {

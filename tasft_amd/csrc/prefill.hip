@@ -5,8 +5,8 @@
 //   * one query block of BS rows attends to the key blocks whose mask byte is non-zero;
 //     with causal=1 the mask is AND-ed with the block lower triangle and, inside the
 //     diagonal block, key > query is excluded;
-//   * scores are fp32 (bf16 MFMA, fp32 accumulate) times `scale`; online softmax in fp32;
-//     P is rounded to bf16 before the PV product (:252); l stays fp32;
+//   * scores are fp32 (bf16 or fp16 MFMA, fp32 accumulate) times `scale`; online softmax in
+//     fp32; P is rounded to the input type before the PV product (:252); l stays fp32;
 //   * rows with no active key output 0 (:257-258); rows >= S are never stored (:268-269).
 //
 // GQA is native: query head h reads key/value head h / (Hq / Hkv) in place, so K/V are
@@ -15,7 +15,7 @@
 //
 // Mapping onto CDNA4. A workgroup owns one (batch, query head, query block) and has
 // BS/32 waves; wave w owns 32 query rows. Each key block is computed as
-// S^T = K . Q^T with v_mfma_f32_32x32x16_bf16, so a lane owns one query column of S^T:
+// S^T = K . Q^T with v_mfma_f32_32x32x16_bf16 (_f16 for fp16 inputs), so a lane owns one query column of S^T:
 // its running max and sum live in that lane (plus the lane 32 away), and the P^T
 // accumulator registers feed the PV product O^T = V^T . P^T directly as the B operand
 // with no shuffle. K (row major) and V^T (transposed while staging) go through LDS
@@ -24,6 +24,8 @@
 #include <type_traits>
 
 #include "common.h"
+
+#include "../../include/tasft_amd.h"
 
 namespace tasft {
 
@@ -109,7 +111,7 @@ __global__ void bsfa_queue_reset_kernel(int* queue) {
   if (threadIdx.x < kQueueSlots) queue[threadIdx.x] = 0;
 }
 
-template <int BS, int D>
+template <int BS, int D, int DT>
 __global__ void __launch_bounds__(BS / 32 * kWave)
 bsfa_prefill_kernel(const PrefillParams p) {
   constexpr int WAVES = BS / 32;
@@ -117,8 +119,8 @@ bsfa_prefill_kernel(const PrefillParams p) {
   constexpr int KSTEPS = D / 16;   // MFMA k-steps over the head dim
   constexpr int KTILES = BS / 32;  // 32-key tiles per key block
   constexpr int DTILES = D / 32;   // 32-row head-dim tiles of O^T
-  constexpr int KST = D + 8;       // LDS row stride of K (bf16 elements)
-  constexpr int VST = BS + 4;      // LDS row stride of V^T (bf16 elements)
+  constexpr int KST = D + 8;       // LDS row stride of K (16-bit elements)
+  constexpr int VST = BS + 4;      // LDS row stride of V^T (16-bit elements)
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[BS * KST];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VST];
@@ -147,12 +149,12 @@ bsfa_prefill_kernel(const PrefillParams p) {
   // ks*16 + half*8 .. +7 for every k-step.
   const int qrow = qb * BS + wave * 32 + col;
   const bool qvalid = qrow < S;
-  bf16x8_t qf[KSTEPS];
+  u32x4_t qf[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
     u32x4_t val = {0u, 0u, 0u, 0u};
     if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
-    qf[ks] = as_bf16x8(val);
+    qf[ks] = val;
   }
 
   f32x16_t oacc[DTILES];
@@ -214,7 +216,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
           const u32x4_t a = *(const u32x4_t*)(k_lds + (t * 32 + col) * KST + ks * 16 + half * 8);
-          s[t] = mfma_32x32x16_bf16(as_bf16x8(a), qf[ks], s[t]);
+          s[t] = mfma16<DT>(a, qf[ks], s[t]);
         }
       }
 
@@ -255,16 +257,16 @@ bsfa_prefill_kernel(const PrefillParams p) {
 
       // P^T as the B operand of O^T = V^T P^T: k-step (t, pp) uses registers 8pp..8pp+7
       // of tile t, i.e. keys t*32 + 16pp + 8*(j/4) + 4*half + j%4 for slot j.
-      bf16x8_t pb[KTILES][2];
+      u32x4_t pb[KTILES][2];
 #pragma unroll
       for (int t = 0; t < KTILES; ++t) {
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
-          const u32x4_t w = {pack_bf16x2(s[t][8 * pp + 0], s[t][8 * pp + 1]),
-                             pack_bf16x2(s[t][8 * pp + 2], s[t][8 * pp + 3]),
-                             pack_bf16x2(s[t][8 * pp + 4], s[t][8 * pp + 5]),
-                             pack_bf16x2(s[t][8 * pp + 6], s[t][8 * pp + 7])};
-          pb[t][pp] = as_bf16x8(w);
+          const u32x4_t w = {pack16x2<DT>(s[t][8 * pp + 0], s[t][8 * pp + 1]),
+                             pack16x2<DT>(s[t][8 * pp + 2], s[t][8 * pp + 3]),
+                             pack16x2<DT>(s[t][8 * pp + 4], s[t][8 * pp + 5]),
+                             pack16x2<DT>(s[t][8 * pp + 6], s[t][8 * pp + 7])};
+          pb[t][pp] = w;
         }
       }
       // V^T as the A operand with the same key order: two 4-key runs per slot group.
@@ -278,14 +280,14 @@ bsfa_prefill_kernel(const PrefillParams p) {
             const u32x2_t lo = *(const u32x2_t*)vp;
             const u32x2_t hi = *(const u32x2_t*)(vp + 8);
             const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
-            oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb[t][pp], oacc[dt]);
+            oacc[dt] = mfma16<DT>(a, pb[t][pp], oacc[dt]);
           }
         }
       }
     }
   }
 
-  // Epilogue: combine the two half-lane denominators, normalise, store bf16.
+  // Epilogue: combine the two half-lane denominators, normalise, store in the input type.
   const float l_tot = l_run + xor32(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qvalid) {
@@ -295,18 +297,18 @@ bsfa_prefill_kernel(const PrefillParams p) {
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         const int d0 = dt * 32 + 8 * gq + 4 * half;
-        const u32x2_t w = {pack_bf16x2(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
-                           pack_bf16x2(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
+        const u32x2_t w = {pack16x2<DT>(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
+                           pack16x2<DT>(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
         *(u32x2_t*)(orow + d0) = w;
       }
     }
   }
 }
 
-template <int BS, int D>
+template <int BS, int D, int DT>
 static hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
-  hipLaunchKernelGGL((bsfa_prefill_kernel<BS, D>), dim3((unsigned)grid), dim3(BS / 32 * kWave), 0,
+  hipLaunchKernelGGL((bsfa_prefill_kernel<BS, D, DT>), dim3((unsigned)grid), dim3(BS / 32 * kWave), 0,
                      stream, p);
   return hipGetLastError();
 }
@@ -356,7 +358,7 @@ __device__ __forceinline__ int next_active_block(const uint8_t* mrow, int64_t st
   return kb;
 }
 
-// One 64 x D bf16 tile in LDS, written by buffer_load_dwordx4 ... lds (DMA, no VGPRs).
+// One 64 x D 16-bit tile in LDS, written by buffer_load_dwordx4 ... lds (DMA, no VGPRs).
 // Unit u (1 KB, one instruction of one wave) covers bytes u*1024 .. +1023 of the tile;
 // lane l of that instruction lands at byte u*1024 + 16*l, i.e. row (u*1024+16l)/ROWB,
 // 16-byte position ((u*1024+16l)%ROWB)/16. The lane therefore loads the global chunk
@@ -381,7 +383,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
-template <int D>
+template <int D, int DT>
 __global__ void __launch_bounds__(256, 2)
 bsfa_prefill_bs64_kernel(const PrefillParams p) {
   constexpr int BS = 64;
@@ -463,12 +465,12 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   // the ticket of the item after the next, which the first wait also covers.
   uint8_t mb = mbyte;
   if (!pre && lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
-  bf16x8_t qf[KSTEPS];
+  u32x4_t qf[KSTEPS];
   {
     // Rows past the end read row S-1: per-row results, never stored.
     const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : S - 1) * p.sq[2] + half * 8;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *(const u32x4_t*)(qr + ks * 16);
   }
   // Start the DMA of key block kb into one stage (rows >= S arrive as zeros). With
   // small spans the resource base and size take 32-bit scalar math only.
@@ -522,7 +524,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     }
     f32x16_t s = (f32x16_t){};
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) s = mfma_32x32x16_bf16(as_bf16x8(kf[ks]), qf[ks], s);
+    for (int ks = 0; ks < KSTEPS; ++ks) s = mfma16<DT>(kf[ks], qf[ks], s);
     // Each S MFMA followed by two V^T reads.
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -565,15 +567,15 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     // O^T += V^T P^T over this wave's 32 keys: two k-steps of 16 keys.
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
-      const u32x4_t w = {pack_bf16x2(s[8 * pp + 0], s[8 * pp + 1]),
-                         pack_bf16x2(s[8 * pp + 2], s[8 * pp + 3]),
-                         pack_bf16x2(s[8 * pp + 4], s[8 * pp + 5]),
-                         pack_bf16x2(s[8 * pp + 6], s[8 * pp + 7])};
-      const bf16x8_t pb = as_bf16x8(w);
+      const u32x4_t w = {pack16x2<DT>(s[8 * pp + 0], s[8 * pp + 1]),
+                         pack16x2<DT>(s[8 * pp + 2], s[8 * pp + 3]),
+                         pack16x2<DT>(s[8 * pp + 4], s[8 * pp + 5]),
+                         pack16x2<DT>(s[8 * pp + 6], s[8 * pp + 7])};
+      const u32x4_t pb = w;
 #pragma unroll
       for (int dt = 0; dt < DTILES; ++dt) {
         const u32x4_t a = {vlo[pp][dt][0], vlo[pp][dt][1], vhi[pp][dt][0], vhi[pp][dt][1]};
-        oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb, oacc[dt]);
+        oacc[dt] = mfma16<DT>(a, pb, oacc[dt]);
       }
     }
   };
@@ -660,7 +662,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
             o4[e] = (p0 * f0 + p1 * f1) * inv;
           }
           const int d0 = dt * 32 + 8 * gq + 4 * half;
-          const u32x2_t w = {pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3])};
+          const u32x2_t w = {pack16x2<DT>(o4[0], o4[1]), pack16x2<DT>(o4[2], o4[3])};
           *(u32x2_t*)(orow + d0) = w;
         }
       }
@@ -718,7 +720,7 @@ __device__ __forceinline__ void dma_tile_2w(uint8_t* tile, __amdgpu_buffer_rsrc_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[7], 0, 3072, 0);
 }
 
-template <int D>
+template <int D, int DT>
 __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   constexpr int BS = 64;
@@ -774,12 +776,12 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   // Loads in the order their results are needed: mask bytes, Q, then the first K DMA.
   uint8_t mb = 0;
   if (lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
-  bf16x8_t qf[KSTEPS];
+  u32x4_t qf[KSTEPS];
   {
     // Rows past the end read row S-1: per-row results, never stored.
     const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : S - 1) * p.sq[2] + half * 8;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = as_bf16x8(*(const u32x4_t*)(qr + ks * 16));
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *(const u32x4_t*)(qr + ks * 16);
   }
   // Buffer resource of key block kb of K or V (rows >= S are out of range: zeros).
   auto block_rsrc = [&](const uint16_t* base, uint32_t rb, int64_t stride, int kb) {
@@ -818,8 +820,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
     f32x16_t s0 = (f32x16_t){}, s1 = (f32x16_t){};
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      s0 = mfma_32x32x16_bf16(as_bf16x8(kf[0][ks]), qf[ks], s0);
-      s1 = mfma_32x32x16_bf16(as_bf16x8(kf[1][ks]), qf[ks], s1);
+      s0 = mfma16<DT>(kf[0][ks], qf[ks], s0);
+      s1 = mfma16<DT>(kf[1][ks], qf[ks], s1);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's K reads returned
     block_barrier();                      // every wave has read K(kb): the K tile is free
@@ -873,14 +875,14 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
     l_run += lsum0 + lsum1;
     // P^T as the B operand of four 16-key k-steps: keys 16pp + 8*(j>>2) + 4*half + (j&3)
     // for element j, the same key order the V^T reads below use.
-    bf16x8_t pb[4];
+    u32x4_t pb[4];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       const f32x16_t& sv = (pp < 2) ? s0 : s1;
       const int o = 8 * (pp & 1);
-      const u32x4_t w = {pack_bf16x2(sv[o + 0], sv[o + 1]), pack_bf16x2(sv[o + 2], sv[o + 3]),
-                         pack_bf16x2(sv[o + 4], sv[o + 5]), pack_bf16x2(sv[o + 6], sv[o + 7])};
-      pb[pp] = as_bf16x8(w);
+      const u32x4_t w = {pack16x2<DT>(sv[o + 0], sv[o + 1]), pack16x2<DT>(sv[o + 2], sv[o + 3]),
+                         pack16x2<DT>(sv[o + 4], sv[o + 5]), pack16x2<DT>(sv[o + 6], sv[o + 7])};
+      pb[pp] = w;
     }
     __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8): own share of V(kb) landed, next K in flight
     block_barrier();                      // V(kb) visible
@@ -902,7 +904,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
 #pragma unroll
       for (int dt = 0; dt < DTILES; ++dt) {
         const u32x4_t a = {vlo[pp][dt][0], vlo[pp][dt][1], vhi[pp][dt][0], vhi[pp][dt][1]};
-        oacc[dt] = mfma_32x32x16_bf16(as_bf16x8(a), pb[pp], oacc[dt]);
+        oacc[dt] = mfma16<DT>(a, pb[pp], oacc[dt]);
       }
     kb = kb_next;
   }
@@ -917,8 +919,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         const int d0 = dt * 32 + 8 * gq + 4 * half;
-        const u32x2_t w = {pack_bf16x2(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
-                           pack_bf16x2(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
+        const u32x2_t w = {pack16x2<DT>(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
+                           pack16x2<DT>(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
         *(u32x2_t*)(orow + d0) = w;
       }
   }
@@ -946,7 +948,7 @@ static int resident_per_cu(K kernel, int threads) {
   return n;
 }
 
-template <int D>
+template <int D, int DT>
 static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t stream) {
   const int64_t total = (int64_t)p.NB * p.B * p.Hq;
   int64_t grid = total;
@@ -959,7 +961,7 @@ static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t s
   if (queue) {
     // Every resident workgroup slot filled once, a whole number per partition.
     p.parts = (((int64_t)p.B * p.Hkv) % 8 == 0) ? 8 : 1;
-    static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D>, threads);
+    static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D, DT>, threads);
     int64_t wg = std::min<int64_t>(total, (int64_t)per_cu * device_cus());
     wg = std::max<int64_t>(p.parts, wg / p.parts * p.parts);
     p.wg_per_part = (int)(wg / p.parts);
@@ -968,27 +970,33 @@ static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t s
     hipLaunchKernelGGL(bsfa_queue_reset_kernel, dim3(1), dim3(64), 0, stream, queue);
   }
   if constexpr (two_wave)
-    hipLaunchKernelGGL((bsfa_prefill_bs64_2w_kernel<D>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
+    hipLaunchKernelGGL((bsfa_prefill_bs64_2w_kernel<D, DT>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
   else
-    hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
+    hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D, DT>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
   return hipGetLastError();
 }
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+template <int DT>
+static hipError_t launch_prefill_any(const PrefillParams& p, int* queue, int64_t head_dim,
+                                     int64_t block_size, hipStream_t s) {
+  if (block_size == 64 && head_dim == 128) return launch_prefill_bs64<128, DT>(p, queue, s);
+  if (block_size == 64 && head_dim == 64) return launch_prefill_bs64<64, DT>(p, queue, s);
+  if (block_size == 32 && head_dim == 128) return launch_prefill<32, 128, DT>(p, s);
+  if (block_size == 32 && head_dim == 64) return launch_prefill<32, 64, DT>(p, s);
+  if (block_size == 128 && head_dim == 128) return launch_prefill<128, 128, DT>(p, s);
+  return launch_prefill<128, 64, DT>(p, s);
+}
 
 }  // namespace tasft
 
 using namespace tasft;
 
 static int dispatch_prefill(const PrefillParams& p, int* queue, int64_t head_dim,
-                            int64_t block_size, hipStream_t s, const char* what) {
-  hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_prefill_bs64<128>(p, queue, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_prefill_bs64<64>(p, queue, s);
-  else if (block_size == 32 && head_dim == 128) err = launch_prefill<32, 128>(p, s);
-  else if (block_size == 32 && head_dim == 64) err = launch_prefill<32, 64>(p, s);
-  else if (block_size == 128 && head_dim == 128) err = launch_prefill<128, 128>(p, s);
-  else err = launch_prefill<128, 64>(p, s);
+                            int64_t block_size, int dtype, hipStream_t s, const char* what) {
+  const hipError_t err = dtype == kF16 ? launch_prefill_any<kF16>(p, queue, head_dim, block_size, s)
+                                       : launch_prefill_any<kBf16>(p, queue, head_dim, block_size, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "%s: launch failed: %s", what, hipGetErrorString(err));
   return kOk;
@@ -1008,10 +1016,12 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
                                       const int64_t* q_strides, const int64_t* k_strides,
                                       const int64_t* v_strides, const int64_t* o_strides,
                                       const int64_t* mask_strides, float scale, int causal,
-                                      void* stream) {
+                                      int dtype, void* stream) {
   if (!q || !k || !v || !out || !block_mask || !q_strides || !k_strides || !v_strides ||
       !o_strides || !mask_strides)
     return set_error(kErrInvalidArgument, "prefill: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "prefill: dtype must be bf16 (0) or fp16 (1), got %d", dtype);
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0)
     return set_error(kErrInvalidArgument, "prefill: batch, heads and seq_len must be positive");
   if (num_q_heads % num_kv_heads != 0)
@@ -1075,7 +1085,7 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   p.wg_per_part = 1;
   p.cu_seqlens = nullptr;
   // Ticket counters of the persistent launch (block size 64).
-  return dispatch_prefill(p, (int*)workspace, head_dim, block_size, (hipStream_t)stream,
+  return dispatch_prefill(p, (int*)workspace, head_dim, block_size, dtype, (hipStream_t)stream,
                           "prefill");
 }
 
@@ -1088,10 +1098,13 @@ extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const
                                              const int64_t* k_strides, const int64_t* v_strides,
                                              const int64_t* o_strides,
                                              const int64_t* mask_strides, float scale, int causal,
-                                             void* stream) {
+                                             int dtype, void* stream) {
   if (!q || !k || !v || !out || !block_mask || !cu_seqlens || !q_strides || !k_strides ||
       !v_strides || !o_strides || !mask_strides)
     return set_error(kErrInvalidArgument, "prefill_varlen: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "prefill_varlen: dtype must be bf16 (0) or fp16 (1), got %d",
+                     dtype);
   if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_seqlen <= 0)
     return set_error(kErrInvalidArgument,
                      "prefill_varlen: num_seqs, heads and max_seqlen must be positive");
@@ -1151,6 +1164,6 @@ extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const
   p.wg_per_part = 1;
   p.cu_seqlens = cu_seqlens;
   // One workgroup per (sequence, head, query block); never the persistent loop.
-  return dispatch_prefill(p, nullptr, head_dim, block_size, (hipStream_t)stream,
+  return dispatch_prefill(p, nullptr, head_dim, block_size, dtype, (hipStream_t)stream,
                           "prefill_varlen");
 }

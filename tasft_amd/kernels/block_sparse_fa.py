@@ -82,6 +82,18 @@ def _kv_compatible(q: torch.Tensor, kv: torch.Tensor) -> bool:
     return bk == b and sk == s and dk == d and hk > 0 and hq % hk == 0
 
 
+def _kernel_dtype(**tensors: torch.Tensor) -> int:
+    """The C-ABI ``dtype`` code shared by the given tensors (bf16 or fp16, all the same, as the
+    reference's ``tl.dot`` needs, ``block_sparse_fa.py:228, 252``)."""
+    items = list(tensors.items())
+    first_name, first = items[0]
+    for name, t in items[1:]:
+        if t.dtype != first.dtype:
+            raise KernelError(f"{name} is {t.dtype} but {first_name} is {first.dtype}",
+                              context={"tensor": name, "dtype": str(t.dtype), "expected": str(first.dtype)})
+    return _native.dtype_code(first.dtype, "block-sparse attention")
+
+
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     """Return ``t`` if its layout suits the kernels (unit d stride, 16-byte rows), else a copy."""
     st = t.stride()
@@ -224,12 +236,8 @@ class BlockSparseFlashAttention:
                 f"HIP kernel supports head_dim in {sorted(_VALID_HEAD_DIMS)}, got {D}",
                 context={"head_dim": D, "supported": sorted(_VALID_HEAD_DIMS)},
             )
-        for name, t in (("q", q), ("k", k), ("v", v)):
-            if t.dtype != torch.bfloat16:
-                raise KernelError(
-                    f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
-                    context={"tensor": name, "dtype": str(t.dtype)},
-                )
+        dtype = _kernel_dtype(q=q, k=k, v=v)
+        for t in (k, v):
             if t.device != q.device:
                 raise KernelError("Q, K, V must be on the same device", context={"device": str(t.device)})
         lib = _native.load_library()
@@ -246,7 +254,7 @@ class BlockSparseFlashAttention:
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
             workspace.data_ptr(), ws_bytes, B, H, k.shape[1], S, D, self.block_size,
             _native.strides(q), _native.strides(k), _native.strides(v), _native.strides(out),
-            _native.strides(mask), scale, 1 if causal else 0, _native.stream_handle(q.device),
+            _native.strides(mask), scale, 1 if causal else 0, dtype, _native.stream_handle(q.device),
         )
         _native.check(status, "tasft_bsfa_prefill_fwd", {"shape": [B, H, S, D]})
         return out
@@ -282,7 +290,8 @@ class BlockSparseFlashAttention:
         semantics of ``forward`` per sequence. There is no low-sparsity dense fallback.
 
         Args:
-            q: ``[T, Hq, D]`` bf16 packed queries; k, v: ``[T, Hkv, D]`` bf16, ``Hq % Hkv == 0``.
+            q: ``[T, Hq, D]`` packed queries; k, v: ``[T, Hkv, D]``, ``Hq % Hkv == 0``; all
+                bf16 or all fp16.
             block_mask: ``[N, Hq, NB, NB]`` with ``NB = ceil(max_seqlen / block_size)``;
                 sequence n uses its leading ``ceil(len_n / block_size)`` square.
             cu_seqlens: ``[N + 1]`` int32 cumulative lengths (``cu_seqlens[0] == 0``,
@@ -348,12 +357,8 @@ class BlockSparseFlashAttention:
                 f"block_mask shape mismatch: expected {expected}, got {tuple(block_mask.shape)}",
                 context={"expected": list(expected), "got": list(block_mask.shape)},
             )
+        dtype = _kernel_dtype(q=q, k=k, v=v)
         for name, t in (("q", q), ("k", k), ("v", v)):
-            if t.dtype != torch.bfloat16:
-                raise KernelError(
-                    f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
-                    context={"tensor": name, "dtype": str(t.dtype)},
-                )
             if not t.is_cuda or t.device != q.device:
                 raise KernelError("Q, K, V must be on the same GPU device",
                                   context={"tensor": name, "device": str(t.device)})
@@ -368,7 +373,7 @@ class BlockSparseFlashAttention:
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
             cu_dev.data_ptr(), n_seq, H, k.shape[1], max_seqlen, D, self.block_size,
             _native.strides(q), _native.strides(k), _native.strides(v), _native.strides(out),
-            _native.strides(mask), 1.0 / math.sqrt(D), 1 if causal else 0,
+            _native.strides(mask), 1.0 / math.sqrt(D), 1 if causal else 0, dtype,
             _native.stream_handle(q.device),
         )
         _native.check(status, "tasft_bsfa_prefill_varlen_fwd",
@@ -390,8 +395,9 @@ class BlockSparseFlashAttention:
         """Block-sparse decode of one new token per sequence.
 
         Args:
-            q: ``[B, Hq, 1, D]`` bf16, the new token's queries.
-            k_cache, v_cache: ``[B, Hkv, S_kv, D]`` bf16; the new token's K/V are included.
+            q: ``[B, Hq, 1, D]``, the new token's queries (bf16 or fp16).
+            k_cache, v_cache: ``[B, Hkv, S_kv, D]`` of q's dtype; the new token's K/V are
+                included.
             block_mask: ``[B, Hq, 1, ceil(S_kv / block_size)]``; non-zero selects a block.
             block_indices: instead of ``block_mask``, ``[B, Hq, K]`` integer lists of the
                 selected block indices per head, ``-1`` marking empty slots (converted on
@@ -446,10 +452,7 @@ class BlockSparseFlashAttention:
                 f"HIP kernel supports head_dim in {sorted(_VALID_HEAD_DIMS)}, got {D}",
                 context={"head_dim": D},
             )
-        for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
-            if t.dtype != torch.bfloat16:
-                raise KernelError(f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
-                                  context={"tensor": name, "dtype": str(t.dtype)})
+        dtype = _kernel_dtype(q=q, k_cache=k_cache, v_cache=v_cache)
         lib = _native.load_library()
         if num_splits is None:
             num_splits = default_decode_splits(B, Hkv, nb)
@@ -471,7 +474,7 @@ class BlockSparseFlashAttention:
             _native.ptr(lens), workspace.data_ptr(), ws_bytes, B, H, Hkv, S_kv, D,
             self.block_size, num_splits,
             _native.strides(q), _native.strides(k_cache), _native.strides(v_cache),
-            _native.strides(out), _native.strides(mask), 1.0 / math.sqrt(D),
+            _native.strides(out), _native.strides(mask), 1.0 / math.sqrt(D), dtype,
             _native.stream_handle(q.device),
         )
         _native.check(status, "tasft_bsfa_decode_fwd", {"shape": [B, H, S_kv, D]})
@@ -498,8 +501,8 @@ class BlockSparseFlashAttention:
         equivalent contiguous cache.
 
         Args:
-            q: ``[B, Hq, 1, D]`` bf16.
-            k_pages, v_pages: ``[num_pages, page_size, Hkv, D]`` bf16 page pools; token t of
+            q: ``[B, Hq, 1, D]`` (bf16 or fp16).
+            k_pages, v_pages: ``[num_pages, page_size, Hkv, D]`` page pools of q's dtype; token t of
                 sequence b is row ``t % page_size`` of page ``block_table[b, t // page_size]``.
             block_table: ``[B, max_pages]`` int32 on the device; only the pages holding a
                 token below ``kv_lens[b]`` are read. An entry outside
@@ -549,10 +552,8 @@ class BlockSparseFlashAttention:
             raise KernelError("Pass exactly one of block_mask and block_indices",
                               context={"block_mask": block_mask is not None,
                                        "block_indices": block_indices is not None})
+        dtype = _kernel_dtype(q=q, k_pages=k_pages, v_pages=v_pages)
         for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages)):
-            if t.dtype != torch.bfloat16:
-                raise KernelError(f"HIP kernel computes in bfloat16; {name} is {t.dtype}",
-                                  context={"tensor": name, "dtype": str(t.dtype)})
             if not t.is_cuda or t.device != q.device:
                 raise KernelError("Tensors must be on one CUDA device",
                                   context={"tensor": name, "device": str(t.device)})
@@ -586,7 +587,7 @@ class BlockSparseFlashAttention:
             table.data_ptr(), lens.data_ptr(), workspace.data_ptr(), ws_bytes, B, H, Hkv, S_kv, D,
             self.block_size, page_size, k_pages.shape[0], num_splits,
             _native.strides(q), _native.strides(k_pages), _native.strides(v_pages),
-            _native.strides(out), _native.strides(mask), table.stride(0), 1.0 / math.sqrt(D),
+            _native.strides(out), _native.strides(mask), table.stride(0), 1.0 / math.sqrt(D), dtype,
             _native.stream_handle(q.device),
         )
         _native.check(status, "tasft_bsfa_decode_paged_fwd", {"shape": [B, H, S_kv, D],

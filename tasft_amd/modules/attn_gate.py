@@ -5,7 +5,7 @@ same constructor and defaults, the same parameters and state-dict keys
 (``gate_proj_in.weight/.bias``, ``gate_proj_out.weight``) created and initialised in the
 same order, the same validation order and messages, and the same ``GateOutput`` fields.
 
-Inference on bf16 GPU tensors (no autograd) runs the fused HIP kernels of
+Inference on bf16 or fp16 GPU tensors (no autograd) runs the fused HIP kernels of
 ``libtasft_amd.so``: one pass over Q and K for the pooling (GQA-native, K pooled per KV
 head) and one pairwise kernel that keeps logits, sigmoid and threshold in fp32 — gate
 scores cluster within ~1e-3 of 0.5, below one bf16 ulp, so the reference's bf16 cast of
@@ -13,13 +13,13 @@ the gate would move mask bits. Those ``soft_scores`` are fp32 whatever the modul
 and ``sparsity_ratio`` is read from a device counter on first access instead of a sync
 inside ``forward``.
 
-Everything else the reference gate accepts — CPU tensors, fp16 or fp32 Q/K, and calls that
-need gradients (gate training) — evaluates the reference formula itself with torch
-operations in the promoted dtype of the inputs and parameters, returning ``soft_scores`` in
-that dtype as the reference does. It uses ``W_in . cat(x, y) = W_q x + W_k y`` (the exact
+Gate training on those tensors runs the same forward and a HIP backward. Everything else
+the reference gate accepts — CPU tensors, fp32 Q/K, and gradients of the logits —
+evaluates the reference formula itself with torch operations in the promoted dtype of the
+inputs and parameters, returning ``soft_scores`` in that dtype as the reference does. It uses ``W_in . cat(x, y) = W_q x + W_k y`` (the exact
 algebra of ``attn_gate.py:250-257``) so no ``[B,H,NB,NB,2D]`` tensor is built. This is the
 gate's own formulation on the devices and dtypes the kernel does not serve, not a second
-backend of the HIP path: a bf16 GPU call without autograd never takes it, and fails with
+backend of the HIP path: a bf16 or fp16 GPU call never takes it, and fails with
 ``KernelError`` if the library is missing.
 
 Additive, keyword-compatible extensions: ``k`` may have ``Hkv`` heads (``Hq % Hkv == 0``);
@@ -226,10 +226,11 @@ class AttnGate(nn.Module):
         return self._forward_torch(q, k, tau, return_logits, force_diagonal)
 
     def _kernel_applies(self, q: torch.Tensor, k: torch.Tensor) -> bool:
-        """The HIP kernels serve bf16 GPU tensors (head_dim a multiple of 8, at most 256):
-        inference, and training through the HIP backward; every other call (CPU, fp16 or
-        fp32 inputs, or gradients of the logits) evaluates the formula with torch."""
-        return (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
+        """The HIP kernels serve bf16 or fp16 GPU tensors (Q and K of one dtype, head_dim a
+        multiple of 8, at most 256): inference, and training through the HIP backward; every
+        other call (CPU, fp32 inputs, or gradients of the logits) evaluates the formula with
+        torch."""
+        return (q.is_cuda and q.dtype in _native.KERNEL_DTYPES and k.dtype == q.dtype
                 and q.shape[-1] % 8 == 0 and q.shape[-1] <= 256)
 
     def _thresholds(self, tau: float | torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -410,7 +411,8 @@ def _launch_gate(gate: AttnGate, q: torch.Tensor, k: torch.Tensor, taus: torch.T
         taus.data_ptr(), soft.data_ptr(), _native.ptr(logits), mask.data_ptr(), active.data_ptr(),
         _native.ptr(qm), _native.ptr(km), workspace.data_ptr(), ws_bytes, B, H, Hkv, S, D,
         gate.block_size, hidden, _native.strides(q), _native.strides(k),
-        (1 if gate.is_causal else 0) | (2 if force_diagonal else 0), _native.stream_handle(dev),
+        (1 if gate.is_causal else 0) | (2 if force_diagonal else 0),
+        _native.dtype_code(q.dtype, "tasft_gate_fwd"), _native.stream_handle(dev),
     )
     _native.check(status, "tasft_gate_fwd", {"shape": [B, H, S, D]})
     return {"soft": soft, "mask": mask, "logits": logits, "active": active, "nb": nb,

@@ -8,7 +8,7 @@ Two entry points:
   ``max_pool2d``, softmax over the flat block grid.
 * ``gate_target_from_qk(q, k, ...)`` is the MI355X kernel path: it takes Q and K and never
   forms the score tensor. The HIP kernel computes each 64x64 block maximum of
-  ``Q K^T * scale`` with bf16 MFMA (causal: -inf above the diagonal; plus the caller's
+  ``Q K^T * scale`` with bf16 or fp16 MFMA (causal: -inf above the diagonal; plus the caller's
   additive ``attention_mask``), then normalises. It replaces the score producer
   ``tasft/modules/tasft_attention.py:426-458`` followed by ``compute_gate_target``;
   ``normalize="row"`` gives the per-row variant and ``temperature``/``clamp`` the variant
@@ -106,7 +106,8 @@ def gate_target_from_qk(
     clamp: float | None = None,
     attention_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Gate target ``[B, Hq, NB, NB]`` fp32 from ``q [B,Hq,S,D]`` and ``k [B,Hkv,S,D]`` (bf16).
+    """Gate target ``[B, Hq, NB, NB]`` fp32 from ``q [B,Hq,S,D]`` and ``k [B,Hkv,S,D]`` (both
+    bf16 or both fp16).
 
     Args:
         block_size: pooling block (32, 64 or 128).
@@ -130,9 +131,9 @@ def gate_target_from_qk(
         raise KernelError("q and k shapes are incompatible", context={"q": list(q.shape), "k": list(k.shape)})
     if not q.is_cuda or not k.is_cuda:
         raise KernelError("Tensors must be on CUDA device", context={"device": str(q.device)})
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
-        raise KernelError("gate target kernel computes in bfloat16",
-                          context={"q": str(q.dtype), "k": str(k.dtype)})
+    if k.dtype != q.dtype:
+        raise KernelError("q and k must have one dtype", context={"q": str(q.dtype), "k": str(k.dtype)})
+    dtype = _native.dtype_code(q.dtype, "gate target kernel")
     if normalize not in _NORMALIZE:
         raise ValueError(f"normalize must be one of {sorted(_NORMALIZE)}, got {normalize!r}")
     if not temperature > 0.0:
@@ -150,7 +151,7 @@ def gate_target_from_qk(
         q.data_ptr(), k.data_ptr(), _native.ptr(mask_buf), out.data_ptr(), B, H, k.shape[1], S, D,
         block_size, _native.strides(q), _native.strides(k), mask_strides, sc, 1 if causal else 0,
         _NORMALIZE[normalize], float(temperature), float(clamp) if clamp is not None else 0.0,
-        _native.stream_handle(q.device),
+        dtype, _native.stream_handle(q.device),
     )
     _native.check(status, "tasft_gate_target_fwd", {"shape": [B, H, S, D]})
     return out
@@ -231,7 +232,7 @@ def gate_loss_from_qk(
     ``[B, H, S, S]`` score tensor the reference's score producer stores
     (``tasft/modules/tasft_attention.py:426-458``).
 
-    The target comes from ``gate_target_from_qk`` (bf16 MFMA block maxima, flat softmax) and
+    The target comes from ``gate_target_from_qk`` (MFMA block maxima, flat softmax) and
     is a constant of the loss, as the reference's detached scores are; the KL and its
     gradient with respect to ``gate_soft_scores`` come from one HIP kernel, so
     ``loss.backward()`` reaches the gate (and, through ``AttnGate``'s HIP backward, its

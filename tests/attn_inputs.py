@@ -38,8 +38,9 @@ def _randn(shape, g, kind):
     return x / math.sqrt(128) if kind == "base" else x
 
 
-def qkv(kind: str, q_shape, kv_shape, seed: int, bs: int, seq_axis: int = 2):
-    """bf16 CPU tensors q, k, v; ``seq_axis`` is the token axis of K (for ``peaky``)."""
+def qkv(kind: str, q_shape, kv_shape, seed: int, bs: int, seq_axis: int = 2,
+        dtype: torch.dtype = torch.bfloat16):
+    """CPU tensors q, k, v of ``dtype``; ``seq_axis`` is the token axis of K (for ``peaky``)."""
     if kind not in KINDS:
         raise ValueError(kind)
     g = torch.Generator().manual_seed(seed)
@@ -52,11 +53,11 @@ def qkv(kind: str, q_shape, kv_shape, seed: int, bs: int, seq_axis: int = 2):
         view = [1] * len(kv_shape)
         view[seq_axis] = n
         k = k * f.view(view)
-    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
 
 
 def packed_qkv(kind: str, lens: list[int], hq: int, hkv: int, d: int, seed: int, bs: int,
-               pad: int = 5):
+               pad: int = 5, dtype: torch.dtype = torch.bfloat16):
     """Packed ``q [T, Hq, D]``, ``k/v [T, Hkv, D]`` (T = sum(lens) + pad) and cu_seqlens.
 
     For ``peaky`` the key factor follows each token's position within its own sequence.
@@ -74,7 +75,7 @@ def packed_qkv(kind: str, lens: list[int], hq: int, hkv: int, d: int, seed: int,
         for n0, n1 in zip(cu[:-1], cu[1:]):
             pos[n0:n1] = torch.arange(n1 - n0)
         k = k * key_block_factor(pos, bs).view(t, 1, 1)
-    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), cu
+    return q.to(dtype), k.to(dtype), v.to(dtype), cu
 
 
 def random_mask(shape, density: float, seed: int) -> torch.Tensor:
@@ -123,39 +124,45 @@ PAGED_CASES = [
 ]
 
 
-def prefill_case_inputs(case, kind: str):
+# fp16 runs of the same kernels: one case per prefill kernel variant and block size, and
+# decode with one and several splits, with GQA and without.
+F16_PREFILL_CASES = [PREFILL_CASES[i] for i in (0, 2, 3, 4, 5)]
+F16_DECODE_CASES = [DECODE_CASES[i] for i in (0, 1, 4, 5)]
+
+
+def prefill_case_inputs(case, kind: str, dtype: torch.dtype = torch.bfloat16):
     """Inputs of one prefill case: ``q, k, v, mask`` (CPU)."""
     B, Hq, Hkv, S, D, bs, causal, density, _variant = case
     seed = 9100 + S + 7 * Hq + D + bs + KINDS.index(kind)
-    q, k, v = qkv(kind, (B, Hq, S, D), (B, Hkv, S, D), seed, bs)
+    q, k, v = qkv(kind, (B, Hq, S, D), (B, Hkv, S, D), seed, bs, dtype=dtype)
     nb = math.ceil(S / bs)
     mask = random_mask((B, Hq, nb, nb), density, seed + 1)
     return q, k, v, mask
 
 
-def varlen_case_inputs(case, kind: str):
+def varlen_case_inputs(case, kind: str, dtype: torch.dtype = torch.bfloat16):
     """Inputs of one varlen case: ``q, k, v, cu, mask`` (CPU)."""
     lens, Hq, Hkv, D, bs, causal, density = case
     seed = 9300 + sum(lens) + D + bs + KINDS.index(kind)
-    q, k, v, cu = packed_qkv(kind, lens, Hq, Hkv, D, seed, bs)
+    q, k, v, cu = packed_qkv(kind, lens, Hq, Hkv, D, seed, bs, dtype=dtype)
     nb = math.ceil(max(lens) / bs)
     mask = random_mask((len(lens), Hq, nb, nb), density, seed + 1)
     return q, k, v, cu, mask
 
 
-def decode_case_inputs(case, kind: str):
+def decode_case_inputs(case, kind: str, dtype: torch.dtype = torch.bfloat16):
     """Inputs of one decode case: ``q, k_cache, v_cache, mask`` (CPU); head (0, 0) selects
     nothing (its output must be exactly 0)."""
     B, Hq, Hkv, S, D, bs, density, _splits = case
     seed = 9500 + S + Hq + D + bs + KINDS.index(kind)
-    q, k, v = qkv(kind, (B, Hq, 1, D), (B, Hkv, S, D), seed, bs)
+    q, k, v = qkv(kind, (B, Hq, 1, D), (B, Hkv, S, D), seed, bs, dtype=dtype)
     nb = math.ceil(S / bs)
     mask = random_mask((B, Hq, 1, nb), density, seed + 1)
     mask[0, 0] = False
     return q, k, v, mask
 
 
-def paged_case_inputs(case, kind: str):
+def paged_case_inputs(case, kind: str, dtype: torch.dtype = torch.bfloat16):
     """Inputs of one paged-decode case.
 
     Returns ``q, k, v`` (contiguous caches ``[B, Hkv, cap, D]``), ``k_pages, v_pages``
@@ -167,7 +174,7 @@ def paged_case_inputs(case, kind: str):
     seed = 9700 + S + ps + D + KINDS.index(kind)
     per = (S + ps - 1) // ps
     cap = per * ps
-    q, k, v = qkv(kind, (B, Hq, 1, D), (B, Hkv, cap, D), seed, bs)
+    q, k, v = qkv(kind, (B, Hq, 1, D), (B, Hkv, cap, D), seed, bs, dtype=dtype)
     g = torch.Generator().manual_seed(seed + 1)
     lens = torch.randint(1, S + 1, (B,), generator=g, dtype=torch.int32)
     lens[0] = S
@@ -177,8 +184,8 @@ def paged_case_inputs(case, kind: str):
     n_pages = B * per + 7
     perm = torch.randperm(n_pages, generator=g)
     table = perm[: B * per].view(B, per).to(torch.int32)
-    kp = torch.randn(n_pages, ps, Hkv, D, generator=g).to(torch.bfloat16)
-    vp = torch.randn(n_pages, ps, Hkv, D, generator=g).to(torch.bfloat16)
+    kp = torch.randn(n_pages, ps, Hkv, D, generator=g).to(dtype)
+    vp = torch.randn(n_pages, ps, Hkv, D, generator=g).to(dtype)
     for b in range(B):
         for j in range(per):
             kp[table[b, j]] = k[b, :, j * ps:(j + 1) * ps].transpose(0, 1)

@@ -14,6 +14,19 @@ REL_TOL = 2e-2
 # Floor of the relative bound (outputs that are all exactly zero).
 _REL_FLOOR = 1e-6
 
+# The same bar for fp16 kernels, four times tighter: fp16 keeps 11 significant bits to
+# bf16's 8, so rounding P and the output costs about an eighth of the bf16 error.
+F16_MAX_ABS_TOL = 5e-3
+F16_MEAN_ABS_TOL = 5e-4
+F16_REL_TOL = 5e-3
+
+
+def bar(dtype: torch.dtype) -> dict[str, float]:
+    """Keyword arguments of ``parity_failure`` / ``assert_close_bf16`` for a kernel dtype."""
+    if dtype == torch.float16:
+        return {"max_abs": F16_MAX_ABS_TOL, "mean_abs": F16_MEAN_ABS_TOL, "rel": F16_REL_TOL}
+    return {"max_abs": MAX_ABS_TOL, "mean_abs": MEAN_ABS_TOL, "rel": REL_TOL}
+
 
 def to_np(t: torch.Tensor) -> np.ndarray:
     """Float32 numpy copy of a (possibly bf16, possibly device) tensor."""
@@ -64,6 +77,11 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
     return u.astype(np.uint32).view(np.float32)
+
+
+def round_f16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest fp16 (ties to even), returned as float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
 def require_gpu() -> torch.device:

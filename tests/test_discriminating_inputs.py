@@ -11,6 +11,8 @@ the same bar the GPU tests apply (``helpers.parity_failure``):
 * a bf16 emulation of the kernel arithmetic (P rounded to bf16 before PV, output rounded
   to bf16) must PASS it, so the bar is reachable.
 
+The fp16 cases repeat this with fp16 inputs, the fp16 emulation and the tighter fp16 bar.
+
 A further check shows that the benchmark-scale inputs (``base``) alone could not make
 that distinction, which is why both kinds are tested.
 """
@@ -20,38 +22,40 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 import attn_inputs as ai
-from helpers import parity_failure, round_bf16, to_np
+from helpers import bar, parity_failure, round_bf16, round_f16, to_np
 from oracle import tasft_oracle as orc
 
 DISC_KINDS = ("unit", "peaky")
 
 
-def _emul_rows(qrows, keys, vals, allowed, scale):
-    """bf16 emulation of one head: rows of q against ``keys`` under ``allowed``."""
+def _emul_rows(qrows, keys, vals, allowed, scale, rnd=round_bf16):
+    """Emulation of one head: rows of q against ``keys`` under ``allowed``, P and the
+    output rounded by ``rnd`` (bf16 or fp16)."""
     sco = (qrows @ keys.T) * np.float32(scale)
     sco = np.where(allowed, sco, -np.inf)
     mx = sco.max(axis=-1, keepdims=True)
     has = np.isfinite(mx)
     p = np.exp(sco - np.where(has, mx, 0.0)).astype(np.float32)
     l = p.sum(axis=-1, keepdims=True)
-    o = round_bf16(p) @ vals
-    return round_bf16(np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0).astype(np.float32))
+    o = rnd(p) @ vals
+    return rnd(np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0).astype(np.float32))
 
 
-def _emul_prefill(q, k, v, mask, bs, causal):
+def _emul_prefill(q, k, v, mask, bs, causal, rnd=round_bf16):
     b_, hq, s, d = q.shape
     g = hq // k.shape[1]
     out = np.zeros(q.shape, dtype=np.float32)
     for b in range(b_):
         for h in range(hq):
             tm = orc.token_mask(mask[b, h], s, bs, causal)
-            out[b, h] = _emul_rows(q[b, h], k[b, h // g], v[b, h // g], tm, 1.0 / math.sqrt(d))
+            out[b, h] = _emul_rows(q[b, h], k[b, h // g], v[b, h // g], tm, 1.0 / math.sqrt(d), rnd)
     return out
 
 
-def _emul_decode(q, kc, vc, mask, bs, kv_lens=None):
+def _emul_decode(q, kc, vc, mask, bs, kv_lens=None, rnd=round_bf16):
     b_, hq, _, d = q.shape
     g = hq // kc.shape[1]
     s = kc.shape[2]
@@ -61,7 +65,7 @@ def _emul_decode(q, kc, vc, mask, bs, kv_lens=None):
         for h in range(hq):
             tok = np.repeat(mask[b, h, 0].astype(bool), bs)[:s] & (np.arange(s) < n)
             out[b, h, 0] = _emul_rows(q[b, h, :1], kc[b, h // g], vc[b, h // g], tok[None, :],
-                                      1.0 / math.sqrt(d))[0]
+                                      1.0 / math.sqrt(d), rnd)[0]
     return out
 
 
@@ -74,13 +78,14 @@ def _swap_row_pairs(q):
     return q[..., idx, :]
 
 
-def _check(what, ref, uniform, double, emul, swapped=None):
-    assert parity_failure(uniform, ref) is not None, f"{what}: uniform weights pass the bar"
-    assert parity_failure(double, ref) is not None, f"{what}: twice the scale passes the bar"
+def _check(what, ref, uniform, double, emul, swapped=None, dtype=torch.bfloat16):
+    kw = bar(dtype)
+    assert parity_failure(uniform, ref, **kw) is not None, f"{what}: uniform weights pass the bar"
+    assert parity_failure(double, ref, **kw) is not None, f"{what}: twice the scale passes the bar"
     if swapped is not None:
-        assert parity_failure(swapped, ref) is not None, f"{what}: swapped query rows pass the bar"
-    fail = parity_failure(emul, ref)
-    assert fail is None, f"{what}: bf16 emulation fails the bar: {fail}"
+        assert parity_failure(swapped, ref, **kw) is not None, f"{what}: swapped query rows pass the bar"
+    fail = parity_failure(emul, ref, **kw)
+    assert fail is None, f"{what}: {dtype} emulation fails the bar: {fail}"
 
 
 @pytest.mark.parametrize("kind", DISC_KINDS)
@@ -146,6 +151,36 @@ def test_paged_cases_discriminate(case, kind):
            orc.sparse_decode_paged(qn, kpn, vpn, tn, ln, m, bs, scale=0.0),
            orc.sparse_decode_paged(qn, kpn, vpn, tn, ln, m, bs, scale=2 * sc),
            _emul_decode(qn, to_np(k), to_np(v), m, bs, kv_lens=ln))
+
+
+@pytest.mark.parametrize("kind", DISC_KINDS)
+@pytest.mark.parametrize("case", ai.F16_PREFILL_CASES, ids=ai.case_id)
+def test_f16_prefill_cases_discriminate(case, kind):
+    """fp16 inputs: the fp16 emulation meets the fp16 bar, the broken stand-ins do not."""
+    _B, _Hq, _Hkv, _S, D, bs, causal, _dens, _var = case
+    qt, kt, vt, mask = ai.prefill_case_inputs(case, kind, torch.float16)
+    q, k, v, m = to_np(qt), to_np(kt), to_np(vt), mask.numpy()
+    sc = 1.0 / math.sqrt(D)
+    ref = orc.attention_block_gather(q, k, v, m, bs, causal)
+    _check(f"fp16 prefill {case} {kind}", ref,
+           orc.attention_block_gather(q, k, v, m, bs, causal, scale=0.0),
+           orc.attention_block_gather(q, k, v, m, bs, causal, scale=2 * sc),
+           _emul_prefill(q, k, v, m, bs, causal, round_f16),
+           orc.attention_block_gather(_swap_row_pairs(q), k, v, m, bs, causal), torch.float16)
+
+
+@pytest.mark.parametrize("kind", DISC_KINDS)
+@pytest.mark.parametrize("case", ai.F16_DECODE_CASES, ids=ai.case_id)
+def test_f16_decode_cases_discriminate(case, kind):
+    D, bs = case[4], case[5]
+    q, kc, vc, mask = ai.decode_case_inputs(case, kind, torch.float16)
+    qn, kn, vn, m = to_np(q), to_np(kc), to_np(vc), mask.numpy()
+    sc = 1.0 / math.sqrt(D)
+    ref = orc.sparse_decode(qn, kn, vn, m, bs)
+    _check(f"fp16 decode {case} {kind}", ref,
+           orc.sparse_decode(qn, kn, vn, m, bs, scale=0.0),
+           orc.sparse_decode(qn, kn, vn, m, bs, scale=2 * sc),
+           _emul_decode(qn, kn, vn, m, bs, rnd=round_f16), dtype=torch.float16)
 
 
 def test_peaky_inputs_move_the_running_maximum():

@@ -149,9 +149,10 @@ def test_config2_gate_full_size_sampled_heads():
     assert np.array_equal(hard[decisive], hard_ref[decisive])
 
 
-def test_fp32_and_fp16_inputs_run_the_reference_formula():
-    """fp32/fp16 Q/K on the GPU evaluate the reference formula in their dtype (the HIP
-    kernel reads bf16); fp32 agrees with the kernel on the same values."""
+def test_fp32_inputs_run_the_reference_formula_and_fp16_the_kernel():
+    """fp32 Q/K on the GPU evaluate the reference formula in fp32 and agree with the kernel on
+    the same values; fp16 Q/K (the same values, exact in fp16 apart from a rare tiny one in
+    fp16's subnormal range) run the kernel's fp16 instantiation and give the same logits."""
     dev = require_gpu()
     gate = _gate(8, 128, 64, 64).to(dev).requires_grad_(False)
     q = wl.randn_bf16((1, 8, 700, 128), 41, scale=1.0).to(dev)
@@ -159,8 +160,8 @@ def test_fp32_and_fp16_inputs_run_the_reference_formula():
     with torch.no_grad():
         hip = gate(q, k, return_logits=True)
         f32 = gate(q.float(), k.float(), return_logits=True)
-        f16 = gate.half()(q.half(), k.half(), return_logits=True)
+        f16 = gate(q.half(), k.half(), return_logits=True)
     torch.cuda.synchronize()
-    assert f32.soft_scores.dtype == torch.float32 and f16.soft_scores.dtype == torch.float16
+    assert f32.soft_scores.dtype == torch.float32 and f16.soft_scores.dtype == torch.float32
     torch.testing.assert_close(f32.logits, hip.logits, rtol=1e-4, atol=1e-5)
-    torch.testing.assert_close(f16.logits.float(), hip.logits, rtol=2e-2, atol=2e-3)
+    torch.testing.assert_close(f16.logits, hip.logits, rtol=1e-5, atol=1e-6)

@@ -207,7 +207,7 @@ def _prefill_capi(q, k, v, mask, bs, causal, workspace=None):
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), m8.data_ptr(), ws_ptr, ws_bytes,
         B, Hq, k.shape[1], S, D, bs, _native.strides(q), _native.strides(k), _native.strides(v),
         _native.strides(out), _native.strides(m8), ctypes.c_float(1.0 / math.sqrt(D)),
-        1 if causal else 0, _native.stream_handle(q.device))
+        1 if causal else 0, _native.dtype_code(q.dtype, "prefill"), _native.stream_handle(q.device))
     _native.check(rc, "tasft_bsfa_prefill_fwd")
     torch.cuda.synchronize()
     return out

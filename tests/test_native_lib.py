@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace_sizes():
     lib = _native.load_library()
-    assert lib.tasft_abi_version() == 6
+    assert lib.tasft_abi_version() == 7
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 8192, 64) == 256
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 0, 64) == 0
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
@@ -53,20 +53,20 @@ def test_invalid_arguments_return_errors_without_launch():
     lib = _native.load_library()
     st = _i64([0, 0, 0, 1])
     rc = lib.tasft_bsfa_prefill_fwd(None, None, None, None, None, None, 0, 1, 32, 8, 128, 128, 64,
-                                    st, st, st, st, st, 1.0, 1, None)
+                                    st, st, st, st, st, 1.0, 1, 0, None)
     assert rc == -1 and b"null pointer" in lib.tasft_last_error()
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, None, 0, 1, 32, 8, 128, 96, 64,
-                                    st, st, st, st, st, 1.0, 1, None)
+                                    st, st, st, st, st, 1.0, 1, 0, None)
     assert rc == -2 and b"head_dim" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, None, 0, 1, 30, 8, 128, 128, 64,
-                                    st, st, st, st, st, 1.0, 1, None)
+                                    st, st, st, st, st, 1.0, 1, 0, None)
     assert rc == -1 and b"multiple" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_prefill_fwd(fake, fake, fake, fake, fake, fake, 16, 1, 32, 8, 128, 128, 64,
-                                    st, st, st, st, st, 1.0, 1, None)
+                                    st, st, st, st, st, 1.0, 1, 0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_fwd(fake, fake, fake, fake, fake, None, fake, 0, 1, 32, 8, 1024, 128,
-                                   64, 4, st, st, st, st, st, 1.0, None)
+                                   64, 4, st, st, st, st, st, 1.0, 0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
     rc = lib.tasft_mask_compact(fake, 1, 1, 4, 4, st, 0, fake, fake, 16, fake, 0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
@@ -74,26 +74,60 @@ def test_invalid_arguments_return_errors_without_launch():
     assert rc == -1 and b"invalid sizes" in lib.tasft_last_error()
     st3 = _i64([0, 0, 1])
     rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, None, 2, 32, 8, 128, 128,
-                                           64, st3, st3, st3, st3, st, 1.0, 1, None)
+                                           64, st3, st3, st3, st3, st, 1.0, 1, 0, None)
     assert rc == -1 and b"null pointer" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128,
-                                           48, st3, st3, st3, st3, st, 1.0, 1, None)
+                                           48, st3, st3, st3, st3, st, 1.0, 1, 0, None)
     assert rc == -2 and b"block_size" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128,
-                                           64, _i64([8, 8, 2]), st3, st3, st3, st, 1.0, 1, None)
+                                           64, _i64([8, 8, 2]), st3, st3, st3, st, 1.0, 1, 0, None)
     assert rc == -1 and b"contiguous" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 128, 16, 100, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 128, 16, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
     assert rc == -2 and b"block_size" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 64, 12, 100, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 64, 12, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
     assert rc == -2 and b"page_size" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 64, 16, 100, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 64, 16, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
     assert rc == -4 and b"workspace" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 1 << 20, 1, 32,
-                                         8, 1024, 128, 64, 16, 0, 4, st, st, st, st, st, 64, 1.0, None)
+                                         8, 1024, 128, 64, 16, 0, 4, st, st, st, st, st, 64, 1.0, 0, None)
     assert rc == -1 and b"positive" in lib.tasft_last_error()
+
+
+def test_dtype_codes_other_than_bf16_and_fp16_are_rejected():
+    lib = _native.load_library()
+    st = _i64([0, 0, 0, 1])
+    st3 = _i64([0, 0, 1])
+    fake = ctypes.c_void_p(16)
+    calls = {
+        "prefill": lambda dt: lib.tasft_bsfa_prefill_fwd(
+            fake, fake, fake, fake, fake, None, 0, 1, 32, 8, 128, 128, 64, st, st, st, st, st, 1.0, 1,
+            dt, None),
+        "prefill_varlen": lambda dt: lib.tasft_bsfa_prefill_varlen_fwd(
+            fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128, 64, st3, st3, st3, st3, st, 1.0,
+            1, dt, None),
+        "decode": lambda dt: lib.tasft_bsfa_decode_fwd(
+            fake, fake, fake, fake, fake, None, fake, 1 << 20, 1, 32, 8, 1024, 128, 64, 4, st, st, st,
+            st, st, 1.0, dt, None),
+        "decode_noalloc": lambda dt: lib.tasft_bsfa_decode_fwd_noalloc(
+            fake, fake, fake, fake, fake, None, 1, 32, 8, 1024, 128, 64, 4, st, st, st, st, st, 1.0,
+            dt, None),
+        "decode_paged": lambda dt: lib.tasft_bsfa_decode_paged_fwd(
+            fake, fake, fake, fake, fake, fake, fake, fake, 1 << 20, 1, 32, 8, 1024, 128, 64, 16, 100,
+            4, st, st, st, st, st, 64, 1.0, dt, None),
+        "gate": lambda dt: lib.tasft_gate_fwd(
+            fake, fake, fake, fake, fake, fake, fake, None, fake, fake, None, None, fake, 1 << 20, 1,
+            32, 8, 1024, 128, 64, 128, st, st, 1, dt, None),
+        "gate_target": lambda dt: lib.tasft_gate_target_fwd(
+            fake, fake, None, fake, 1, 32, 8, 1024, 128, 64, st, st, None, 1.0, 1, 0, 1.0, 0.0, dt,
+            None),
+    }
+    for name, call in calls.items():
+        for dt in (2, -1):
+            rc = call(dt)
+            assert rc == -2 and b"dtype" in lib.tasft_last_error(), name
 
 
 def test_check_raises_kernel_error_with_message():
@@ -101,6 +135,6 @@ def test_check_raises_kernel_error_with_message():
     lib = _native.load_library()
     st = _i64([0, 0, 0, 1])
     rc = lib.tasft_gate_target_fwd(None, None, None, None, 1, 1, 1, 64, 128, 64, st, st, None, 1.0, 1, 0,
-                                   1.0, 0.0, None)
+                                   1.0, 0.0, 0, None)
     with pytest.raises(KernelError, match="null pointer"):
         _native.check(rc, "tasft_gate_target_fwd")

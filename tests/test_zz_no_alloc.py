@@ -27,7 +27,8 @@ def _args(q, kc, vc, out, mask, lens, splits, bs):
             _native.ptr(lens)), (B, Hq, kc.shape[1], kc.shape[2], D, bs, splits,
                                  _native.strides(q), _native.strides(kc), _native.strides(vc),
                                  _native.strides(out), _native.strides(mask),
-                                 ctypes.c_float(1.0 / math.sqrt(D)), _native.stream_handle(q.device))
+                                 ctypes.c_float(1.0 / math.sqrt(D)),
+                                 _native.dtype_code(q.dtype, "decode"), _native.stream_handle(q.device))
 
 
 def _decode_both(case, kind, dev):
