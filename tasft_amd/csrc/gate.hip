@@ -218,35 +218,61 @@ gate_pool_proj64_kernel(const GatePoolParams p) {
     for (int e = tid; e < nblk * D; e += 256) mdst[e] = red[0][e / D][e % D];
   }
 
-  // u[blk][c] = sum_d mean[blk][d] * W_in[c][off + d] (+ b_in[c] for query rows). Thread t
-  // takes unit c0 + t % 128 of blocks 8 * (t / 128) .. +7; the mean reads are broadcasts.
-  constexpr int HB = kFusePB / 2;
+  // u[blk][c] = sum_d mean[blk][d] * W_in[c][off + d] (+ b_in[c] for query rows) on the
+  // fp32 MFMA (v_mfma_f32_16x16x4_f32): M = the kFusePB = 16 blocks, N = 16 hidden units per
+  // tile (tiles dealt to the four waves in turn), K = D. The reduction index is permuted so
+  // that each lane reads contiguous runs: k-step s of lane group q = lane / 16 covers
+  // d = q * D/4 + s (A and B use the same order). Lane l then holds A[l % 16][.] = the means
+  // of block l % 16 and B[.][l % 16] = W_in row c0 + l % 16, and receives D[4q + r][l % 16]
+  // for r = 0..3. The 16 W_in rows of a tile are first copied to a per-wave LDS area with
+  // whole-line loads (two rows per instruction), since the operand order itself would touch
+  // 64 cache lines per load.
+  static_assert(kFusePB == 16, "one 16-row MFMA tile of blocks");
+  constexpr int KQ = D / 4;      // k-steps per lane group
+  constexpr int WCH = D / 4;     // 16-byte chunks per staged row
+  static_assert(4 * 16 * D <= 4 * kFusePB * D, "W staging fits the pooling LDS");
+  const int lane = tid % kWave, lr = lane % 16, lq = lane / 16;
+  float a[KQ];
+#pragma unroll
+  for (int s4 = 0; s4 < KQ; s4 += 4) {
+    const f32x4_t m4 = *(const f32x4_t*)&red[0][lr][lq * KQ + s4];
+    a[s4] = m4[0], a[s4 + 1] = m4[1], a[s4 + 2] = m4[2], a[s4 + 3] = m4[3];
+  }
+  __syncthreads();  // every wave holds its means: the LDS is free for W staging
+  // This wave's staging area: 16 rows x D floats, 16-byte chunk k of row r at position
+  // k ^ (r & 7) (conflict-free operand reads).
+  float* wst = &red[0][0][0] + wave * 16 * D;
   const int off = is_q ? 0 : D;
   float* dst = (is_q ? p.uq : p.uk) + (bh * p.NB + blk0) * (int64_t)p.hidden;
-  const int bsel = (tid / 128) * HB, cl = tid % 128;
-  for (int c0 = 0; c0 < p.hidden; c0 += 128) {
-    const int c = c0 + cl;
-    if (c >= p.hidden) continue;
-    const float* w = p.w_in + (int64_t)c * 2 * D + off;
-    float acc[HB];
+  const int ntiles = (p.hidden + 15) / 16;
+  for (int nt = wave; nt < ntiles; nt += 4) {
+    // Copy rows nt*16 .. +15 (rows past hidden read row 0; their results are not stored).
 #pragma unroll
-    for (int k = 0; k < HB; ++k) acc[k] = 0.f;
-#pragma unroll 4
-    for (int d = 0; d < D; d += 4) {
-      const f32x4_t wv = *(const f32x4_t*)(w + d);
+    for (int i = 0; i < (16 * WCH) / kWave; ++i) {
+      const int e = i * kWave + lane, r = e / WCH, k = e % WCH;
+      const int row = nt * 16 + r < p.hidden ? nt * 16 + r : 0;
+      const f32x4_t v = *(const f32x4_t*)(p.w_in + (int64_t)row * 2 * D + off + 4 * k);
+      *(f32x4_t*)(wst + r * D + 4 * (k ^ (r & 7))) = v;
+    }
+    const int c = nt * 16 + lr;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < HB; ++k) {
-        const f32x4_t m4 = *(const f32x4_t*)&red[0][bsel + k][d];
-        acc[k] = fmaf(m4[0], wv[0], acc[k]);
-        acc[k] = fmaf(m4[1], wv[1], acc[k]);
-        acc[k] = fmaf(m4[2], wv[2], acc[k]);
-        acc[k] = fmaf(m4[3], wv[3], acc[k]);
+    for (int s4 = 0; s4 < KQ; s4 += 4) {
+      const int k = (lq * KQ + s4) / 4;
+      const f32x4_t w4 = *(const f32x4_t*)(wst + lr * D + 4 * (k ^ (lr & 7)));
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4], w4[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4 + 1], w4[1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4 + 2], w4[2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4 + 3], w4[3], acc, 0, 0, 0);
+    }
+    if (c < p.hidden) {
+      const float bias = is_q ? p.b_in[c] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int blk = 4 * lq + r;
+        if (blk < nblk) dst[(int64_t)blk * p.hidden + c] = acc[r] + bias;
       }
     }
-    const float bias = is_q ? p.b_in[c] : 0.f;
-#pragma unroll
-    for (int k = 0; k < HB; ++k)
-      if (bsel + k < nblk) dst[(int64_t)(bsel + k) * p.hidden + c] = acc[k] + bias;
   }
 }
 
