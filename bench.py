@@ -39,7 +39,7 @@ FLOP_PER_BLOCK = 4 * 64 * 64 * 128  # QK^T + PV of one 64x64 tile at D=128
 # 673.2 MB algorithmic bytes (Q + K + V + O + mask) this is 1.71x: between launches the gate
 # streams 335 MB of Q and K, and K/V blocks are fetched again by the rows of a KV group
 # (4 MB of K/V per group against a 4 MB L2 per XCD).
-PREFILL_TRAFFIC_BYTES = 429130 * 1024 * 2.0 + 266429 * 1024
+PREFILL_TRAFFIC_BYTES = 430297 * 1024 * 2.0 + 266257 * 1024
 
 
 def log(msg: str) -> None:
@@ -415,7 +415,7 @@ def main() -> int:
             "block": res["shape"].block, "gate_hidden": 128, "target_causal_sparsity": 0.8,
         },
         "roofline": {
-            "kernel": "bsfa_prefill_bs64_2w_kernel<128>",
+            "kernel": "bsfa_prefill_bs64_2w_kernel<128, 0>",
             "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": round(PREFILL_TRAFFIC_BYTES),
