@@ -204,6 +204,38 @@ def bench_decode(torch, dev, steps, warmup):
             "decode_paged_ms": ms_paged, "decode_paged_hbm_gbps": total / (ms_paged * 1e-3) / 1e9}
 
 
+def bench_decode_qwen(torch, dev, steps, warmup):
+    """Decode with seven query heads per KV head (Qwen-2.5-7B: 28/4 heads, the kernel built
+    for up to eight heads) at the config-3 batch, cache length and selection density."""
+    from tasft_amd import workloads as wl
+    from tasft_amd.kernels import BlockSparseFlashAttention
+
+    shape = wl.Shape(64, 28, 4, 32768)
+    gen = torch.Generator(device=dev).manual_seed(1023)
+    scale = 1.0 / math.sqrt(shape.head_dim)
+    kv_shape = (shape.batch, shape.kv_heads, shape.seq, shape.head_dim)
+    kc = (torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16) * scale)
+    vc = (torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16) * scale)
+    q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1023).to(dev)
+    mask = wl.decode_mask(shape, 51, 2023).to(dev)
+    bsfa = BlockSparseFlashAttention(block_size=shape.block, min_sparsity_for_speedup=0.0)
+    for _ in range(warmup):
+        bsfa.forward_decode(q, kc, vc, mask)
+    torch.cuda.synchronize()
+    t = LaunchTimer(torch)
+    with _Span(t):
+        for _ in range(steps):
+            bsfa.forward_decode(q, kc, vc, mask)
+    torch.cuda.synchronize()
+    ms = t.total_ms() / steps
+    grp = shape.q_heads // shape.kv_heads
+    union = mask[:, :, 0, :].reshape(shape.batch, shape.kv_heads, grp, -1).any(dim=2)
+    total = int(union.sum().item()) * shape.block * shape.head_dim * 2 * 2 + q.numel() * 2 * 2 + mask.numel()
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"ms": ms, "gbps": total / (ms * 1e-3) / 1e9}
+
+
 def bench_qwen(torch, dev, steps, warmup):
     from tasft_amd import workloads as wl
     from tasft_amd.kernels import BlockSparseFlashAttention, executed_blocks
@@ -380,6 +412,9 @@ def main() -> int:
                       "decode_bytes": d["decode_bytes"],
                       "decode_paged16_ms": round(d["decode_paged_ms"], 4),
                       "decode_paged16_hbm_gbps": round(d["decode_paged_hbm_gbps"], 1)})
+        dq = bench_decode_qwen(torch, dev, max(10, args.steps), max(20, args.warmup))
+        extra.update({"decode_qwen_ms": round(dq["ms"], 4), "decode_qwen_hbm_gbps": round(dq["gbps"], 1),
+                      "decode_qwen_hbm_frac": round(dq["gbps"] / PEAK_HBM_GBPS, 4)})
     if "qwen" in extras:
         log("bench: config 4 Qwen prefill")
         qw = bench_qwen(torch, dev, max(5, args.steps // 2), max(10, args.warmup // 4))

@@ -79,9 +79,12 @@ __device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int voff
 
 // SUB keys (<= 64) of one KV block are processed at a time; a block of BS keys is
 // BS/SUB sub-blocks. MG >= G is the head count the loops are unrolled for (padding heads
-// carry zero probability).
+// carry zero probability). Up to four heads run two waves per SIMD (at most 256
+// registers each, two workgroups per CU). Five to eight heads need more than that: built
+// for two waves per SIMD they spilled about 120 bytes per lane to scratch inside the
+// block loop, so they run one wave per SIMD (up to 512 registers, one workgroup per CU).
 template <int BS, int D, int MG, bool PAGED, int DT>
-__global__ void __launch_bounds__(kDecodeWaves * kWave, 2)
+__global__ void __launch_bounds__(kDecodeWaves * kWave, MG == 8 ? 1 : 2)
 bsfa_decode_split_kernel(const DecodeParams p) {
   static_assert(!PAGED || BS <= 64, "paged caches use the one-sub-block path");
   constexpr int SUB = BS < 64 ? BS : 64;

@@ -455,7 +455,7 @@ class BlockSparseFlashAttention:
         dtype = _kernel_dtype(q=q, k_cache=k_cache, v_cache=v_cache)
         lib = _native.load_library()
         if num_splits is None:
-            num_splits = default_decode_splits(B, Hkv, nb)
+            num_splits = default_decode_splits(B, Hkv, nb, H // Hkv)
         q = q.contiguous()
         k_cache = _kernel_ready(k_cache)
         v_cache = _kernel_ready(v_cache)
@@ -571,7 +571,7 @@ class BlockSparseFlashAttention:
             )
         lib = _native.load_library()
         if num_splits is None:
-            num_splits = default_decode_splits(B, Hkv, nb)
+            num_splits = default_decode_splits(B, Hkv, nb, H // Hkv)
         q = q.contiguous()
         k_pages = _kernel_ready(k_pages)
         v_pages = _kernel_ready(v_pages)
@@ -672,13 +672,16 @@ def mask_to_csr(block_mask: torch.Tensor, causal: bool = False) -> tuple[torch.T
     return row_ptr, col_idx[:nnz]
 
 
-def default_decode_splits(batch: int, num_kv_heads: int, num_blocks: int) -> int:
-    """Split-K factor giving about 512 decode workgroups: every workgroup is resident at
-    once (2 per CU on 256 CUs), each streams as many blocks as possible per prologue, and
-    one split per row needs no combine pass. At least the number of splits that keeps
-    every split within 1024 key blocks."""
+def default_decode_splits(batch: int, num_kv_heads: int, num_blocks: int,
+                          q_per_kv: int = 1) -> int:
+    """Split-K factor filling the GPU's resident decode workgroups once: 512 (2 per CU on
+    256 CUs) for up to four query heads per KV head, 256 (one per CU: that kernel runs one
+    wave per SIMD) for five to eight. Each workgroup then streams as many blocks as
+    possible per prologue, and one split per row needs no combine pass. At least the
+    number of splits that keeps every split within 1024 key blocks."""
     groups = max(1, batch * num_kv_heads)
-    want = min(max(1, num_blocks // 4), math.ceil(512 / groups))
+    resident = 256 if q_per_kv > 4 else 512
+    want = min(max(1, num_blocks // 4), math.ceil(resident / groups))
     return int(max(1, want, math.ceil(num_blocks / 1024)))
 
 

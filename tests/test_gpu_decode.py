@@ -147,6 +147,33 @@ def test_config3_full_size_default_splits():
         del kd, vd
 
 
+def test_qwen_geometry_full_size_default_splits():
+    """Seven query heads per KV head (Qwen-2.5-7B: 28/4 heads), the kernel built for up to
+    eight heads with one wave per SIMD, at the config-3 batch and cache (B=64, S_kv=32768,
+    51 of 512 blocks per KV head): the default is one split per (b, KV head), 256
+    workgroups, direct writes. Unit-scale Q/K/V drawn on the device; sampled (b, h) pairs,
+    including the last head of a group, against the oracle."""
+    dev = require_gpu()
+    shape = wl.Shape(64, 28, 4, 32768)
+    nb = shape.nb
+    assert default_decode_splits(shape.batch, shape.kv_heads, nb, 7) == 1
+    gen = torch.Generator(device=dev).manual_seed(1023)
+    kv_shape = (shape.batch, shape.kv_heads, shape.seq, shape.head_dim)
+    kc = torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(kv_shape, generator=gen, device=dev, dtype=torch.bfloat16)
+    mask = wl.decode_mask(shape, 51, 2023)
+    q = wl.randn_bf16((shape.batch, shape.q_heads, 1, shape.head_dim), 1033, scale=1.0)
+    print("qwen decode geometry B=64 28/4", flush=True)
+    out = _decode(q.to(dev), kc, vc, mask.to(dev), shape.block).cpu()
+    assert torch.isfinite(out.float()).all()
+    for b, h in [(0, 0), (9, 6), (33, 13), (63, 27)]:
+        kvh = h // 7
+        ref = orc.sparse_decode(to_np(q[b:b + 1, h:h + 1]), to_np(kc[b:b + 1, kvh:kvh + 1]),
+                                to_np(vc[b:b + 1, kvh:kvh + 1]), mask[b:b + 1, h:h + 1].numpy(),
+                                shape.block)
+        assert_close_bf16(out[b:b + 1, h:h + 1], ref, f"qwen decode ({b},{h})")
+
+
 # ----------------------------------------------------------------------------- paged cache
 PAGED_CASES = [
     # B, Hq, Hkv, S, D, bs, page_size, splits

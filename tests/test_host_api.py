@@ -308,6 +308,22 @@ class TestGateTargetDense:
             TASFTObjective.compute_gate_target(torch.randn(1, 1, 4, 4), block_size=0)
 
 
+# ----------------------------------------------------------------------------- decode splits
+def test_default_decode_splits_fill_the_resident_workgroups_once():
+    from tasft_amd.kernels import default_decode_splits
+
+    # Up to four query heads per KV head: 512 resident workgroups (two per CU).
+    assert default_decode_splits(64, 8, 512) == 1          # config 3
+    assert default_decode_splits(64, 4, 512, 4) == 2
+    assert default_decode_splits(4, 8, 64) == 16
+    # Five to eight heads: one workgroup per CU, 256 resident.
+    assert default_decode_splits(64, 4, 512, 7) == 1       # Qwen-2.5-7B at config-3 batch
+    assert default_decode_splits(4, 8, 64, 8) == 8
+    # Never fewer splits than keep each within 1024 key blocks, never more than blocks // 4.
+    assert default_decode_splits(64, 8, 5000) == 5
+    assert default_decode_splits(1, 1, 8, 7) == 2
+
+
 # ----------------------------------------------------------------------------- varlen validation
 def _varlen_args(T=40, H=4, Hkv=2, D=64):
     q = torch.zeros(T, H, D, dtype=torch.bfloat16)
