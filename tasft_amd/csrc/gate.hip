@@ -304,6 +304,10 @@ struct GatePairParams {
 // threshold with coalesced stores.
 constexpr int kPairTile = 32;
 constexpr int kPairLd = kPairTile + 4;
+// Row r of staged unit cc sits at position r ^ 4 * ((cc / 8) % 8) of its LDS row: the eight
+// threads that stage one tile row write units eight apart, which the swizzle spreads over
+// different banks; runs of four rows (r % 4 == 0) stay contiguous and 16-byte aligned.
+__device__ __forceinline__ int pair_swz(int cc, int r) { return r ^ (4 * ((cc >> 3) & 7)); }
 
 __global__ void __launch_bounds__(256)
 gate_pairwise_kernel(const GatePairParams p) {
@@ -359,8 +363,9 @@ gate_pairwise_kernel(const GatePairParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float w = p.w_out[c0 + su + u + e];
-            uq_t[(su + u + e) * kPairLd + sr] = a[e];
-            uk_t[(su + u + e) * kPairLd + sr] = c[e];
+            const int cc = su + u + e;
+            uq_t[cc * kPairLd + pair_swz(cc, sr)] = a[e];
+            uk_t[cc * kPairLd + pair_swz(cc, sr)] = c[e];
             a_part = fmaf(w, a[e], a_part);
             b_part = fmaf(w, c[e], b_part);
           }
@@ -372,8 +377,8 @@ gate_pairwise_kernel(const GatePairParams p) {
           const float a = (cc < hc && i < p.NBq) ? qrow[cc] : 0.f;
           const float c = (cc < hc && j < p.NBk) ? krow[cc] : 0.f;
           const float w = cc < hc ? p.w_out[c0 + cc] : 0.f;
-          uq_t[cc * kPairLd + sr] = a;
-          uk_t[cc * kPairLd + sr] = c;
+          uq_t[cc * kPairLd + pair_swz(cc, sr)] = a;
+          uk_t[cc * kPairLd + pair_swz(cc, sr)] = c;
           a_part = fmaf(w, a, a_part);
           b_part = fmaf(w, c, b_part);
         }
@@ -386,8 +391,8 @@ gate_pairwise_kernel(const GatePairParams p) {
 #pragma unroll 8
       for (int u = 0; u < nu; ++u) {
         const int cc = 4 * u + wave;
-        const f32x4_t av = *(const f32x4_t*)&uq_t[cc * kPairLd + 4 * tr];
-        const f32x4_t bv = *(const f32x4_t*)&uk_t[cc * kPairLd + 4 * tc];
+        const f32x4_t av = *(const f32x4_t*)&uq_t[cc * kPairLd + pair_swz(cc, 4 * tr)];
+        const f32x4_t bv = *(const f32x4_t*)&uk_t[cc * kPairLd + pair_swz(cc, 4 * tc)];
         const float w = wo[cc];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
