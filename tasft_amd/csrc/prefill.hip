@@ -957,22 +957,22 @@ static hipError_t launch_prefill_bs64(PrefillParams p, int* queue, hipStream_t s
   // four-wave one, persistent when the caller passes a workspace.
   constexpr bool two_wave = D == 128;
   constexpr int threads = two_wave ? 128 : 256;
-  if (two_wave) queue = nullptr;
-  if (queue) {
-    // Every resident workgroup slot filled once, a whole number per partition.
-    p.parts = (((int64_t)p.B * p.Hkv) % 8 == 0) ? 8 : 1;
-    static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D, DT>, threads);
-    int64_t wg = std::min<int64_t>(total, (int64_t)per_cu * device_cus());
-    wg = std::max<int64_t>(p.parts, wg / p.parts * p.parts);
-    p.wg_per_part = (int)(wg / p.parts);
-    p.queue = queue;
-    grid = wg;
-    hipLaunchKernelGGL(bsfa_queue_reset_kernel, dim3(1), dim3(64), 0, stream, queue);
-  }
-  if constexpr (two_wave)
+  if constexpr (two_wave) {
     hipLaunchKernelGGL((bsfa_prefill_bs64_2w_kernel<D, DT>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
-  else
+  } else {
+    if (queue) {
+      // Every resident workgroup slot filled once, a whole number per partition.
+      p.parts = (((int64_t)p.B * p.Hkv) % 8 == 0) ? 8 : 1;
+      static const int per_cu = resident_per_cu(bsfa_prefill_bs64_kernel<D, DT>, threads);
+      int64_t wg = std::min<int64_t>(total, (int64_t)per_cu * device_cus());
+      wg = std::max<int64_t>(p.parts, wg / p.parts * p.parts);
+      p.wg_per_part = (int)(wg / p.parts);
+      p.queue = queue;
+      grid = wg;
+      hipLaunchKernelGGL(bsfa_queue_reset_kernel, dim3(1), dim3(64), 0, stream, queue);
+    }
     hipLaunchKernelGGL((bsfa_prefill_bs64_kernel<D, DT>), dim3((unsigned)grid), dim3(threads), 0, stream, p);
+  }
   return hipGetLastError();
 }
 
