@@ -8,7 +8,8 @@
  * (raw words) of the type named by the call's `dtype` argument: TASFT_DTYPE_BF16 or
  * TASFT_DTYPE_F16 (scores, softmax and accumulation are fp32 either way); other tensors
  * are as stated. Each 4-D tensor is described by element strides for its dims
- * (b, h, s, d) and the d stride must be 1. Return value: 0 on success, a negative
+ * (b, h, s, d); the d stride must be 1 and no stride may be negative (a negative one is
+ * rejected with TASFT_ERR_INVALID_ARGUMENT). Return value: 0 on success, a negative
  * status on error, with the message available from tasft_last_error() on the
  * calling thread.
  *

@@ -36,6 +36,14 @@ enum Status : int {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// True if none of the n element strides is negative: the kernels index forward from each
+// tensor's base pointer.
+inline bool strides_nonneg(const int64_t* s, int n) {
+  for (int i = 0; i < n; ++i)
+    if (s[i] < 0) return false;
+  return true;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }

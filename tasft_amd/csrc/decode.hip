@@ -672,6 +672,10 @@ static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, v
   if (workspace_bytes < need)
     return set_error(kErrWorkspace, "decode: workspace too small: need %zu bytes, got %zu", need,
                      workspace_bytes);
+  if (!strides_nonneg(q_strides, 4) || !strides_nonneg(k_strides, 4) ||
+      !strides_nonneg(v_strides, 4) || !strides_nonneg(o_strides, 4) ||
+      !strides_nonneg(mask_strides, 4))
+    return set_error(kErrInvalidArgument, "decode: strides must be non-negative");
   if (q_strides[3] != 1 || k_strides[3] != 1 || v_strides[3] != 1 || o_strides[3] != 1)
     return set_error(kErrInvalidArgument, "decode: head_dim must be the contiguous dimension");
   for (int j = 0; j < 3; ++j)
@@ -851,6 +855,10 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
     return set_error(kErrWorkspace, "decode_paged: workspace too small: need %zu bytes, got %zu",
                      need, workspace_bytes);
   // q, out [B, Hq, 1, D]; K/V pools [pages, page_size, Hkv, D].
+  if (!strides_nonneg(q_strides, 4) || !strides_nonneg(k_strides, 4) ||
+      !strides_nonneg(v_strides, 4) || !strides_nonneg(o_strides, 4) ||
+      !strides_nonneg(mask_strides, 4) || block_table_stride < 0)
+    return set_error(kErrInvalidArgument, "decode_paged: strides must be non-negative");
   if (q_strides[3] != 1 || k_strides[3] != 1 || v_strides[3] != 1 || o_strides[3] != 1)
     return set_error(kErrInvalidArgument, "decode_paged: head_dim must be the contiguous dimension");
   for (int j = 0; j < 3; ++j)

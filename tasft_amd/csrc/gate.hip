@@ -649,6 +649,8 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   if (head_dim % 8 != 0 || head_dim > kGateMaxD || head_dim <= 0)
     return set_error(kErrUnsupported, "gate: head_dim must be a multiple of 8 and at most %d, got %lld",
                      kGateMaxD, (long long)head_dim);
+  if (!strides_nonneg(q_strides, 4) || !strides_nonneg(k_strides, 4))
+    return set_error(kErrInvalidArgument, "gate: strides must be non-negative");
   if (q_strides[3] != 1 || k_strides[3] != 1)
     return set_error(kErrInvalidArgument, "gate: head_dim must be the contiguous dimension");
   for (int j = 0; j < 3; ++j)

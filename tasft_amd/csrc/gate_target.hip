@@ -505,6 +505,8 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
   if (!(temperature > 0.f))
     return set_error(kErrInvalidArgument, "gate_target: temperature must be > 0");
   const int64_t* st[2] = {q_strides, k_strides};
+  if (!strides_nonneg(q_strides, 4) || !strides_nonneg(k_strides, 4))
+    return set_error(kErrInvalidArgument, "gate_target: strides must be non-negative");
   for (int i = 0; i < 2; ++i) {
     if (st[i][3] != 1)
       return set_error(kErrInvalidArgument, "gate_target: head_dim must be the contiguous dimension");

@@ -163,6 +163,8 @@ extern "C" int tasft_mask_compact(const uint8_t* block_mask, int64_t batch, int6
     return set_error(kErrInvalidArgument, "mask_compact: null pointer argument");
   if (batch <= 0 || num_heads <= 0 || num_q_blocks <= 0 || num_k_blocks <= 0 || col_capacity < 0)
     return set_error(kErrInvalidArgument, "mask_compact: sizes must be positive");
+  if (!strides_nonneg(mask_strides, 4))
+    return set_error(kErrInvalidArgument, "mask_compact: strides must be non-negative");
   const int64_t rows = batch * num_heads * num_q_blocks;
   if (rows * num_k_blocks > 0x7fffffffLL || num_k_blocks > 0x7fffffffLL)
     return set_error(kErrUnsupported, "mask_compact: more than 2^31 mask entries");

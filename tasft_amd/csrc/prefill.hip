@@ -1035,6 +1035,10 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
     return set_error(kErrUnsupported, "prefill: block_size must be 32, 64 or 128, got %lld",
                      (long long)block_size);
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  if (!strides_nonneg(q_strides, 4) || !strides_nonneg(k_strides, 4) ||
+      !strides_nonneg(v_strides, 4) || !strides_nonneg(o_strides, 4) ||
+      !strides_nonneg(mask_strides, 4))
+    return set_error(kErrInvalidArgument, "prefill: strides must be non-negative");
   for (int i = 0; i < 4; ++i) {
     if (st[i][3] != 1)
       return set_error(kErrInvalidArgument, "prefill: head_dim must be the contiguous dimension");
@@ -1119,6 +1123,10 @@ extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const
     return set_error(kErrUnsupported, "prefill_varlen: block_size must be 32, 64 or 128, got %lld",
                      (long long)block_size);
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  if (!strides_nonneg(q_strides, 3) || !strides_nonneg(k_strides, 3) ||
+      !strides_nonneg(v_strides, 3) || !strides_nonneg(o_strides, 3) ||
+      !strides_nonneg(mask_strides, 4))
+    return set_error(kErrInvalidArgument, "prefill_varlen: strides must be non-negative");
   for (int i = 0; i < 4; ++i) {
     if (st[i][2] != 1)
       return set_error(kErrInvalidArgument,

@@ -130,6 +130,43 @@ def test_dtype_codes_other_than_bf16_and_fp16_are_rejected():
             assert rc == -2 and b"dtype" in lib.tasft_last_error(), name
 
 
+def test_negative_strides_are_rejected_before_any_launch():
+    """Every strided entry point refuses a negative stride (the kernels index forward from
+    each tensor's base pointer) with an argument error, without touching the GPU."""
+    lib = _native.load_library()
+    st, neg = _i64([0, 0, 0, 1]), _i64([-8, 0, 0, 1])
+    st3, neg3 = _i64([0, 0, 1]), _i64([-8, 0, 1])
+    fake = ctypes.c_void_p(16)
+    calls = {
+        "prefill": lambda s4, s3, m: lib.tasft_bsfa_prefill_fwd(
+            fake, fake, fake, fake, fake, None, 0, 1, 32, 8, 128, 128, 64, s4, st, st, st, m, 1.0,
+            1, 0, None),
+        "prefill_varlen": lambda s4, s3, m: lib.tasft_bsfa_prefill_varlen_fwd(
+            fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128, 64, st3, s3, st3, st3, m, 1.0,
+            1, 0, None),
+        "decode": lambda s4, s3, m: lib.tasft_bsfa_decode_fwd(
+            fake, fake, fake, fake, fake, None, fake, 1 << 20, 1, 32, 8, 1024, 128, 64, 4, st, s4,
+            st, st, m, 1.0, 0, None),
+        "decode_paged": lambda s4, s3, m: lib.tasft_bsfa_decode_paged_fwd(
+            fake, fake, fake, fake, fake, fake, fake, fake, 1 << 20, 1, 32, 8, 1024, 128, 64, 16,
+            100, 4, st, st, s4, st, m, 64, 1.0, 0, None),
+        "gate": lambda s4, s3, m: lib.tasft_gate_fwd(
+            fake, fake, fake, fake, fake, fake, fake, None, fake, fake, None, None, fake, 1 << 20, 1,
+            32, 8, 1024, 128, 64, 128, st, s4, 1, 0, None),
+        "gate_target": lambda s4, s3, m: lib.tasft_gate_target_fwd(
+            fake, fake, None, fake, 1, 32, 8, 1024, 128, 64, s4, st, None, 1.0, 1, 0, 1.0, 0.0, 0,
+            None),
+    }
+    for name, call in calls.items():
+        rc = call(neg, neg3, st)
+        assert rc == -1 and b"non-negative" in lib.tasft_last_error(), name
+    for name in ("prefill", "prefill_varlen", "decode", "decode_paged"):
+        rc = calls[name](st, st3, neg)  # the mask strides
+        assert rc == -1 and b"non-negative" in lib.tasft_last_error(), name
+    rc = lib.tasft_mask_compact(fake, 1, 2, 4, 4, neg, 1, fake, fake, 16, fake, 1 << 20, None)
+    assert rc == -1 and b"non-negative" in lib.tasft_last_error()
+
+
 def test_check_raises_kernel_error_with_message():
     from tasft_amd.exceptions import KernelError
     lib = _native.load_library()
