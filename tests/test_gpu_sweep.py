@@ -1,0 +1,186 @@
+"""Seeded sweep over valid shapes: every attention kernel family and the gate against the
+oracle on configurations drawn at random from the supported sets (batch, query and KV head
+counts, ragged lengths, head dim, block size, causal or not, mask density, bf16 or fp16,
+unit-scale or peaky scores). The draws are fixed by the case seed, so the sweep is the same
+on every run; each case prints its configuration before its launch.
+
+The hand-picked cases of the other GPU tests pin the kernel variants one by one; this sweep
+covers their combinations (e.g. fp16 with block 32 and GQA 7, a partial last block with a
+non-causal mask, several splits over a ragged cache) under the same parity bars.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import attn_inputs as ai
+from helpers import assert_close_bf16, bar, require_gpu, to_np
+from oracle import tasft_oracle as orc
+from tasft_amd.kernels import BlockSparseFlashAttention
+from tasft_amd.modules import AttnGate
+
+pytestmark = pytest.mark.gpu
+
+N_PREFILL = 24
+N_VARLEN = 8
+N_DECODE = 16
+N_PAGED = 8
+N_GATE = 10
+
+
+def _rng(kind: str, i: int) -> np.random.Generator:
+    return np.random.default_rng([20261202, ["prefill", "varlen", "decode", "paged", "gate"].index(kind), i])
+
+
+def _heads(rng) -> tuple[int, int]:
+    g = int(rng.choice([1, 2, 4, 7]))
+    hkv = 1 if g == 7 else int(rng.choice([1, 2]))
+    return g * hkv, hkv
+
+
+def _dtype(rng) -> torch.dtype:
+    return torch.float16 if rng.random() < 0.35 else torch.bfloat16
+
+
+@pytest.mark.parametrize("i", range(N_PREFILL))
+def test_prefill_sweep(i):
+    dev = require_gpu()
+    rng = _rng("prefill", i)
+    hq, hkv = _heads(rng)
+    b = int(rng.integers(1, 3))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64, 128]))
+    s = int(rng.integers(1, 600))
+    causal = bool(rng.random() < 0.7)
+    density = float(rng.uniform(0.1, 0.9))
+    dtype = _dtype(rng)
+    kind = str(rng.choice(["unit", "peaky"]))
+    print(f"prefill sweep {i}: B={b} Hq={hq} Hkv={hkv} S={s} D={d} bs={bs} causal={causal} "
+          f"density={density:.2f} {dtype} {kind}", flush=True)
+    seed = 31000 + i
+    q, k, v = ai.qkv(kind, (b, hq, s, d), (b, hkv, s, d), seed, bs, dtype=dtype)
+    nb = math.ceil(s / bs)
+    mask = ai.random_mask((b, hq, nb, nb), density, seed + 1)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), causal=causal)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype
+    ref = orc.attention_block_gather(to_np(q), to_np(k), to_np(v), mask.numpy(), bs, causal)
+    assert_close_bf16(out, ref, f"prefill sweep {i}", **bar(dtype))
+
+
+@pytest.mark.parametrize("i", range(N_VARLEN))
+def test_varlen_sweep(i):
+    dev = require_gpu()
+    rng = _rng("varlen", i)
+    hq, hkv = _heads(rng)
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64, 128]))
+    lens = [int(x) for x in rng.integers(0, 400, size=int(rng.integers(2, 5)))]
+    lens[0] = max(lens[0], 1)
+    causal = bool(rng.random() < 0.7)
+    density = float(rng.uniform(0.2, 0.9))
+    dtype = _dtype(rng)
+    print(f"varlen sweep {i}: lens={lens} Hq={hq} Hkv={hkv} D={d} bs={bs} causal={causal} "
+          f"density={density:.2f} {dtype}", flush=True)
+    seed = 32000 + i
+    q, k, v, cu = ai.packed_qkv("peaky", lens, hq, hkv, d, seed, bs, dtype=dtype)
+    nb = math.ceil(max(lens) / bs)
+    mask = ai.random_mask((len(lens), hq, nb, nb), density, seed + 1)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward_varlen(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                              torch.tensor(cu, dtype=torch.int32), causal=causal)
+    torch.cuda.synchronize()
+    ref = orc.attention_varlen(to_np(q), to_np(k), to_np(v), cu, mask.numpy(), bs, causal)
+    # Padding tokens after the last sequence are outside every sequence: not compared.
+    t = cu[-1]
+    assert_close_bf16(to_np(out)[:t], ref[:t], f"varlen sweep {i}", **bar(dtype))
+
+
+@pytest.mark.parametrize("i", range(N_DECODE))
+def test_decode_sweep(i):
+    dev = require_gpu()
+    rng = _rng("decode", i)
+    hq, hkv = _heads(rng)
+    b = int(rng.integers(1, 5))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64, 128]))
+    s = int(rng.integers(1, 2000))
+    nb = math.ceil(s / bs)
+    splits = None if rng.random() < 0.5 else int(rng.integers(1, 5))
+    density = float(rng.uniform(0.05, 0.8))
+    dtype = _dtype(rng)
+    kind = str(rng.choice(["unit", "peaky"]))
+    print(f"decode sweep {i}: B={b} Hq={hq} Hkv={hkv} S={s} D={d} bs={bs} splits={splits} "
+          f"density={density:.2f} {dtype} {kind}", flush=True)
+    seed = 33000 + i
+    q, kc, vc = ai.qkv(kind, (b, hq, 1, d), (b, hkv, s, d), seed, bs, dtype=dtype)
+    mask = ai.random_mask((b, hq, 1, nb), density, seed + 1)
+    lens = torch.from_numpy(rng.integers(1, s + 1, size=b)).to(torch.int32)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward_decode(q.to(dev), kc.to(dev), vc.to(dev), mask.to(dev), kv_lens=lens,
+                              num_splits=splits)
+    torch.cuda.synchronize()
+    ref = orc.sparse_decode(to_np(q), to_np(kc), to_np(vc), mask.numpy(), bs, kv_lens=lens.numpy())
+    assert_close_bf16(out, ref, f"decode sweep {i}", **bar(dtype))
+
+
+@pytest.mark.parametrize("i", range(N_PAGED))
+def test_paged_decode_sweep(i):
+    dev = require_gpu()
+    rng = _rng("paged", i)
+    hq, hkv = _heads(rng)
+    b = int(rng.integers(1, 4))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64]))
+    ps = int(rng.choice([16, 32, 64]))
+    s = int(rng.integers(1, 1200))
+    splits = None if rng.random() < 0.5 else int(rng.integers(1, 4))
+    dtype = _dtype(rng)
+    print(f"paged sweep {i}: B={b} Hq={hq} Hkv={hkv} S={s} D={d} bs={bs} page={ps} "
+          f"splits={splits} {dtype}", flush=True)
+    q, _k, _v, kp, vp, table, lens, mask = ai.paged_case_inputs(
+        (b, hq, hkv, s, d, bs, ps, splits), "peaky", dtype)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    out = bsfa.forward_decode_paged(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lens.to(dev),
+                                    mask.to(dev), num_splits=splits)
+    torch.cuda.synchronize()
+    ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),
+                                  mask.numpy(), bs)
+    assert_close_bf16(out, ref, f"paged sweep {i}", **bar(dtype))
+
+
+@pytest.mark.parametrize("i", range(N_GATE))
+def test_gate_sweep(i):
+    dev = require_gpu()
+    rng = _rng("gate", i)
+    hq, hkv = _heads(rng)
+    b = int(rng.integers(1, 3))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64]))
+    s = int(rng.integers(1, 900))
+    hidden = int(rng.choice([32, 48, 64, 128]))
+    causal = bool(rng.random() < 0.8)
+    dtype = _dtype(rng)
+    print(f"gate sweep {i}: B={b} Hq={hq} Hkv={hkv} S={s} D={d} bs={bs} hidden={hidden} "
+          f"causal={causal} {dtype}", flush=True)
+    torch.manual_seed(34000 + i)
+    gate = AttnGate(num_heads=hq, head_dim=d, block_size=bs, gate_hidden_dim=hidden,
+                    is_causal=causal).to(dev)
+    gate.requires_grad_(False)
+    q, k, _ = ai.qkv("unit", (b, hq, s, d), (b, hkv, s, d), 34100 + i, bs, dtype=dtype)
+    with torch.no_grad():
+        out = gate(q.to(dev), k.to(dev), return_logits=True)
+    torch.cuda.synchronize()
+    gate.cpu()
+    ref = orc.gate_logits(to_np(q), to_np(k), gate.gate_proj_in.weight.numpy(),
+                          gate.gate_proj_in.bias.numpy(), gate.gate_proj_out.weight.numpy(), bs,
+                          dtype=np.float64)
+    np.testing.assert_allclose(to_np(out.logits), ref, rtol=1e-4, atol=1e-5)
+    soft_ref, hard_ref = orc.threshold_mask(to_np(out.logits), 0.5, causal)
+    np.testing.assert_allclose(to_np(out.soft_scores), soft_ref, rtol=0, atol=2e-7)
+    decisive = np.abs(soft_ref - 0.5) > 1e-6
+    assert np.array_equal(out.hard_mask.cpu().numpy()[decisive], hard_ref[decisive])
