@@ -21,6 +21,7 @@ from helpers import assert_close_bf16, bar, require_gpu, to_np
 from oracle import tasft_oracle as orc
 from tasft_amd.kernels import BlockSparseFlashAttention
 from tasft_amd.modules import AttnGate
+from tasft_amd.training import gate_target_from_qk
 
 pytestmark = pytest.mark.gpu
 
@@ -29,10 +30,12 @@ N_VARLEN = 8
 N_DECODE = 16
 N_PAGED = 8
 N_GATE = 10
+N_TARGET = 10
 
 
 def _rng(kind: str, i: int) -> np.random.Generator:
-    return np.random.default_rng([20261202, ["prefill", "varlen", "decode", "paged", "gate"].index(kind), i])
+    kinds = ["prefill", "varlen", "decode", "paged", "gate", "target"]
+    return np.random.default_rng([20261202, kinds.index(kind), i])
 
 
 def _heads(rng) -> tuple[int, int]:
@@ -184,3 +187,43 @@ def test_gate_sweep(i):
     np.testing.assert_allclose(to_np(out.soft_scores), soft_ref, rtol=0, atol=2e-7)
     decisive = np.abs(soft_ref - 0.5) > 1e-6
     assert np.array_equal(out.hard_mask.cpu().numpy()[decisive], hard_ref[decisive])
+
+
+@pytest.mark.parametrize("i", range(N_TARGET))
+def test_gate_target_sweep(i):
+    dev = require_gpu()
+    rng = _rng("target", i)
+    hq, hkv = _heads(rng)
+    b = int(rng.integers(1, 3))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64, 128]))
+    s = int(rng.integers(1, 700))
+    causal = bool(rng.random() < 0.8)
+    normalize = str(rng.choice(["none", "flat", "row"]))
+    masked = bool(rng.random() < 0.5)
+    dtype = _dtype(rng)
+    print(f"gate target sweep {i}: B={b} Hq={hq} Hkv={hkv} S={s} D={d} bs={bs} causal={causal} "
+          f"normalize={normalize} masked={masked} {dtype}", flush=True)
+    q, k, _ = ai.qkv("unit", (b, hq, s, d), (b, hkv, s, d), 35000 + i, bs, dtype=dtype)
+    amask = None
+    if masked:
+        # A key-padding mask: each sequence's tail beyond a random length is -inf, and a
+        # few finite negative entries shift scores before the max-pool.
+        amask = torch.zeros(b, s)
+        for bb in range(b):
+            n = int(rng.integers(1, s + 1))
+            amask[bb, n:] = float("-inf")
+        amask[:, : min(s, 3)] += -2.5
+    got = gate_target_from_qk(q.to(dev), k.to(dev), bs, causal=causal, normalize=normalize,
+                              attention_mask=None if amask is None else amask.to(dev))
+    torch.cuda.synchronize()
+    raw_ref = orc.block_max(to_np(q), to_np(k), bs, causal, dtype=np.float64,
+                            attn_mask=None if amask is None else amask.numpy())
+    got = to_np(got)
+    if normalize == "none":
+        assert np.array_equal(np.isneginf(got), np.isneginf(raw_ref))
+        fin = np.isfinite(raw_ref)
+        np.testing.assert_allclose(got[fin], raw_ref[fin], rtol=1e-4, atol=1e-5)
+    else:
+        ref = orc.normalize_block_max(raw_ref, normalize)
+        np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-7)
