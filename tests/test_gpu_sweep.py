@@ -31,10 +31,11 @@ N_DECODE = 16
 N_PAGED = 8
 N_GATE = 10
 N_TARGET = 10
+N_GATE_BWD = 6
 
 
 def _rng(kind: str, i: int) -> np.random.Generator:
-    kinds = ["prefill", "varlen", "decode", "paged", "gate", "target"]
+    kinds = ["prefill", "varlen", "decode", "paged", "gate", "target", "gate_bwd"]
     return np.random.default_rng([20261202, kinds.index(kind), i])
 
 
@@ -227,3 +228,57 @@ def test_gate_target_sweep(i):
     else:
         ref = orc.normalize_block_max(raw_ref, normalize)
         np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-7)
+
+
+@pytest.mark.parametrize("i", range(N_GATE_BWD))
+def test_gate_backward_sweep(i):
+    """The gate's HIP forward and backward against torch autograd of the reference formula
+    (the module's own torch path, fp32), for every parameter and, in some cases, Q and K."""
+    dev = require_gpu()
+    rng = _rng("gate_bwd", i)
+    hq, hkv = _heads(rng)
+    b = int(rng.integers(1, 3))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([32, 64]))
+    s = int(rng.integers(1, 900))
+    hidden = int(rng.choice([32, 48, 64, 128, 200]))
+    causal = bool(rng.random() < 0.8)
+    qk_grad = bool(rng.random() < 0.5)
+    print(f"gate backward sweep {i}: B={b} Hq={hq} Hkv={hkv} S={s} D={d} bs={bs} hidden={hidden} "
+          f"causal={causal} qk_grad={qk_grad}", flush=True)
+    torch.manual_seed(36000 + i)
+    gate = AttnGate(num_heads=hq, head_dim=d, block_size=bs, gate_hidden_dim=hidden,
+                    is_causal=causal).to(dev)
+    q, k, _ = ai.qkv("unit", (b, hq, s, d), (b, hkv, s, d), 36100 + i, bs)
+    q, k = q.to(dev), k.to(dev)
+    nb = math.ceil(s / bs)
+    r = torch.randn(b, hq, nb, nb, generator=torch.Generator().manual_seed(36200 + i)).to(dev)
+
+    def run(path):
+        gate.zero_grad(set_to_none=True)
+        qq = q.clone().requires_grad_(qk_grad)
+        kk = k.clone().requires_grad_(qk_grad)
+        out = gate(qq, kk) if path == "hip" else gate._forward_torch(qq, kk, 0.5, False, False)
+        (out.soft_scores.float() * r).sum().backward()
+        grads = {n: p.grad.detach().clone() for n, p in gate.named_parameters()}
+        if qk_grad:
+            grads["q"], grads["k"] = qq.grad.float(), kk.grad.float()
+        return out, grads
+
+    out_h, g_h = run("hip")
+    out_t, g_t = run("torch")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_h.soft_scores.detach(), out_t.soft_scores.detach().float(),
+                               rtol=1e-5, atol=1e-6)
+    # The gate is a ReLU network: a pre-activation within fp32 rounding of zero takes the
+    # other branch when it is summed in another order, which moves a few gradient entries
+    # by about 1e-3 of the largest one. The two fp32 paths then still agree more closely
+    # than either agrees with float64. So the sweep bounds the relative L2 error and bounds
+    # the largest entry loosely; a wrong formula misses both by orders of magnitude. The
+    # hand-picked backward tests keep an element-wise bar on their fixed inputs.
+    for name, ref in g_t.items():
+        ref = ref.float()
+        diff = g_h[name].float() - ref
+        rel_l2 = float(diff.norm() / (ref.norm() + 1e-30))
+        rel_max = float(diff.abs().max() / (ref.abs().max() + 1e-30))
+        assert rel_l2 <= 5e-3 and rel_max <= 1e-2, f"{name}: rel L2 {rel_l2:.2e}, max {rel_max:.2e}"
