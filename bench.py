@@ -249,6 +249,115 @@ def bench_decode_qwen(torch, dev, steps, warmup):
     return {"ms": ms, "gbps": total / (ms * 1e-3) / 1e9}
 
 
+def bench_varlen(torch, dev, steps, warmup):
+    """Packed variable-length prefill: four sequences of 8192, 6144, 4096 and 2048 tokens
+    (Llama-3-8B heads) in one [T, H, D] batch, each with a causal block mask keeping the
+    diagonal and 20% of the other causal blocks, through ``forward_varlen``."""
+    from tasft_amd import workloads as wl
+    from tasft_amd.kernels import BlockSparseFlashAttention
+
+    lens = [8192, 6144, 4096, 2048]
+    hq, hkv, d, bs = 32, 8, 128, 64
+    total = sum(lens)
+    q = wl.randn_bf16((total, hq, d), 1011).to(dev)
+    k = wl.randn_bf16((total, hkv, d), 1012).to(dev)
+    v = wl.randn_bf16((total, hkv, d), 1013).to(dev)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    nb = max(lens) // bs
+    g = torch.Generator().manual_seed(2011)
+    keep = torch.rand((len(lens), hq, nb, nb), generator=g) < 0.2
+    mask = ((keep & torch.ones(nb, nb, dtype=torch.bool).tril(-1)) | torch.eye(nb, dtype=torch.bool)).to(dev)
+    executed = 0
+    for n, ln in enumerate(lens):
+        nb_n = ln // bs
+        tri = torch.ones(nb_n, nb_n, dtype=torch.bool, device=dev).tril()
+        executed += int((mask[n, :, :nb_n, :nb_n] & tri).sum().item())
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    for _ in range(warmup):
+        bsfa.forward_varlen(q, k, v, mask, cu, causal=True)
+    torch.cuda.synchronize()
+    t = LaunchTimer(torch)
+    for _ in range(steps):
+        with _Span(t):
+            bsfa.forward_varlen(q, k, v, mask, cu, causal=True)
+    torch.cuda.synchronize()
+    ms = t.total_ms() / steps
+    return {"ms": ms, "tflops": executed * FLOP_PER_BLOCK / (ms * 1e-3) / 1e12, "tokens": total}
+
+
+def bench_decode_step(torch, dev, steps, warmup):
+    """One cached decode step through ``SparseAttentionDecoder`` (gate row of the new token
+    from the kept key units + split-K sparse decode) after a prefill of 8191 tokens, B=8,
+    Llama-3-8B heads, per-head thresholds keeping 10% of the causal blocks. Every timed step
+    decodes at the same position (the state is restored between steps)."""
+    from tasft_amd import workloads as wl
+    from tasft_amd.inference import SparseAttentionDecoder
+
+    from tasft_amd.modules import AttnGate
+
+    b, hq, hkv, d, s = 8, 32, 8, 128, 8192
+    shape = wl.Shape(b, hq, hkv, s)
+    q, k, v = (t.to(dev) for t in wl.qkv(shape, 1021))
+    gate = AttnGate(num_heads=hq, head_dim=d, block_size=64, gate_hidden_dim=128)
+    gate.load_state_dict(wl.gate_params(128, d, 3002))
+    gate = gate.to(dev).requires_grad_(False)
+    with torch.no_grad():
+        probe = gate(q[:, :, :s - 1], k[:, :, :s - 1], threshold=0.5)
+    taus = wl.per_head_threshold(probe.soft_scores, keep_causal=0.10)
+    dec = SparseAttentionDecoder(gate, threshold=taus, max_len=s)
+    dec.prefill(q[:, :, :s - 1], k[:, :, :s - 1], v[:, :, :s - 1])
+    state = (dec.length, dec._ksum.clone(), dec._qsum.clone())
+    q_new = q[:, :, s - 1:s].contiguous()
+
+    def restore():
+        dec.length = state[0]
+        dec._ksum.copy_(state[1])
+        dec._qsum.copy_(state[2])
+
+    for _ in range(warmup):
+        restore()
+        dec.step(q_new, k, v)
+    torch.cuda.synchronize()
+    t = LaunchTimer(torch)
+    for _ in range(steps):
+        restore()
+        with _Span(t):
+            dec.step(q_new, k, v)
+    torch.cuda.synchronize()
+    return {"us": t.total_ms() / steps * 1e3}
+
+
+def bench_gate_train(torch, dev, steps, warmup):
+    """One gate training step at config 2: HIP gate forward, gate target from Q and K, the
+    fused KL loss and the HIP backward into the gate parameters (``loss.backward()``)."""
+    from tasft_amd import workloads as wl
+    from tasft_amd.modules import AttnGate
+    from tasft_amd.training import gate_loss_from_qk
+
+    shape = wl.CONFIG_SHAPES[2]
+    q, k, _ = (t.to(dev) for t in wl.qkv(shape, 1002))
+    gate = AttnGate(num_heads=shape.q_heads, head_dim=shape.head_dim, block_size=shape.block,
+                    gate_hidden_dim=128)
+    gate.load_state_dict(wl.gate_params(128, shape.head_dim, 3002))
+    gate = gate.to(dev)
+
+    def step():
+        gate.zero_grad(set_to_none=True)
+        out = gate(q, k)
+        loss = gate_loss_from_qk(out.soft_scores, q, k, shape.block)
+        loss.backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t = LaunchTimer(torch)
+    for _ in range(steps):
+        with _Span(t):
+            step()
+    torch.cuda.synchronize()
+    return {"ms": t.total_ms() / steps}
+
+
 def bench_qwen(torch, dev, steps, warmup):
     from tasft_amd import workloads as wl
     from tasft_amd.kernels import BlockSparseFlashAttention, executed_blocks
@@ -385,8 +494,9 @@ def main() -> int:
     # The GPU settles over the first ~150 steps after the idle setup phase (about 1.2 ms
     # per step at first, 0.85 ms after 50 steps, 0.73 ms steady); warm-up steps are untimed.
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--extras", default="decode,qwen,gate_target",
-                    help="comma list of extra workloads (decode, qwen, gate_target) or 'none'")
+    ap.add_argument("--extras", default="decode,qwen,gate_target,varlen,decode_step,gate_train",
+                    help="comma list of extra workloads (decode, qwen, gate_target, varlen, "
+                         "decode_step, gate_train) or 'none'")
     ap.add_argument("--no-extras", action="store_true", help="same as --extras none")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -398,7 +508,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
     extras = set() if args.no_extras or args.extras == "none" else set(args.extras.split(","))
-    unknown = extras - {"decode", "qwen", "gate_target"}
+    unknown = extras - {"decode", "qwen", "gate_target", "varlen", "decode_step", "gate_train"}
     if unknown:
         print(f"unknown --extras entries: {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -428,6 +538,19 @@ def main() -> int:
         dq = bench_decode_qwen(torch, dev, max(10, args.steps), max(20, args.warmup))
         extra.update({"decode_qwen_ms": round(dq["ms"], 4), "decode_qwen_hbm_gbps": round(dq["gbps"], 1),
                       "decode_qwen_hbm_frac": round(dq["gbps"] / PEAK_HBM_GBPS, 4)})
+    if "varlen" in extras:
+        log("bench: packed varlen prefill")
+        vl = bench_varlen(torch, dev, max(10, args.steps // 2), max(10, args.warmup // 10))
+        extra.update({"varlen_prefill_ms": round(vl["ms"], 4),
+                      "varlen_prefill_tflops_executed": round(vl["tflops"], 1)})
+    if "decode_step" in extras:
+        log("bench: cached decode step")
+        ds = bench_decode_step(torch, dev, max(20, args.steps), max(20, args.warmup // 10))
+        extra.update({"decode_step_us": round(ds["us"], 1)})
+    if "gate_train" in extras:
+        log("bench: gate training step")
+        gt = bench_gate_train(torch, dev, max(10, args.steps // 5), max(5, args.warmup // 30))
+        extra.update({"gate_train_step_ms": round(gt["ms"], 4)})
     if "qwen" in extras:
         log("bench: config 4 Qwen prefill")
         qw = bench_qwen(torch, dev, max(5, args.steps // 2), max(10, args.warmup // 4))

@@ -81,6 +81,15 @@ class SparseAttentionDecoder:
             self._ksum = torch.zeros((B, Hkv, D), dtype=torch.float32, device=q.device)
             self._qsum = torch.zeros((B, Hq, D), dtype=torch.float32, device=q.device)
         self.length = S
+        # Per-step constants, read from the gate once: the W_in halves with the 1/block of
+        # the zero-padded mean folded in, the bias, w_out, the thresholds and the flags.
+        w_in = self.gate.gate_proj_in.weight.detach().float()
+        self._wk_t = (w_in[:, D:] / bs).t().contiguous()
+        self._wq_t = (w_in[:, :D] / bs).t().contiguous()
+        self._b_in = self.gate.gate_proj_in.bias.detach().float().contiguous()
+        self._w_out = self.gate.gate_proj_out.weight.detach().float().reshape(-1).contiguous()
+        self._taus = taus
+        self._flags = (1 if self.gate.is_causal else 0) | (2 if self.force_diagonal else 0)
         return out, g
 
     # ------------------------------------------------------------------ decode
@@ -100,25 +109,20 @@ class SparseAttentionDecoder:
         if t % bs == 0:
             self._ksum.zero_()
             self._qsum.zero_()
-        self._ksum += k_new[:, :, 0].float()
-        self._qsum += q_new[:, :, 0].float()
-        w_in = self.gate.gate_proj_in.weight.detach().float()
-        b_in = self.gate.gate_proj_in.bias.detach().float()
-        w_out = self.gate.gate_proj_out.weight.detach().float().reshape(-1).contiguous()
-        self._vk[:, :, i] = (self._ksum / bs) @ w_in[:, D:].t()
-        uq = ((self._qsum / bs) @ w_in[:, :D].t() + b_in).unsqueeze(2).contiguous()
-        nbk = i + 1
+        self._ksum.add_(k_new[:, :, 0])
+        self._qsum.add_(q_new[:, :, 0])
         hid = self.gate.gate_hidden_dim
+        self._vk[:, :, i] = torch.matmul(self._ksum, self._wk_t)
+        uq = torch.addmm(self._b_in, self._qsum.view(B * Hq, D), self._wq_t).view(B, Hq, 1, hid)
+        nbk = i + 1
         soft = torch.empty((B, Hq, 1, nbk), dtype=torch.float32, device=q_new.device)
         mask = torch.empty((B, Hq, 1, nbk), dtype=torch.uint8, device=q_new.device)
         active = torch.empty((1,), dtype=torch.int64, device=q_new.device)
-        taus = self.gate._thresholds(self.threshold, q_new.device)
-        flags = (1 if self.gate.is_causal else 0) | (2 if self.force_diagonal else 0)
         lib = _native.load_library()
         status = lib.tasft_gate_rows_fwd(
-            uq.data_ptr(), self._vk.data_ptr(), w_out.data_ptr(), taus.data_ptr(), soft.data_ptr(),
-            None, mask.data_ptr(), active.data_ptr(), B, Hq, Hkv, 1, nbk, i, hid,
-            self._vk.shape[2] * hid, flags, _native.stream_handle(q_new.device))
+            uq.data_ptr(), self._vk.data_ptr(), self._w_out.data_ptr(), self._taus.data_ptr(),
+            soft.data_ptr(), None, mask.data_ptr(), active.data_ptr(), B, Hq, Hkv, 1, nbk, i, hid,
+            self._vk.shape[2] * hid, self._flags, _native.stream_handle(q_new.device))
         _native.check(status, "tasft_gate_rows_fwd", {"position": t})
         self.length = t + 1
         return GateOutput(soft_scores=soft, hard_mask=mask.view(torch.bool), num_blocks_q=1,
