@@ -10,12 +10,19 @@
 // this computes u_i = W_q qbar_i + b_in once per query block and v_j = W_k kbar_j once
 // per key block, so each pair costs hidden x (add, max, fma) instead of a 2D-wide GEMV.
 //
-// Pooling streams Q and K (bf16 or fp16, accumulated in fp32) from HBM exactly once (GQA-native: K is pooled per KV head,
-// never expanded) in one kernel that also projects the block means (a streaming variant
-// for block size 64 and D in {64, 128}, a generic one otherwise). The pairwise kernel evaluates the MLP for the causal pairs in fp32, applies
+// Pooling streams Q and K (bf16 or fp16, accumulated in fp32) from HBM exactly once
+// (GQA-native: K is pooled per KV head, never expanded) in kernels that also project the
+// block means. The pairwise stage evaluates the MLP for the causal pairs in fp32, applies
 // sigmoid, the causal zero and the per-head threshold, and writes soft scores (fp32),
 // optional logits, the uint8 hard mask and the active count. Flag bit 1 forces the
 // diagonal blocks on in the hard mask (soft scores unchanged).
+//
+// Block size 64, D in {64, 128}, hidden a multiple of 32 up to 128 (the benchmarked gate):
+// two launches. gate_pool_proj64_kernel pools and projects every key chunk and half of the
+// query chunks; gate_qpool_pair64_kernel then takes every query chunk, pooling the other
+// half itself, and evaluates each chunk's rows as soon as its units exist. No workgroup
+// waits for another within a launch. Otherwise one pooling launch (streaming for block 64,
+// generic else) is followed by gate_pairwise_kernel.
 #include <algorithm>
 
 #include "common.h"
@@ -39,8 +46,30 @@ struct GatePoolParams {
   float* kmeans;      // [B, Hkv, NB, D] block means of K, or null
   unsigned long long* counter;
   int64_t sq[3], sk[3];
+  int64_t wg0;  // first workgroup index of the launch (gate_pool_proj64_kernel)
+  int64_t mix;  // gate_qpool_pair64_kernel: workgroups per round (the CU count)
+  int64_t kinds;  // gate_qpool_pair64_kernel: rounds per group (see there)
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
+  int rotate;   // query chunk of stream index g is (g % chunks + bh) % chunks
 };
+
+// Query chunks gate_qpool_pair64_kernel pools itself: the last round of every group of
+// `kinds` rounds of `mix` workgroups (a partial last group fills its first rounds first).
+__host__ __device__ __forceinline__ int64_t gate_fresh_chunks(int64_t nq, int64_t mix,
+                                                              int64_t kinds) {
+  const int64_t tail = nq % (kinds * mix);
+  const int64_t rest = tail - (kinds - 1) * mix;
+  return (nq / (kinds * mix)) * mix + (rest > 0 ? rest : 0);
+}
+
+// Query chunk index g (0 .. B*Hq*chunks - 1) to its (b, head) and chunk; with rotation the
+// chunks of one (b, head) are taken in an order that starts at bh % chunks.
+__device__ __forceinline__ void query_chunk(const GatePoolParams& p, int64_t g, int chunks,
+                                            int64_t& bh, int& chunk) {
+  bh = g / chunks;
+  chunk = (int)(g % chunks);
+  if (p.rotate) chunk = (int)((chunk + bh) % chunks);
+}
 
 template <int DT>
 __global__ void __launch_bounds__(256)
@@ -137,9 +166,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
+// Pools kFusePB blocks (chunk `chunk`) of one (b, head) row stream of Q (is_q) or K and
+// projects their means; `red` is the workgroup's LDS (4 x kFusePB x D floats).
 template <int D, int DT>
-__global__ void __launch_bounds__(256)
-gate_pool_proj64_kernel(const GatePoolParams p) {
+__device__ __forceinline__ void pool_proj64(const GatePoolParams& p, bool is_q, int64_t bh,
+                                            int chunk, float (&red)[4][kFusePB][D]) {
   constexpr int BSZ = 64;
   constexpr int DOCT = D / 8;        // 16-byte chunks per row
   constexpr int RG = 256 / DOCT;     // row groups in the workgroup
@@ -147,17 +178,9 @@ gate_pool_proj64_kernel(const GatePoolParams p) {
   constexpr int WRG = kWave / DOCT;  // row groups per wave
   constexpr int GB = 4;              // blocks per load group
   static_assert(WRG == 4 || WRG == 8, "row groups per wave");
-  __shared__ __attribute__((aligned(16))) float red[4][kFusePB][D];  // per-wave sums, then means
 
   const int tid = threadIdx.x;
-  if (blockIdx.x == 0 && tid == 0 && p.counter) *p.counter = 0ull;
-  const int chunks = (p.NB + kFusePB - 1) / kFusePB;
-  const int64_t nq = (int64_t)p.B * p.Hq * chunks;
-  const bool is_q = blockIdx.x < nq;
-  const int64_t local = is_q ? blockIdx.x : blockIdx.x - nq;
   const int heads = is_q ? p.Hq : p.Hkv;
-  const int64_t bh = local / chunks;
-  const int chunk = (int)(local % chunks);
   const int b = (int)(bh / heads);
   const int h = (int)(bh % heads);
   const uint16_t* src = is_q ? p.q + b * p.sq[0] + h * p.sq[1] : p.k + b * p.sk[0] + h * p.sk[1];
@@ -273,6 +296,26 @@ gate_pool_proj64_kernel(const GatePoolParams p) {
         if (blk < nblk) dst[(int64_t)blk * p.hidden + c] = acc[r] + bias;
       }
     }
+  }
+}
+
+// Workgroup wg0 + blockIdx.x pools query chunks first (B x Hq x chunks, see query_chunk),
+// then key chunks.
+template <int D, int DT>
+__global__ void __launch_bounds__(256)
+gate_pool_proj64_kernel(const GatePoolParams p) {
+  __shared__ __attribute__((aligned(16))) float red[4][kFusePB][D];  // per-wave sums, then means
+  if (blockIdx.x == 0 && threadIdx.x == 0 && p.counter) *p.counter = 0ull;
+  const int chunks = (p.NB + kFusePB - 1) / kFusePB;
+  const int64_t nq = (int64_t)p.B * p.Hq * chunks;
+  const int64_t wg = (int64_t)blockIdx.x + p.wg0;
+  if (wg < nq) {
+    int64_t bh;
+    int chunk;
+    query_chunk(p, wg, chunks, bh, chunk);
+    pool_proj64<D, DT>(p, true, bh, chunk, red);
+  } else {
+    pool_proj64<D, DT>(p, false, (wg - nq) / chunks, (int)((wg - nq) % chunks), red);
   }
 }
 
@@ -455,6 +498,210 @@ gate_pairwise_kernel(const GatePairParams p) {
   }
 }
 
+// Query pooling and the pairwise MLP in one kernel (block size 64, D in {64, 128}, hidden a
+// multiple of kFuseHid and at most kFuseMaxHid). It runs after gate_pool_proj64_kernel has
+// projected every key block (that launch covers the key chunks only), so a workgroup
+// depends on no other workgroup of its own launch: it pools and projects query chunk
+// `chunk` of one (b, head) (kFusePB query-block rows), then evaluates those rows against
+// the key blocks they need (blocks 0 .. chunk end under causal without logits, all blocks
+// otherwise) and writes the rows' soft scores, hard mask and logits.
+//
+// Pairwise layout: key blocks in groups of kFuseKeys = 128, 32 per wave. The chunk's query
+// units (all hidden units) and w_out are staged once, transposed, for the workgroup; each
+// wave stages the units of its own 32 key blocks, kFuseHid at a time, in its own LDS area,
+// with the next round's loads in flight during the current round's MLP, so the rounds need
+// no workgroup barrier. Lane (tr, tc) accumulates rows 2tr, 2tr+1 against keys 4tc ..
+// 4tc+3 of its wave over every hidden unit. The logit uses the same relu(x) = (x + |x|) / 2
+// split as gate_pairwise_kernel, with A_i and B_j summed in a fixed order.
+constexpr int kFuseHid = 32;
+constexpr int kFuseMaxHid = 128;
+constexpr int kGateKinds = 2;  // rounds per group in gate_qpool_pair64_kernel
+constexpr int kFuseKeys = 128;
+constexpr int kFuseLdq = kFusePB + 4;
+constexpr int kFuseLdw = 32 + 4;
+constexpr int kFuseWave = kFuseHid * kFuseLdw + 32;  // one wave's key units + its B_j
+constexpr int kFuseFloats = kFuseMaxHid * kFuseLdq + kFuseMaxHid + 16 * kFusePB + kFusePB +
+                            4 * kFuseWave;
+
+template <int D, int DT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
+gate_qpool_pair64_kernel(const GatePoolParams p, const GatePairParams q) {
+  constexpr int kRed = 4 * kFusePB * D;
+  constexpr int kLds = kRed > kFuseFloats ? kRed : kFuseFloats;
+  __shared__ __attribute__((aligned(16))) float lds[kLds];
+  __shared__ unsigned int wave_count[4];
+  static_assert(kFuseHid == 32 && kFusePB == 16 && kFuseKeys == 128, "thread layouts below");
+
+  // Workgroups come in rounds of `mix` (the CU count, so every CU holds both kinds), in
+  // groups of `kinds` rounds: the first kinds - 1 rounds take query chunks the first launch
+  // already pooled (the last n1 of the nq chunk indices), which go straight to the pairwise
+  // MLP; the last round takes the others, pooled and projected here first. One kind's MLP
+  // then runs while the other streams Q.
+  // Chunks rotate with the head (query_chunk), so the XCDs (workgroup i runs on XCD i % 8)
+  // each get a mix of short (early) and long (late) query rows.
+  const int fchunks = (p.NB + kFusePB - 1) / kFusePB;
+  const int64_t nq = (int64_t)p.B * p.Hq * fchunks;
+  const int64_t n1 = nq - gate_fresh_chunks(nq, p.mix, p.kinds);
+  const int64_t grp = blockIdx.x / (p.kinds * p.mix), o = blockIdx.x % (p.kinds * p.mix);
+  const bool pooled = o < (p.kinds - 1) * p.mix;
+  const int64_t g = pooled ? nq - n1 + grp * (p.kinds - 1) * p.mix + o
+                           : grp * p.mix + (o - (p.kinds - 1) * p.mix);
+  int64_t bh;
+  int chunk;
+  query_chunk(p, g, fchunks, bh, chunk);
+  if (!pooled)
+    pool_proj64<D, DT>(p, true, bh, chunk, *reinterpret_cast<float(*)[4][kFusePB][D]>(lds));
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int tr = lane / 8, tc = lane % 8;
+  const int b = (int)(bh / q.Hq), h = (int)(bh % q.Hq), kvh = h / q.G;
+  const int i0 = chunk * kFusePB;
+  const int nrows = min(kFusePB, q.NBq - i0);
+  const int hid = q.hidden;
+  const float* uq = q.uq + (bh * q.NBq + i0) * (int64_t)hid;
+  const float* uk = q.uk + ((int64_t)b * q.Hkv + kvh) * q.uk_bh_stride;
+  const int kneed = (q.causal && q.logits == nullptr) ? min(i0 + kFusePB, q.NBk) : q.NBk;
+  const float tau = q.tau[h];
+  float* uq_t = lds;                            // [hid][kFuseLdq]
+  float* wo = uq_t + kFuseMaxHid * kFuseLdq;    // [hid]
+  float* apart = wo + kFuseMaxHid;              // [16][kFusePB] partial A_i
+  float* arow = apart + 16 * kFusePB;           // A_i [kFusePB]
+  float* wst = arow + kFusePB + wave * kFuseWave;  // this wave: [kFuseHid][kFuseLdw] units
+  float* bkey = wst + kFuseHid * kFuseLdw;         // this wave: B_j of its 32 keys
+
+  // The chunk's units were stored by all four waves, and the pooling LDS is reused below.
+  __syncthreads();
+  {
+    const int row = tid % kFusePB;
+    for (int u4 = tid / kFusePB; 4 * u4 < hid; u4 += 256 / kFusePB) {
+      const f32x4_t v = row < nrows ? *(const f32x4_t*)(uq + (int64_t)row * hid + 4 * u4)
+                                    : (f32x4_t){};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) uq_t[(4 * u4 + e) * kFuseLdq + row] = v[e];
+    }
+    for (int c = tid; c < hid; c += 256) wo[c] = q.w_out[c];
+  }
+  __syncthreads();
+  {
+    // A_i: sixteen groups of hid / 16 units per row, then the groups in order.
+    const int row = tid % kFusePB, g = tid / kFusePB, per = hid / 16;
+    float a = 0.f;
+    for (int c = g * per; c < (g + 1) * per; ++c) a = fmaf(wo[c], uq_t[c * kFuseLdq + row], a);
+    apart[g * kFusePB + row] = a;
+  }
+  __syncthreads();
+  if (tid < kFusePB) {
+    float a = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) a += apart[g * kFusePB + tid];
+    arow[tid] = a;
+  }
+  __syncthreads();
+
+  // Staging role of this lane: key block kk of the wave's 32, units 16*hh .. +15 of a round.
+  const int kk = lane % 32, hh = lane / 32;
+  const bool vec_out = (q.NBk % 4) == 0;
+  unsigned int active = 0;
+  for (int k0 = 0; k0 < q.NBk; k0 += kFuseKeys) {
+    const int kw = k0 + 32 * wave;  // first key block of this wave
+    const bool wave_on = kw < kneed;
+    float acc[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[r][e] = 0.f;
+    if (wave_on) {
+      const int j = kw + kk;
+      const bool kin = j < q.NBk;
+      const float* ksrc = uk + (int64_t)j * hid + 16 * hh;
+      f32x4_t kv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kv[i] = kin ? *(const f32x4_t*)(ksrc + 4 * i) : (f32x4_t){};
+      float b_part = 0.f;
+      for (int c0 = 0; c0 < hid; c0 += kFuseHid) {
+        // LDS accesses of one wave execute in order: the previous round's reads of this
+        // area are done before these writes, and these writes before the reads below. The
+        // wave barriers keep the compiler from reordering them.
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int cc = 16 * hh + 4 * i + e;
+            wst[cc * kFuseLdw + kk] = kv[i][e];
+            b_part = fmaf(wo[c0 + cc], kv[i][e], b_part);
+          }
+        __builtin_amdgcn_wave_barrier();
+        if (c0 + kFuseHid < hid) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            kv[i] = kin ? *(const f32x4_t*)(ksrc + c0 + kFuseHid + 4 * i) : (f32x4_t){};
+        }
+#pragma unroll 8
+        for (int cc = 0; cc < kFuseHid; ++cc) {
+          const f32x2_t av = *(const f32x2_t*)&uq_t[(c0 + cc) * kFuseLdq + 2 * tr];
+          const f32x4_t bv = *(const f32x4_t*)&wst[cc * kFuseLdw + 4 * tc];
+          const float w = wo[c0 + cc];
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[r][e] = fmaf(fabsf(av[r] + bv[e]), w, acc[r][e]);
+        }
+      }
+      // B_j of key kk: its two unit halves, held by lanes kk and kk + 32.
+      const float bj = b_part + __shfl_xor(b_part, 32, kWave);
+      __builtin_amdgcn_wave_barrier();
+      if (hh == 0) bkey[kk] = bj;
+      __builtin_amdgcn_wave_barrier();
+    }
+    // Rows 2tr + r, keys kw + 4tc + e. Keys at or past kneed are above the diagonal of
+    // every row here (causal, no logits): their soft scores are exactly 0.
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int ii = 2 * tr + r, i = i0 + ii;
+      if (ii >= nrows) continue;
+      float soft[4], lg[4];
+      uint32_t on4 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int jk = kw + 4 * tc + e;
+        float logit = 0.f;
+        if (wave_on) logit = 0.5f * ((arow[ii] + bkey[4 * tc + e]) + acc[r][e]);
+        float sv = 1.f / (1.f + expf(-logit));
+        if (q.causal && jk > q.row0 + i) sv = 0.f;
+        const bool on = jk < q.NBk && (sv >= tau || (q.force_diag && q.row0 + i == jk));
+        active += on ? 1u : 0u;
+        on4 |= (on ? 1u : 0u) << (8 * e);
+        soft[e] = sv;
+        lg[e] = logit;
+      }
+      const int j0 = kw + 4 * tc;
+      const int64_t o = (bh * q.NBq + i) * (int64_t)q.NBk + j0;
+      if (vec_out && j0 + 4 <= q.NBk) {
+        *(f32x4_t*)(q.soft + o) = (f32x4_t){soft[0], soft[1], soft[2], soft[3]};
+        *(uint32_t*)(q.mask + o) = on4;
+        if (q.logits) *(f32x4_t*)(q.logits + o) = (f32x4_t){lg[0], lg[1], lg[2], lg[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (j0 + e >= q.NBk) break;
+          q.soft[o + e] = soft[e];
+          q.mask[o + e] = (uint8_t)((on4 >> (8 * e)) & 1u);
+          if (q.logits) q.logits[o + e] = lg[e];
+        }
+      }
+    }
+  }
+  const float tot = wave_sum((float)active);
+  if (lane == 0) wave_count[wave] = (unsigned int)(tot + 0.5f);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int t = (wave_count[0] + wave_count[1]) + (wave_count[2] + wave_count[3]);
+    if (t) atomicAdd(q.counter, (unsigned long long)t);
+  }
+}
+
 __global__ void gate_counter_reset_kernel(unsigned long long* counter) {
   if (threadIdx.x == 0) *counter = 0ull;
 }
@@ -615,6 +862,20 @@ gate_pairwise_bwd_kernel(const GateBwdParams p) {
 
 using namespace tasft;
 
+// Compute units of the current device (cached per device).
+static int gate_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 extern "C" size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads,
                                              int64_t num_kv_heads, int64_t seq_len,
                                              int64_t head_dim, int64_t block_size,
@@ -694,31 +955,10 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   pp.hidden = (int)hidden;
   pp.chunks = (int)chunks;
 
-  hipStream_t s = (hipStream_t)stream;
-  const bool fast = block_size == 64 && (head_dim == 64 || head_dim == 128) &&
-                    seq_len * std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
-  if (fast) {
-    const int64_t fchunks = (nb + kFusePB - 1) / kFusePB;
-    const int64_t grid1 = batch * (num_q_heads + num_kv_heads) * fchunks;
-    const dim3 g1((unsigned)grid1);
-    if (head_dim == 128 && dtype == kF16)
-      hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16>), g1, dim3(256), 0, s, pp);
-    else if (head_dim == 128)
-      hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kBf16>), g1, dim3(256), 0, s, pp);
-    else if (dtype == kF16)
-      hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kF16>), g1, dim3(256), 0, s, pp);
-    else
-      hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kBf16>), g1, dim3(256), 0, s, pp);
-  } else {
-    const dim3 g1((unsigned)(batch * (num_q_heads + num_kv_heads) * chunks));
-    if (dtype == kF16)
-      hipLaunchKernelGGL(gate_pool_project_kernel<kF16>, g1, dim3(256), 0, s, pp);
-    else
-      hipLaunchKernelGGL(gate_pool_project_kernel<kBf16>, g1, dim3(256), 0, s, pp);
-  }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess)
-    return set_error(kErrLaunch, "gate: pool launch failed: %s", hipGetErrorString(err));
+  pp.wg0 = 0;
+  pp.mix = 1;
+  pp.kinds = 2;
+  pp.rotate = 0;
 
   GatePairParams qp;
   qp.uq = pp.uq;
@@ -742,6 +982,64 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   qp.tiles_q = (int)tiles;
   qp.tiles_k = (int)tiles;
   qp.uk_bh_stride = nb * hidden;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t err;
+  const bool fast = block_size == 64 && (head_dim == 64 || head_dim == 128) &&
+                    seq_len * std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
+  if (fast) {
+    const int64_t fchunks = (nb + kFusePB - 1) / kFusePB;
+    // With hidden a multiple of kFuseHid, at most kFuseMaxHid: the first launch pools and projects the key
+    // chunks only, and gate_qpool_pair64_kernel pools each query chunk and evaluates its
+    // rows. Otherwise one launch pools both and gate_pairwise_kernel follows.
+    const bool fused = hidden % kFuseHid == 0 && hidden <= kFuseMaxHid;
+    const int64_t nq = batch * num_q_heads * fchunks;
+    int64_t n1 = 0;
+    if (fused) {
+      // The first launch pools the key chunks and the n1 query chunks that the fused
+      // kernel's even rounds take (see gate_qpool_pair64_kernel).
+      pp.mix = gate_device_cus();
+      pp.kinds = kGateKinds;
+      pp.rotate = 1;
+      n1 = nq - gate_fresh_chunks(nq, pp.mix, pp.kinds);
+      pp.wg0 = nq - n1;
+    }
+    const dim3 g1((unsigned)(fused ? n1 + batch * num_kv_heads * fchunks
+                                   : batch * (num_q_heads + num_kv_heads) * fchunks));
+    if (head_dim == 128 && dtype == kF16)
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16>), g1, dim3(256), 0, s, pp);
+    else if (head_dim == 128)
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kBf16>), g1, dim3(256), 0, s, pp);
+    else if (dtype == kF16)
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kF16>), g1, dim3(256), 0, s, pp);
+    else
+      hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kBf16>), g1, dim3(256), 0, s, pp);
+    if ((err = hipGetLastError()) != hipSuccess)
+      return set_error(kErrLaunch, "gate: pool launch failed: %s", hipGetErrorString(err));
+    if (fused) {
+      const dim3 g2((unsigned)nq);
+      if (head_dim == 128 && dtype == kF16)
+        hipLaunchKernelGGL((gate_qpool_pair64_kernel<128, kF16>), g2, dim3(256), 0, s, pp, qp);
+      else if (head_dim == 128)
+        hipLaunchKernelGGL((gate_qpool_pair64_kernel<128, kBf16>), g2, dim3(256), 0, s, pp, qp);
+      else if (dtype == kF16)
+        hipLaunchKernelGGL((gate_qpool_pair64_kernel<64, kF16>), g2, dim3(256), 0, s, pp, qp);
+      else
+        hipLaunchKernelGGL((gate_qpool_pair64_kernel<64, kBf16>), g2, dim3(256), 0, s, pp, qp);
+      if ((err = hipGetLastError()) != hipSuccess)
+        return set_error(kErrLaunch, "gate: fused launch failed: %s", hipGetErrorString(err));
+      return kOk;
+    }
+  } else {
+    const dim3 g1((unsigned)(batch * (num_q_heads + num_kv_heads) * chunks));
+    if (dtype == kF16)
+      hipLaunchKernelGGL(gate_pool_project_kernel<kF16>, g1, dim3(256), 0, s, pp);
+    else
+      hipLaunchKernelGGL(gate_pool_project_kernel<kBf16>, g1, dim3(256), 0, s, pp);
+    if ((err = hipGetLastError()) != hipSuccess)
+      return set_error(kErrLaunch, "gate: pool launch failed: %s", hipGetErrorString(err));
+  }
+
   const int64_t grid2 = batch * num_q_heads * tiles * tiles;
   hipLaunchKernelGGL(gate_pairwise_kernel, dim3((unsigned)grid2), dim3(256), 0, s, qp);
   if ((err = hipGetLastError()) != hipSuccess)

@@ -74,6 +74,8 @@ CASES = [
     (1, 2, 1, 777, 128, 48, 64, True),     # block size outside {32,64,128}
     (1, 4, 2, 700, 64, 64, 32, True),      # block 64, D=64, 11 blocks (partial pool chunk)
     (1, 4, 2, 1300, 128, 64, 200, False),  # block 64, 21 blocks, hidden > one staging tile
+    (1, 4, 2, 1300, 128, 64, 64, False),   # block 64, non-causal, fused query-pool + pairwise
+    (1, 2, 1, 9000, 128, 64, 32, True),    # 141 blocks: two 128-key groups per row
 ]
 
 
@@ -147,6 +149,31 @@ def test_config2_gate_full_size_sampled_heads():
     decisive = np.abs(soft_ref - 0.5) > TAU_BAND
     hard = out.hard_mask.cpu().numpy()
     assert np.array_equal(hard[decisive], hard_ref[decisive])
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "hidden"), [
+    (4, 32, 8, 8192, 128, 128),  # config 2
+    (1, 2, 1, 9000, 128, 32),    # two 128-key groups per row
+    (2, 4, 2, 700, 64, 64),      # D = 64, partial last query chunk
+])
+def test_causal_rows_skip_matches_full_evaluation(B, Hq, Hkv, S, D, hidden):
+    """Without logits, the causal gate evaluates only the key blocks a query chunk needs
+    (the rest are exactly 0); with logits it evaluates every pair. Soft scores, the mask
+    (per-head tau, forced diagonal) and the active count must agree bit for bit."""
+    dev = require_gpu()
+    gate = _gate(Hq, D, 64, hidden, True, seed=S + hidden).to(dev).requires_grad_(False)
+    q = wl.randn_bf16((B, Hq, S, D), S + 7, scale=1.0).to(dev)
+    k = wl.randn_bf16((B, Hkv, S, D), S + 8, scale=1.0).to(dev)
+    taus = torch.linspace(0.3, 0.7, Hq, device=dev)
+    with torch.no_grad():
+        full = gate(q, k, threshold=taus, return_logits=True, force_diagonal=True)
+        rows = gate(q, k, threshold=taus, force_diagonal=True)
+    torch.cuda.synchronize()
+    assert rows.logits is None
+    assert torch.equal(rows.soft_scores, full.soft_scores)
+    assert torch.equal(rows.hard_mask, full.hard_mask)
+    assert rows.sparsity_ratio == full.sparsity_ratio
+    assert rows.sparsity_ratio == pytest.approx(1.0 - full.hard_mask.double().mean().item(), abs=1e-12)
 
 
 def test_fp32_inputs_run_the_reference_formula_and_fp16_the_kernel():
