@@ -18,9 +18,10 @@
 // diagonal blocks on in the hard mask (soft scores unchanged).
 //
 // Block size 64, D in {64, 128}, hidden a multiple of 32 up to 128 (the benchmarked gate):
-// two launches. gate_pool_proj64_kernel pools and projects every key chunk and half of the
-// query chunks; gate_qpool_pair64_kernel then takes every query chunk, pooling the other
-// half itself, and evaluates each chunk's rows as soon as its units exist. No workgroup
+// two launches. gate_pool_proj64_kernel pools and projects every key chunk and a share of
+// the query chunks (half at B=4, 32 heads, S=8192); gate_qpool_pair64_kernel then takes
+// every query chunk, pooling the others itself, and evaluates each chunk's rows as soon as
+// its units exist. No workgroup
 // waits for another within a launch. Otherwise one pooling launch (streaming for block 64,
 // generic else) is followed by gate_pairwise_kernel.
 #include <algorithm>
@@ -48,27 +49,36 @@ struct GatePoolParams {
   int64_t sq[3], sk[3];
   int64_t wg0;  // first workgroup index of the launch (gate_pool_proj64_kernel)
   int64_t mix;  // gate_qpool_pair64_kernel: workgroups per round (the CU count)
-  int64_t kinds;  // gate_qpool_pair64_kernel: rounds per group (see there)
+  int64_t rounds;  // gate_qpool_pair64_kernel: rounds per group (see there)
+  int64_t pre;     // gate_qpool_pair64_kernel: rounds per group on pre-pooled chunks
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
-  int rotate;   // query chunk of stream index g is (g % chunks + bh) % chunks
+  int rotate;   // chunk-major query chunk order (query_chunk)
 };
 
-// Query chunks gate_qpool_pair64_kernel pools itself: the last round of every group of
-// `kinds` rounds of `mix` workgroups (a partial last group fills its first rounds first).
+// Query chunks gate_qpool_pair64_kernel pools itself: the last rounds - pre rounds of every
+// group of `rounds` rounds of `mix` workgroups (a partial last group fills its first rounds
+// first).
 __host__ __device__ __forceinline__ int64_t gate_fresh_chunks(int64_t nq, int64_t mix,
-                                                              int64_t kinds) {
-  const int64_t tail = nq % (kinds * mix);
-  const int64_t rest = tail - (kinds - 1) * mix;
-  return (nq / (kinds * mix)) * mix + (rest > 0 ? rest : 0);
+                                                              int64_t rounds, int64_t pre) {
+  const int64_t tail = nq % (rounds * mix);
+  const int64_t rest = tail - pre * mix;
+  return (nq / (rounds * mix)) * (rounds - pre) * mix + (rest > 0 ? rest : 0);
 }
 
-// Query chunk index g (0 .. B*Hq*chunks - 1) to its (b, head) and chunk; with rotation the
-// chunks of one (b, head) are taken in an order that starts at bh % chunks.
+// Query chunk index g (0 .. B*Hq*chunks - 1) to its (b, head) and chunk: (b, head)-major,
+// or with `rotate` chunk-major (g = chunk * B*Hq + bh), so that low indices are the early
+// query rows (the cheapest under causal) and consecutive workgroups, which run on
+// different XCDs, take different (b, head) of one chunk.
 __device__ __forceinline__ void query_chunk(const GatePoolParams& p, int64_t g, int chunks,
                                             int64_t& bh, int& chunk) {
-  bh = g / chunks;
-  chunk = (int)(g % chunks);
-  if (p.rotate) chunk = (int)((chunk + bh) % chunks);
+  if (p.rotate) {
+    const int64_t nbh = (int64_t)p.B * p.Hq;
+    bh = g % nbh;
+    chunk = (int)(g / nbh);
+  } else {
+    bh = g / chunks;
+    chunk = (int)(g % chunks);
+  }
 }
 
 template <int DT>
@@ -515,7 +525,8 @@ gate_pairwise_kernel(const GatePairParams p) {
 // split as gate_pairwise_kernel, with A_i and B_j summed in a fixed order.
 constexpr int kFuseHid = 32;
 constexpr int kFuseMaxHid = 128;
-constexpr int kGateKinds = 2;  // rounds per group in gate_qpool_pair64_kernel
+constexpr int kGateRounds = 3;     // rounds per group in gate_qpool_pair64_kernel
+constexpr int kGatePreRounds = 1;  // of which on chunks the first launch pooled
 constexpr int kFuseKeys = 128;
 constexpr int kFuseLdq = kFusePB + 4;
 constexpr int kFuseLdw = 32 + 4;
@@ -533,19 +544,19 @@ gate_qpool_pair64_kernel(const GatePoolParams p, const GatePairParams q) {
   static_assert(kFuseHid == 32 && kFusePB == 16 && kFuseKeys == 128, "thread layouts below");
 
   // Workgroups come in rounds of `mix` (the CU count, so every CU holds both kinds), in
-  // groups of `kinds` rounds: the first kinds - 1 rounds take query chunks the first launch
+  // groups of `rounds` rounds: the first `pre` rounds take query chunks the first launch
   // already pooled (the last n1 of the nq chunk indices), which go straight to the pairwise
-  // MLP; the last round takes the others, pooled and projected here first. One kind's MLP
-  // then runs while the other streams Q.
-  // Chunks rotate with the head (query_chunk), so the XCDs (workgroup i runs on XCD i % 8)
-  // each get a mix of short (early) and long (late) query rows.
+  // MLP; the other rounds take the rest, pooled and projected here first. One kind's MLP
+  // then runs while the other streams Q. In chunk-major order (query_chunk) the chunks
+  // pooled here are the early query rows, whose MLP is the shortest, and the pre-pooled
+  // ones the late rows.
   const int fchunks = (p.NB + kFusePB - 1) / kFusePB;
   const int64_t nq = (int64_t)p.B * p.Hq * fchunks;
-  const int64_t n1 = nq - gate_fresh_chunks(nq, p.mix, p.kinds);
-  const int64_t grp = blockIdx.x / (p.kinds * p.mix), o = blockIdx.x % (p.kinds * p.mix);
-  const bool pooled = o < (p.kinds - 1) * p.mix;
-  const int64_t g = pooled ? nq - n1 + grp * (p.kinds - 1) * p.mix + o
-                           : grp * p.mix + (o - (p.kinds - 1) * p.mix);
+  const int64_t n1 = nq - gate_fresh_chunks(nq, p.mix, p.rounds, p.pre);
+  const int64_t grp = blockIdx.x / (p.rounds * p.mix), o = blockIdx.x % (p.rounds * p.mix);
+  const bool pooled = o < p.pre * p.mix;
+  const int64_t g = pooled ? nq - n1 + grp * p.pre * p.mix + o
+                           : grp * (p.rounds - p.pre) * p.mix + (o - p.pre * p.mix);
   int64_t bh;
   int chunk;
   query_chunk(p, g, fchunks, bh, chunk);
@@ -957,7 +968,8 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
 
   pp.wg0 = 0;
   pp.mix = 1;
-  pp.kinds = 2;
+  pp.rounds = 2;
+  pp.pre = 1;
   pp.rotate = 0;
 
   GatePairParams qp;
@@ -999,9 +1011,10 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
       // The first launch pools the key chunks and the n1 query chunks that the fused
       // kernel's even rounds take (see gate_qpool_pair64_kernel).
       pp.mix = gate_device_cus();
-      pp.kinds = kGateKinds;
+      pp.rounds = kGateRounds;
+      pp.pre = kGatePreRounds;
       pp.rotate = 1;
-      n1 = nq - gate_fresh_chunks(nq, pp.mix, pp.kinds);
+      n1 = nq - gate_fresh_chunks(nq, pp.mix, pp.rounds, pp.pre);
       pp.wg0 = nq - n1;
     }
     const dim3 g1((unsigned)(fused ? n1 + batch * num_kv_heads * fchunks
