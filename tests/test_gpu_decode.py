@@ -266,3 +266,45 @@ def test_decode_paged_block_indices_equals_mask():
     m = bsfa.forward_decode_paged(q, kp, vp, table, lens, mask.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(a, m)
+
+
+@pytest.mark.parametrize("splits", (1, 4))
+def test_decode_empty_sequences_and_heads_give_zero(splits):
+    """Zero-length sequences and heads that select no block output exactly 0 (the closed
+    form's empty case), with one split and with partials merged by the combine pass, for the
+    contiguous and the paged cache; the other rows still match the oracle."""
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, bs, ps = 4, 8, 2, 300, 128, 64, 16
+    print(f"decode empty rows splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(7700 + splits)
+    per = (S + ps - 1) // ps
+    cap = per * ps
+    q = (torch.randn(B, Hq, 1, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    k = (torch.randn(B, Hkv, cap, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    v = (torch.randn(B, Hkv, cap, D, generator=g) / math.sqrt(D)).to(torch.bfloat16)
+    lens = torch.tensor([0, 300, 1, 0], dtype=torch.int32)
+    nb = (cap + bs - 1) // bs
+    mask = torch.rand((B, Hq, 1, nb), generator=g) < 0.5
+    mask[:, :, :, 0] = True
+    mask[1, 3] = False  # a head of a non-empty sequence with nothing selected
+    mask[2, 5] = False
+    table = torch.randperm(B * per, generator=g).view(B, per).to(torch.int32)
+    kp = torch.zeros(B * per, ps, Hkv, D, dtype=torch.bfloat16)
+    vp = torch.zeros(B * per, ps, Hkv, D, dtype=torch.bfloat16)
+    for b in range(B):
+        for j in range(per):
+            kp[table[b, j]] = k[b, :, j * ps:(j + 1) * ps].transpose(0, 1)
+            vp[table[b, j]] = v[b, :, j * ps:(j + 1) * ps].transpose(0, 1)
+    bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
+    contig = bsfa.forward_decode(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                 kv_lens=lens.to(dev), num_splits=splits)
+    paged = bsfa.forward_decode_paged(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                      lens.to(dev), mask.to(dev), num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(paged, contig)
+    out = contig.cpu()
+    assert (out[0] == 0).all() and (out[3] == 0).all()
+    assert (out[1, 3] == 0).all() and (out[2, 5] == 0).all()
+    assert torch.isfinite(out.float()).all()
+    ref = orc.sparse_decode(to_np(q), to_np(k), to_np(v), mask.numpy(), bs, kv_lens=lens.numpy())
+    assert_close_bf16(contig, ref, f"decode empty rows splits={splits}")
