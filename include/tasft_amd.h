@@ -36,7 +36,7 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (7). */
+/* ABI version of this library (8). */
 int tasft_abi_version(void);
 
 /* Element types of the 16-bit tensors (the `dtype` argument). The reference kernel takes
@@ -253,6 +253,37 @@ int tasft_gate_rows_fwd(const float* uq, const float* uk, const float* w_out,
                         int64_t num_q_heads, int64_t num_kv_heads, int64_t rows,
                         int64_t key_blocks, int64_t row0, int64_t hidden, int64_t uk_head_stride,
                         int flags, void* stream);
+
+/*
+ * One cached decode step's gate rows with the state update folded in: what
+ * SparseAttentionDecoder does per token before its decode (the running block sums, the
+ * projection of the current key block and of the query heads, then tasft_gate_rows_fwd's
+ * row), in one launch per (b, KV head). No reference counterpart: the reference gate
+ * rejects S_q != S_k (tasft/modules/attn_gate.py:216-221).
+ *
+ * q_new [B, Hq, D] and k_new [B, Hkv, D] 16-bit (dtype), with (b, head) strides
+ * q_strides[0..1] / k_strides[0..1] and D contiguous: the new token. q_sum [B, Hq, D] and
+ * k_sum [B, Hkv, D] fp32 contiguous: the sums of the current block's queries and keys before
+ * this token, updated in place (reset_sums != 0 starts a new block: the sums are replaced by
+ * the token). uk: the kept key units, block j of (b, KV head g) at uk[(b * Hkv + g) *
+ * uk_head_stride + j * hidden] (16-byte aligned; uk_head_stride a multiple of 4 holding at
+ * least row + 1 blocks); block `row` (the token's block) is rewritten with
+ * k_sum x wk_t. wq_t and wk_t [D, hidden] fp32: W_in[:, :D] and W_in[:, D:] transposed and
+ * divided by the block size (a zero-padded block mean is then sum x W); b_in, w_out
+ * [hidden]; thresholds [Hq]. Outputs [B, Hq, 1, row + 1] contiguous: soft_scores (sigmoid
+ * of w_out . relu(q_sum x wq_t + b_in + v_j)), hard_mask (soft >= tau, and the diagonal
+ * j = row with TASFT_GATE_FORCE_DIAGONAL). active_count is zeroed and counted by the call.
+ * Limits: Hq / Hkv <= 8, head_dim <= 256, hidden <= 256 and a multiple of 4.
+ */
+int tasft_gate_decode_rows_fwd(const void* q_new, const void* k_new, const int64_t* q_strides,
+                               const int64_t* k_strides, float* q_sum, float* k_sum, float* uk,
+                               int64_t uk_head_stride, const float* wq_t, const float* wk_t,
+                               const float* b_in, const float* w_out, const float* thresholds,
+                               float* soft_scores, uint8_t* hard_mask,
+                               unsigned long long* active_count, int64_t batch,
+                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                               int64_t hidden, int64_t row, int reset_sums, int flags, int dtype,
+                               void* stream);
 
 /*
  * Backward of the gate's pairwise MLP, for gate training: the gradient the reference gets

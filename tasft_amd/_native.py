@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
     "tasft_gate_rows_fwd",
+    "tasft_gate_decode_rows_fwd",
     "tasft_gate_bwd_workspace_bytes",
     "tasft_gate_bwd",
     "tasft_gate_target_fwd",
@@ -89,6 +90,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_gate_rows_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P],
+    ),
+    "tasft_gate_decode_rows_fwd": (
+        _I,
+        [_P, _P, _I64P, _I64P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+         _I64, _I64, _I64, _I64, _I, _I, _I, _P],
     ),
     "tasft_gate_bwd_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "tasft_gate_bwd": (

@@ -25,6 +25,7 @@
 // waits for another within a launch. Otherwise one pooling launch (streaming for block 64,
 // generic else) is followed by gate_pairwise_kernel.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -713,6 +714,161 @@ gate_qpool_pair64_kernel(const GatePoolParams p, const GatePairParams q) {
   }
 }
 
+// One cached decode step's gate rows, for a KV head and its G <= kRowMaxG query heads per
+// workgroup. It adds the new token's key and queries to the running sums of its block
+// (reset first at a block start), projects the sums (W_in halves transposed with 1/block
+// folded in, so a zero-padded block mean is sum x W), stores the key unit of the
+// current block `row` among the kept units, and evaluates the rows of the G heads against
+// key blocks 0 .. row: logit = w_out . relu(u + v_j), sigmoid, per-head tau, the forced
+// diagonal. Thread j takes key block j (and j + 256, ...), all G heads at once.
+constexpr int kRowMaxG = 8;
+constexpr int kRowMaxHid = 256;
+
+struct GateDecodeRowParams {
+  const uint16_t* q_new;  // [B, Hq, D] (16-bit), strides sq
+  const uint16_t* k_new;  // [B, Hkv, D], strides sk
+  int64_t sq[2], sk[2];
+  float* q_sum;           // [B, Hq, D]
+  float* k_sum;           // [B, Hkv, D]
+  float* uk;              // kept key units, block j of (b, KV head g) at (b*Hkv+g)*uk_stride + j*hidden
+  int64_t uk_stride;
+  const float* wq_t;      // [D, hidden]
+  const float* wk_t;      // [D, hidden]
+  const float* b_in;      // [hidden]
+  const float* w_out;     // [hidden]
+  const float* tau;       // [Hq]
+  float* soft;            // [B, Hq, 1, row + 1]
+  uint8_t* mask;          // [B, Hq, 1, row + 1]
+  unsigned long long* counter;
+  int B, Hq, Hkv, G, D, hidden, row, reset, force_diag;
+};
+
+// MG: the query heads per KV head rounded up to 1, 2, 4 or 8; heads G .. MG - 1 are zero and
+// never stored, so the loops carry no per-head branch.
+template <int DT, int MG>
+__global__ void __launch_bounds__(256)
+gate_decode_row_kernel(const GateDecodeRowParams p) {
+  __shared__ float ks[kGateMaxD];
+  __shared__ float qs[MG][kGateMaxD];
+  __shared__ __attribute__((aligned(16))) float u[MG][kRowMaxHid];
+  __shared__ __attribute__((aligned(16))) float vrow[kRowMaxHid];
+  __shared__ float wo[kRowMaxHid];
+  __shared__ unsigned int wave_count[4];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int b = blockIdx.x / p.Hkv, kvh = blockIdx.x % p.Hkv;
+  const int h0 = kvh * p.G;
+  const int D = p.D, hid = p.hidden;
+  for (int d = tid; d < D; d += 256) {
+    const float kn = bits16_to_f32<DT>(p.k_new[b * p.sk[0] + kvh * p.sk[1] + d]);
+    float* ksp = p.k_sum + ((int64_t)b * p.Hkv + kvh) * D + d;
+    const float v = (p.reset ? 0.f : *ksp) + kn;
+    *ksp = v;
+    ks[d] = v;
+  }
+  for (int e = tid; e < MG * D; e += 256) {
+    const int g = e / D, d = e % D, h = h0 + g;
+    if (g >= p.G) {
+      qs[g][d] = 0.f;
+      continue;
+    }
+    const float qn = bits16_to_f32<DT>(p.q_new[b * p.sq[0] + h * p.sq[1] + d]);
+    float* qsp = p.q_sum + ((int64_t)b * p.Hq + h) * D + d;
+    const float v = (p.reset ? 0.f : *qsp) + qn;
+    *qsp = v;
+    qs[g][d] = v;
+  }
+  for (int c = tid; c < hid; c += 256) wo[c] = p.w_out[c];
+  __syncthreads();
+  float* ukb = p.uk + ((int64_t)b * p.Hkv + kvh) * p.uk_stride;
+  {
+    // Projections. Up to 128 hidden units, two threads per unit, each over half of d
+    // (partial sums meet in LDS); above that one thread per unit. The loads of eight d run
+    // ahead of their FMAs.
+    const int per = hid <= 128 ? 128 : 256;
+    const int nsp = 256 / per;
+    const int c = tid % per, sp = tid / per;
+    const int d0 = sp * D / nsp, d1 = (sp + 1) * D / nsp;
+    float vk = 0.f;
+    float acc[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g) acc[g] = 0.f;
+    if (c < hid) {
+#pragma unroll 8
+      for (int d = d0; d < d1; ++d) {
+        const float wk = p.wk_t[(int64_t)d * hid + c];
+        const float wq = p.wq_t[(int64_t)d * hid + c];
+        vk = fmaf(ks[d], wk, vk);
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+          acc[g] = fmaf(qs[g][d], wq, acc[g]);
+      }
+    }
+    if (nsp == 2 && sp == 1 && c < hid) {
+      vrow[c] = vk;
+#pragma unroll
+      for (int g = 0; g < MG; ++g)
+        u[g][c] = acc[g];
+    }
+    __syncthreads();
+    if (sp == 0 && c < hid) {
+      if (nsp == 2) {
+        vk += vrow[c];
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+          acc[g] += u[g][c];
+      }
+      vrow[c] = vk;
+      ukb[(int64_t)p.row * hid + c] = vk;
+      const float bias = p.b_in[c];
+#pragma unroll
+      for (int g = 0; g < MG; ++g)
+        u[g][c] = acc[g] + bias;
+    }
+  }
+  __syncthreads();
+  const int nbk = p.row + 1;
+  unsigned int active = 0;
+  for (int j = tid; j < nbk; j += 256) {
+    float acc[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g) acc[g] = 0.f;
+    // Block `row` was stored above by this workgroup (visible after the barrier), so every
+    // key block is read from the kept units with plain global loads.
+    const float* vj = ukb + (int64_t)j * hid;
+#pragma unroll 8
+    for (int c = 0; c < hid; c += 4) {
+      const f32x4_t v4 = *(const f32x4_t*)(vj + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float w = wo[c + e];
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+          acc[g] = fmaf(w, fmaxf(u[g][c + e] + v4[e], 0.f), acc[g]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < MG; ++g) {
+      if (g >= p.G) break;
+      const int h = h0 + g;
+      const float sv = 1.f / (1.f + expf(-acc[g]));
+      const bool on = sv >= p.tau[h] || (p.force_diag && j == p.row);
+      const int64_t o = ((int64_t)b * p.Hq + h) * nbk + j;
+      p.soft[o] = sv;
+      p.mask[o] = on ? 1 : 0;
+      active += on ? 1u : 0u;
+    }
+  }
+  const float tot = wave_sum((float)active);
+  if (lane == 0) wave_count[wave] = (unsigned int)(tot + 0.5f);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int t = (wave_count[0] + wave_count[1]) + (wave_count[2] + wave_count[3]);
+    if (t) atomicAdd(p.counter, (unsigned long long)t);
+  }
+}
+
 __global__ void gate_counter_reset_kernel(unsigned long long* counter) {
   if (threadIdx.x == 0) *counter = 0ull;
 }
@@ -1172,5 +1328,92 @@ extern "C" int tasft_gate_rows_fwd(const float* uq, const float* uk, const float
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate_rows: launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}
+
+extern "C" int tasft_gate_decode_rows_fwd(
+    const void* q_new, const void* k_new, const int64_t* q_strides, const int64_t* k_strides,
+    float* q_sum, float* k_sum, float* uk, int64_t uk_head_stride, const float* wq_t,
+    const float* wk_t, const float* b_in, const float* w_out, const float* thresholds,
+    float* soft_scores, uint8_t* hard_mask, unsigned long long* active_count, int64_t batch,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t hidden, int64_t row,
+    int reset_sums, int flags, int dtype, void* stream) {
+  if (!q_new || !k_new || !q_strides || !k_strides || !q_sum || !k_sum || !uk || !wq_t ||
+      !wk_t || !b_in || !w_out || !thresholds || !soft_scores || !hard_mask || !active_count)
+    return set_error(kErrInvalidArgument, "gate_decode_rows: null pointer argument");
+  if (dtype != kBf16 && dtype != kF16)
+    return set_error(kErrUnsupported, "gate_decode_rows: dtype must be bf16 (0) or fp16 (1), got %d",
+                     dtype);
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || hidden <= 0 ||
+      row < 0)
+    return set_error(kErrInvalidArgument, "gate_decode_rows: sizes must be positive (row >= 0)");
+  if (num_q_heads % num_kv_heads != 0)
+    return set_error(kErrInvalidArgument,
+                     "gate_decode_rows: num_q_heads must be a multiple of num_kv_heads");
+  const int64_t G = num_q_heads / num_kv_heads;
+  if (G > kRowMaxG || head_dim > kGateMaxD || hidden > kRowMaxHid || hidden % 4 != 0)
+    return set_error(kErrUnsupported,
+                     "gate_decode_rows: needs at most %d query heads per KV head, head_dim <= %d "
+                     "and hidden <= %d, a multiple of 4 (got %lld, %lld, %lld)",
+                     kRowMaxG, kGateMaxD, kRowMaxHid, (long long)G, (long long)head_dim,
+                     (long long)hidden);
+  if (uk_head_stride < (row + 1) * hidden || uk_head_stride % 4 != 0 ||
+      (((uintptr_t)uk) & 15u))
+    return set_error(kErrInvalidArgument,
+                     "gate_decode_rows: uk_head_stride must hold row + 1 blocks and be a multiple "
+                     "of 4, uk 16-byte aligned");
+  if (!strides_nonneg(q_strides, 2) || !strides_nonneg(k_strides, 2))
+    return set_error(kErrInvalidArgument, "gate_decode_rows: strides must be non-negative");
+  if (batch * num_kv_heads > 0x7fffffffLL || row >= 0x3fffffffLL)
+    return set_error(kErrUnsupported, "gate_decode_rows: problem too large for one launch");
+  GateDecodeRowParams rp;
+  rp.q_new = (const uint16_t*)q_new;
+  rp.k_new = (const uint16_t*)k_new;
+  for (int j = 0; j < 2; ++j) {
+    rp.sq[j] = q_strides[j];
+    rp.sk[j] = k_strides[j];
+  }
+  rp.q_sum = q_sum;
+  rp.k_sum = k_sum;
+  rp.uk = uk;
+  rp.uk_stride = uk_head_stride;
+  rp.wq_t = wq_t;
+  rp.wk_t = wk_t;
+  rp.b_in = b_in;
+  rp.w_out = w_out;
+  rp.tau = thresholds;
+  rp.soft = soft_scores;
+  rp.mask = hard_mask;
+  rp.counter = active_count;
+  rp.B = (int)batch;
+  rp.Hq = (int)num_q_heads;
+  rp.Hkv = (int)num_kv_heads;
+  rp.G = (int)G;
+  rp.D = (int)head_dim;
+  rp.hidden = (int)hidden;
+  rp.row = (int)row;
+  rp.reset = reset_sums ? 1 : 0;
+  rp.force_diag = (flags & 2) ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(gate_counter_reset_kernel, dim3(1), dim3(64), 0, s, active_count);
+  const dim3 grid((unsigned)(batch * num_kv_heads));
+  auto launch = [&](auto mg) {
+    constexpr int MG = decltype(mg)::value;
+    if (dtype == kF16)
+      hipLaunchKernelGGL((gate_decode_row_kernel<kF16, MG>), grid, dim3(256), 0, s, rp);
+    else
+      hipLaunchKernelGGL((gate_decode_row_kernel<kBf16, MG>), grid, dim3(256), 0, s, rp);
+  };
+  if (G == 1)
+    launch(std::integral_constant<int, 1>());
+  else if (G == 2)
+    launch(std::integral_constant<int, 2>());
+  else if (G <= 4)
+    launch(std::integral_constant<int, 4>());
+  else
+    launch(std::integral_constant<int, 8>());
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "gate_decode_rows: launch failed: %s", hipGetErrorString(err));
   return kOk;
 }

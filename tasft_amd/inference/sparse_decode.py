@@ -12,7 +12,9 @@ far; the key means are those of every key block so far (the last one zero-padded
 Per step nothing is pooled again: the state keeps the projected key units
 ``v_j = W_k kbar_j`` ([B, Hkv, blocks, hidden] fp32, from the prefill gate's workspace) and
 the running sums of the current block's keys and queries, updates the one changing block,
-and evaluates the row with ``tasft_gate_rows_fwd``. The row feeds
+and evaluates the row. With at most 8 query heads per KV head that is one call,
+``tasft_gate_decode_rows_fwd``; otherwise torch updates the sums and projections and
+``tasft_gate_rows_fwd`` evaluates the row. The row feeds
 ``BlockSparseFlashAttention.forward_decode`` with the KV cache in its GQA layout
 (``Hkv`` heads, never repeat-interleaved as ``tasft/inference/tasft_model.py:267-271`` does).
 """
@@ -24,7 +26,11 @@ import torch
 
 from tasft_amd import _native
 from tasft_amd.exceptions import KernelError
-from tasft_amd.kernels.block_sparse_fa import BlockSparseFlashAttention
+from tasft_amd.kernels.block_sparse_fa import (
+    _VALID_HEAD_DIMS,
+    BlockSparseFlashAttention,
+    default_decode_splits,
+)
 from tasft_amd.modules.attn_gate import AttnGate, GateOutput, _launch_gate
 
 
@@ -49,6 +55,7 @@ class SparseAttentionDecoder:
         self._vk = None
         self._ksum = None
         self._qsum = None
+        self._ws: dict[int, tuple[torch.Tensor, int]] = {}  # decode workspace per split count
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -106,24 +113,40 @@ class SparseAttentionDecoder:
         if t >= self.max_len:
             raise KernelError(f"KV cache full: max_len={self.max_len}", context={"length": t})
         i = t // bs
-        if t % bs == 0:
-            self._ksum.zero_()
-            self._qsum.zero_()
-        self._ksum.add_(k_new[:, :, 0])
-        self._qsum.add_(q_new[:, :, 0])
         hid = self.gate.gate_hidden_dim
-        self._vk[:, :, i] = torch.matmul(self._ksum, self._wk_t)
-        uq = torch.addmm(self._b_in, self._qsum.view(B * Hq, D), self._wq_t).view(B, Hq, 1, hid)
         nbk = i + 1
-        soft = torch.empty((B, Hq, 1, nbk), dtype=torch.float32, device=q_new.device)
-        mask = torch.empty((B, Hq, 1, nbk), dtype=torch.uint8, device=q_new.device)
-        active = torch.empty((1,), dtype=torch.int64, device=q_new.device)
+        dev = q_new.device
+        soft = torch.empty((B, Hq, 1, nbk), dtype=torch.float32, device=dev)
+        mask = torch.empty((B, Hq, 1, nbk), dtype=torch.uint8, device=dev)
+        active = torch.empty((1,), dtype=torch.int64, device=dev)
         lib = _native.load_library()
-        status = lib.tasft_gate_rows_fwd(
-            uq.data_ptr(), self._vk.data_ptr(), self._w_out.data_ptr(), self._taus.data_ptr(),
-            soft.data_ptr(), None, mask.data_ptr(), active.data_ptr(), B, Hq, Hkv, 1, nbk, i, hid,
-            self._vk.shape[2] * hid, self._flags, _native.stream_handle(q_new.device))
-        _native.check(status, "tasft_gate_rows_fwd", {"position": t})
+        if (Hq // Hkv <= 8 and D <= 256 and hid <= 256 and hid % 4 == 0
+                and q_new.dtype in (torch.bfloat16, torch.float16) and k_new.dtype == q_new.dtype
+                and q_new.stride(-1) == 1 and k_new.stride(-1) == 1):
+            # One launch per (b, KV head): block sums, both projections, the kept key unit of
+            # block i and the rows (tasft_gate_decode_rows_fwd).
+            status = lib.tasft_gate_decode_rows_fwd(
+                q_new.data_ptr(), k_new.data_ptr(), _native.strides(q_new), _native.strides(k_new),
+                self._qsum.data_ptr(), self._ksum.data_ptr(), self._vk.data_ptr(),
+                self._vk.shape[2] * hid, self._wq_t.data_ptr(), self._wk_t.data_ptr(),
+                self._b_in.data_ptr(), self._w_out.data_ptr(), self._taus.data_ptr(),
+                soft.data_ptr(), mask.data_ptr(), active.data_ptr(), B, Hq, Hkv, D, hid, i,
+                1 if t % bs == 0 else 0, self._flags, _native.dtype_code(q_new.dtype, "decode rows"),
+                _native.stream_handle(dev))
+            _native.check(status, "tasft_gate_decode_rows_fwd", {"position": t})
+        else:
+            if t % bs == 0:
+                self._ksum.zero_()
+                self._qsum.zero_()
+            self._ksum.add_(k_new[:, :, 0])
+            self._qsum.add_(q_new[:, :, 0])
+            self._vk[:, :, i] = torch.matmul(self._ksum, self._wk_t)
+            uq = torch.addmm(self._b_in, self._qsum.view(B * Hq, D), self._wq_t).view(B, Hq, 1, hid)
+            status = lib.tasft_gate_rows_fwd(
+                uq.data_ptr(), self._vk.data_ptr(), self._w_out.data_ptr(), self._taus.data_ptr(),
+                soft.data_ptr(), None, mask.data_ptr(), active.data_ptr(), B, Hq, Hkv, 1, nbk, i, hid,
+                self._vk.shape[2] * hid, self._flags, _native.stream_handle(dev))
+            _native.check(status, "tasft_gate_rows_fwd", {"position": t})
         self.length = t + 1
         return GateOutput(soft_scores=soft, hard_mask=mask.view(torch.bool), num_blocks_q=1,
                           num_blocks_k=nbk, active_count=active)
@@ -139,8 +162,39 @@ class SparseAttentionDecoder:
             raise KernelError(f"KV cache holds {k_cache.shape[2]} tokens, expected {t + 1}",
                               context={"cache_len": k_cache.shape[2], "length": t})
         row = self.select(q_new, k_cache[:, :, t:t + 1])
-        out = self.bsfa.forward_decode(q_new, k_cache, v_cache, row.hard_mask)
-        return out, row
+        return self._decode(q_new, k_cache, v_cache, row.hard_mask), row
+
+    def _decode(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                mask: torch.Tensor) -> torch.Tensor:
+        """``tasft_bsfa_decode_fwd`` on the step's row, called directly when the layouts suit
+        the kernel as they are (the shapes are the decoder's own, already consistent), with
+        the workspace kept between steps; ``forward_decode`` (validation, copies) otherwise."""
+        B, Hq, _, D = q.shape
+        Hkv, S_kv = k_cache.shape[1], k_cache.shape[2]
+        ready = (D in _VALID_HEAD_DIMS and q.dtype in (torch.bfloat16, torch.float16)
+                 and k_cache.dtype == q.dtype and v_cache.dtype == q.dtype and q.is_cuda
+                 and all(t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1])
+                         and t.data_ptr() % 16 == 0 for t in (q, k_cache, v_cache)))
+        if not ready:
+            return self.bsfa.forward_decode(q, k_cache, v_cache, mask)
+        lib = _native.load_library()
+        nb = mask.shape[-1]
+        splits = default_decode_splits(B, Hkv, nb, Hq // Hkv)
+        ws = self._ws.get(splits)
+        if ws is None:
+            n = lib.tasft_bsfa_decode_workspace_bytes(B, Hq, D, splits)
+            ws = (torch.empty(n, dtype=torch.uint8, device=q.device), n)
+            self._ws[splits] = ws
+        out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+        m8 = mask.view(torch.uint8)
+        status = lib.tasft_bsfa_decode_fwd(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), m8.data_ptr(),
+            None, ws[0].data_ptr(), ws[1], B, Hq, Hkv, S_kv, D, self.bsfa.block_size, splits,
+            _native.strides(q), _native.strides(k_cache), _native.strides(v_cache),
+            _native.strides(out), _native.strides(m8), 1.0 / math.sqrt(D),
+            _native.dtype_code(q.dtype, "decode"), _native.stream_handle(q.device))
+        _native.check(status, "tasft_bsfa_decode_fwd", {"shape": [B, Hq, S_kv, D]})
+        return out
 
 
 __all__ = ["SparseAttentionDecoder"]

@@ -23,6 +23,9 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize(("B", "Hq", "Hkv", "D", "hid", "S0", "steps"), [
     (2, 8, 2, 128, 64, 1021, 5),    # crosses the block boundary at 1024
     (1, 4, 4, 64, 32, 128, 3),      # prompt of whole blocks, MHA, D=64
+    (1, 16, 2, 128, 128, 2045, 4),  # 8 query heads per KV head (one launch per step), boundary
+    (2, 8, 1, 64, 320, 190, 3),     # hidden 320 (> 256): torch state update +
+                                    # tasft_gate_rows_fwd
 ])
 def test_cached_decode_steps_match_oracle(B, Hq, Hkv, D, hid, S0, steps):
     dev = require_gpu()

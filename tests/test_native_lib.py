@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace_sizes():
     lib = _native.load_library()
-    assert lib.tasft_abi_version() == 7
+    assert lib.tasft_abi_version() == 8
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 8192, 64) == 256
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 0, 64) == 0
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
@@ -123,6 +123,9 @@ def test_dtype_codes_other_than_bf16_and_fp16_are_rejected():
         "gate_target": lambda dt: lib.tasft_gate_target_fwd(
             fake, fake, None, fake, 1, 32, 8, 1024, 128, 64, st, st, None, 1.0, 1, 0, 1.0, 0.0, dt,
             None),
+        "gate_decode_rows": lambda dt: lib.tasft_gate_decode_rows_fwd(
+            fake, fake, st, st, fake, fake, fake, 4096, fake, fake, fake, fake, fake, fake, fake,
+            fake, 1, 32, 8, 128, 128, 3, 0, 2, dt, None),
     }
     for name, call in calls.items():
         for dt in (2, -1):
@@ -156,6 +159,9 @@ def test_negative_strides_are_rejected_before_any_launch():
         "gate_target": lambda s4, s3, m: lib.tasft_gate_target_fwd(
             fake, fake, None, fake, 1, 32, 8, 1024, 128, 64, s4, st, None, 1.0, 1, 0, 1.0, 0.0, 0,
             None),
+        "gate_decode_rows": lambda s4, s3, m: lib.tasft_gate_decode_rows_fwd(
+            fake, fake, st, s4, fake, fake, fake, 4096, fake, fake, fake, fake, fake, fake, fake,
+            fake, 1, 32, 8, 128, 128, 3, 0, 2, 0, None),
     }
     for name, call in calls.items():
         rc = call(neg, neg3, st)
@@ -175,3 +181,25 @@ def test_check_raises_kernel_error_with_message():
                                    1.0, 0.0, 0, None)
     with pytest.raises(KernelError, match="null pointer"):
         _native.check(rc, "tasft_gate_target_fwd")
+
+
+def test_gate_decode_rows_limits_are_checked_before_any_launch():
+    """The one-launch decode rows take at most 8 query heads per KV head, head_dim and hidden
+    up to 256 (hidden a multiple of 4) and a kept-unit stride that holds the current block;
+    outside that the call returns an error without touching the GPU."""
+    lib = _native.load_library()
+    st = _i64([0, 0, 0, 1])
+    fake = ctypes.c_void_p(16)
+
+    def call(hq, hkv, d, hid, row, stride):
+        return lib.tasft_gate_decode_rows_fwd(
+            fake, fake, st, st, fake, fake, fake, stride, fake, fake, fake, fake, fake, fake, fake,
+            fake, 1, hq, hkv, d, hid, row, 0, 2, 0, None)
+
+    assert call(32, 2, 128, 128, 3, 4096) == -2 and b"8 query heads" in lib.tasft_last_error()
+    assert call(32, 8, 512, 128, 3, 4096) == -2
+    assert call(32, 8, 128, 260, 3, 4096) == -2
+    assert call(32, 8, 128, 126, 3, 4096) == -2
+    assert call(32, 8, 128, 128, 40, 4096) == -1 and b"uk_head_stride" in lib.tasft_last_error()
+    assert call(32, 8, 128, 128, -1, 4096) == -1
+    assert call(30, 8, 128, 128, 3, 4096) == -1 and b"multiple" in lib.tasft_last_error()
