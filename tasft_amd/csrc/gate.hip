@@ -906,7 +906,7 @@ struct GateBwdParams {
   int B, Hq, Hkv, G, NB, hidden, causal, tiles;
 };
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
 gate_pairwise_bwd_kernel(const GateBwdParams p) {
   __shared__ float g_t[kBwdTile][kBwdTile + 1];
   __shared__ float uq_s[kBwdTile][kBwdHC + 1];
@@ -969,6 +969,7 @@ gate_pairwise_bwd_kernel(const GateBwdParams p) {
       su[e] = 0.f;
       sw[e] = 0.f;
     }
+#pragma unroll 4
     for (int jj = 0; jj < kBwdTile; ++jj) {
       const float g = g_t[r][jj];
 #pragma unroll
@@ -1007,6 +1008,7 @@ gate_pairwise_bwd_kernel(const GateBwdParams p) {
       bv[e] = uk_s[r][8 * ug + e];
       sv[e] = 0.f;
     }
+#pragma unroll 4
     for (int ii = 0; ii < kBwdTile; ++ii) {
       const float g = g_t[ii][r];
 #pragma unroll
