@@ -27,13 +27,13 @@ pytestmark = pytest.mark.gpu
     (2, 8, 1, 64, 320, 190, 3),     # hidden 320 (> 256): torch state update +
                                     # tasft_gate_rows_fwd
 ])
-def test_cached_decode_steps_match_oracle(B, Hq, Hkv, D, hid, S0, steps):
+def test_cached_decode_steps_match_oracle(B, Hq, Hkv, D, hid, S0, steps, dtype=torch.bfloat16):
     dev = require_gpu()
     bs = 64
     n = S0 + steps
-    q = wl.randn_bf16((B, Hq, n, D), 71 + n, scale=1.0)
-    k = wl.randn_bf16((B, Hkv, n, D), 72 + n, scale=1.0)
-    v = wl.randn_bf16((B, Hkv, n, D), 73 + n, scale=1.0)
+    q = wl.randn_bf16((B, Hq, n, D), 71 + n, scale=1.0).to(dtype)
+    k = wl.randn_bf16((B, Hkv, n, D), 72 + n, scale=1.0).to(dtype)
+    v = wl.randn_bf16((B, Hkv, n, D), 73 + n, scale=1.0).to(dtype)
     torch.manual_seed(n)
     gate = AttnGate(num_heads=Hq, head_dim=D, block_size=bs, gate_hidden_dim=hid).to(dev).requires_grad_(False)
     tau = 0.5
@@ -65,3 +65,9 @@ def test_cached_decode_steps_match_oracle(B, Hq, Hkv, D, hid, S0, steps):
                                 row.hard_mask.cpu().numpy(), bs)
         assert_close_bf16(out, ref, f"decode step {t}")
     assert dec.length == n
+
+
+def test_cached_decode_steps_fp16():
+    """fp16 prompt and cache (the same values as a bf16 draw, exact in fp16 at this scale):
+    the one-launch rows and the decode run their fp16 instantiations."""
+    test_cached_decode_steps_match_oracle(1, 8, 2, 128, 64, 509, 4, dtype=torch.float16)
