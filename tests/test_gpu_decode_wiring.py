@@ -24,6 +24,7 @@ pytestmark = pytest.mark.gpu
     (2, 8, 2, 128, 64, 1021, 5),    # crosses the block boundary at 1024
     (1, 4, 4, 64, 32, 128, 3),      # prompt of whole blocks, MHA, D=64
     (1, 16, 2, 128, 128, 2045, 4),  # 8 query heads per KV head (one launch per step), boundary
+    (1, 8, 2, 64, 64, 8250, 2),     # 130 key blocks: one thread per block in the row kernel
     (2, 8, 1, 64, 320, 190, 3),     # hidden 320 (> 256): torch state update +
                                     # tasft_gate_rows_fwd
 ])
@@ -37,7 +38,7 @@ def test_cached_decode_steps_match_oracle(B, Hq, Hkv, D, hid, S0, steps, dtype=t
     torch.manual_seed(n)
     gate = AttnGate(num_heads=Hq, head_dim=D, block_size=bs, gate_hidden_dim=hid).to(dev).requires_grad_(False)
     tau = 0.5
-    dec = SparseAttentionDecoder(gate, tau, max_len=4096)
+    dec = SparseAttentionDecoder(gate, tau, max_len=max(4096, n))
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     out_p, g_p = dec.prefill(qd[:, :, :S0], kd[:, :, :S0], vd[:, :, :S0])
     w_in = gate.gate_proj_in.weight.cpu().numpy()
