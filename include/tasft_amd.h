@@ -58,12 +58,14 @@ int tasft_abi_version(void);
  * Rows with no admissible key are 0. P is rounded to `dtype` before the PV product.
  * block_mask: [B, Hq, ceil(S/bs), ceil(S/bs)] bytes, strides in mask_strides (bytes).
  * head_dim in {64, 128}; block_size in {32, 64, 128}; strides of b/h/s multiples of 8.
+ * Block size 128 runs on the block-64 kernels, each 128-token block as its four 64-token
+ * quarters (the same tokens attend to the same keys).
  * workspace: NULL (one workgroup per query-block row), or >=
- * tasft_bsfa_prefill_workspace_bytes(...) bytes, 16-byte aligned: then (block size 64,
- * head_dim 64) a persistent launch keeps every CU slot busy, pulling rows from ticket
- * counters kept in the workspace (zeroed on `stream` by the call itself). Block size 64
- * with head_dim 128 always runs one workgroup per row (its two-wave kernel fills four
- * slots per CU) and leaves the workspace untouched. The output does not depend on it.
+ * tasft_bsfa_prefill_workspace_bytes(...) bytes, 16-byte aligned: then (block size 64 or
+ * 128, head_dim 64) a persistent launch keeps every CU slot busy, pulling rows from ticket
+ * counters kept in the workspace (zeroed on `stream` by the call itself). head_dim 128
+ * always runs one workgroup per row (its two-wave kernel fills four slots per CU) and
+ * leaves the workspace untouched. The output does not depend on it.
  * Calls that share one workspace must be ordered on one stream.
  */
 int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* v, void* out,

@@ -48,6 +48,10 @@ struct PrefillParams {
   // of dimension s (the b strides are 0), S is the longest length and NB its block count.
   // Null for a dense [B, H, S, D] launch.
   const int* cu_seqlens;
+  // Mask index shift: 64-token query block qb and key block kb read mask entry
+  // (qb >> mshift, kb >> mshift). 1 runs a block-128 mask on the block-64 kernels (a
+  // 128-token block is active iff each of its 64-token quarters is); 0 otherwise.
+  int mshift;
 };
 
 // Static order of the (batch, query head, query block) work items. gfx950 dispatches
@@ -143,7 +147,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
   const uint16_t* kbase = p.k + b * p.sk[0] + span.tok0 * p.sk[2] + kvh * p.sk[1];
   const uint16_t* vbase = p.v + b * p.sv[0] + span.tok0 * p.sv[2] + kvh * p.sv[1];
   uint16_t* obase = p.o + b * p.so[0] + span.tok0 * p.so[2] + h * p.so[1];
-  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
+  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)(qb >> p.mshift) * p.sm[2];
 
   // Q^T as the B operand: lane (col, half) holds query row `qrow`, head dims
   // ks*16 + half*8 .. +7 for every k-step.
@@ -167,7 +171,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
   for (int chunk = 0; chunk < kb_end; chunk += kWave) {
     // Every wave reads the same 64 mask bytes, so all waves walk the same key blocks.
     const int kbl = chunk + lane;
-    const bool act = (kbl < kb_end) && (mrow[(int64_t)kbl * p.sm[3]] != 0);
+    const bool act = (kbl < kb_end) && (mrow[(int64_t)(kbl >> p.mshift) * p.sm[3]] != 0);
     uint64_t bits = __ballot(act);
     while (bits) {
       const int kb = chunk + __builtin_ctzll(bits);
@@ -346,12 +350,13 @@ __device__ __forceinline__ int swz_v(int r, int cc) {
 // Next active key block of a mask row, scanning 64 mask bytes per ballot. Returns -1 at
 // the end. All lanes of all waves see the same sequence.
 __device__ __forceinline__ int next_active_block(const uint8_t* mrow, int64_t stride, int kb_end,
-                                                 int lane, int& chunk, uint64_t& bits) {
+                                                 int lane, int& chunk, uint64_t& bits,
+                                                 int mshift) {
   while (bits == 0) {
     chunk += kWave;
     if (chunk >= kb_end) return -1;
     const int kbl = chunk + lane;
-    bits = __ballot(kbl < kb_end && mrow[(int64_t)kbl * stride] != 0);
+    bits = __ballot(kbl < kb_end && mrow[(int64_t)(kbl >> mshift) * stride] != 0);
   }
   const int kb = chunk + __builtin_ctzll(bits);
   bits &= bits - 1;
@@ -451,7 +456,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   const uint16_t* kbase = p.k + b * p.sk[0] + span.tok0 * p.sk[2] + kvh * p.sk[1];
   const uint16_t* vbase = p.v + b * p.sv[0] + span.tok0 * p.sv[2] + kvh * p.sv[1];
   uint16_t* obase = p.o + b * p.so[0] + span.tok0 * p.so[2] + h * p.so[1];
-  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
+  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)(qb >> p.mshift) * p.sm[2];
 
   const int qrow = qb * BS + rh * 32 + col;
   const bool qvalid = qrow < S;
@@ -464,7 +469,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   // DMA follows once the mask bytes are in, and only then the next item's mask bytes and
   // the ticket of the item after the next, which the first wait also covers.
   uint8_t mb = mbyte;
-  if (!pre && lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
+  if (!pre && lane < kb_end) mb = mrow[(int64_t)(lane >> p.mshift) * p.sm[3]];
   u32x4_t qf[KSTEPS];
   {
     // Rows past the end read row S-1: per-row results, never stored.
@@ -582,7 +587,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 
   int chunk = 0;
   uint64_t bits = __ballot(mb != 0);
-  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits, p.mshift);
   if (kb >= 0) issue(kA, vA, kb);
   mbyte = 0;
   pre = slot_nx < per_part;
@@ -590,8 +595,8 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     item_nx = prefill_item(p, p.parts == 8 ? part + 8 * slot_nx : slot_nx);
     const int kb_end_nx = p.causal ? item_nx.qb + 1 : p.NB;
     const uint8_t* mrow_nx =
-        p.mask + item_nx.b * p.sm[0] + item_nx.h * p.sm[1] + (int64_t)item_nx.qb * p.sm[2];
-    if (lane < kb_end_nx) mbyte = mrow_nx[(int64_t)lane * p.sm[3]];
+        p.mask + item_nx.b * p.sm[0] + item_nx.h * p.sm[1] + (int64_t)(item_nx.qb >> p.mshift) * p.sm[2];
+    if (lane < kb_end_nx) mbyte = mrow_nx[(int64_t)(lane >> p.mshift) * p.sm[3]];
   }
   // atomicInc (not atomicAdd, which the compiler rewrites into a wave-aggregated form that
   // waits for the result on the spot); the counter never reaches the wrap limit.
@@ -601,14 +606,14 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
   while (kb >= 0) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's DMA of block kb landed
     __syncthreads();                      // every wave's DMA landed; stage B is free
-    int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits, p.mshift);
     if (kb_next >= 0) issue(kB, vB, kb_next);
     compute(kA, vA, kb);
     kb = kb_next;
     if (kb < 0) break;
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
-    kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits, p.mshift);
     if (kb_next >= 0) issue(kA, vA, kb_next);
     compute(kB, vB, kb);
     kb = kb_next;
@@ -766,7 +771,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   const uint16_t* kbase = p.k + b * p.sk[0] + span.tok0 * p.sk[2] + kvh * p.sk[1];
   const uint16_t* vbase = p.v + b * p.sv[0] + span.tok0 * p.sv[2] + kvh * p.sv[1];
   uint16_t* obase = p.o + b * p.so[0] + span.tok0 * p.so[2] + h * p.so[1];
-  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)qb * p.sm[2];
+  const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)(qb >> p.mshift) * p.sm[2];
 
   const int qrow = qb * BS + wave * 32 + col;
   const bool qvalid = qrow < S;
@@ -775,7 +780,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   const int mask_from = p.causal ? qb : ((S % BS) != 0 ? NB - 1 : NB);
   // Loads in the order their results are needed: mask bytes, Q, then the first K DMA.
   uint8_t mb = 0;
-  if (lane < kb_end) mb = mrow[(int64_t)lane * p.sm[3]];
+  if (lane < kb_end) mb = mrow[(int64_t)(lane >> p.mshift) * p.sm[3]];
   u32x4_t qf[KSTEPS];
   {
     // Rows past the end read row S-1: per-row results, never stored.
@@ -802,7 +807,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
 
   int chunk = 0;
   uint64_t bits = __ballot(mb != 0);
-  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+  int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits, p.mshift);
   if (kb >= 0) dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb), kvoff, wave);
 
   while (kb >= 0) {
@@ -825,7 +830,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's K reads returned
     block_barrier();                      // every wave has read K(kb): the K tile is free
-    const int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits);
+    const int kb_next = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits, p.mshift);
     // Always eight DMA units after V(kb) (the last block of a row loads its own K tile
     // again), so the V wait below is one fixed count.
     dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb_next >= 0 ? kb_next : kb), kvoff, wave);
@@ -981,12 +986,21 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 template <int DT>
 static hipError_t launch_prefill_any(const PrefillParams& p, int* queue, int64_t head_dim,
                                      int64_t block_size, hipStream_t s) {
+  if (block_size == 128 && (head_dim == 128 || head_dim == 64)) {
+    // A block-128 mask on the block-64 kernels: each 128-token block is its four 64-token
+    // quarters, read through the mask index shift. The same tokens attend to the same
+    // keys; the online softmax merely visits them in 64-key steps (2.7x faster than
+    // the generic block-128 kernel at config-2 geometry).
+    PrefillParams q = p;
+    q.mshift = 1;
+    q.NB = (p.S + 63) / 64;
+    return head_dim == 128 ? launch_prefill_bs64<128, DT>(q, queue, s)
+                           : launch_prefill_bs64<64, DT>(q, queue, s);
+  }
   if (block_size == 64 && head_dim == 128) return launch_prefill_bs64<128, DT>(p, queue, s);
   if (block_size == 64 && head_dim == 64) return launch_prefill_bs64<64, DT>(p, queue, s);
-  if (block_size == 32 && head_dim == 128) return launch_prefill<32, 128, DT>(p, s);
-  if (block_size == 32 && head_dim == 64) return launch_prefill<32, 64, DT>(p, s);
-  if (block_size == 128 && head_dim == 128) return launch_prefill<128, 128, DT>(p, s);
-  return launch_prefill<128, 64, DT>(p, s);
+  if (head_dim == 128) return launch_prefill<32, 128, DT>(p, s);  // block 32
+  return launch_prefill<32, 64, DT>(p, s);
 }
 
 }  // namespace tasft
@@ -1050,7 +1064,9 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return set_error(kErrInvalidArgument, "prefill: tensors must be 16-byte aligned");
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  if (nb * batch * num_q_heads > 0x7fffffffLL || seq_len > 0x3fffffffLL)
+  // Block 128 runs on the block-64 kernels (launch_prefill_any): twice the query blocks.
+  if (nb * (block_size == 128 ? 2 : 1) * batch * num_q_heads > 0x7fffffffLL ||
+      seq_len > 0x3fffffffLL)
     return set_error(kErrUnsupported, "prefill: problem too large for one launch");
   const size_t ws_need = tasft_bsfa_prefill_workspace_bytes(batch, num_q_heads, seq_len, block_size);
   if (workspace) {
@@ -1088,6 +1104,7 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
   p.parts = 1;
   p.wg_per_part = 1;
   p.cu_seqlens = nullptr;
+  p.mshift = 0;
   // Ticket counters of the persistent launch (block size 64).
   return dispatch_prefill(p, (int*)workspace, head_dim, block_size, dtype, (hipStream_t)stream,
                           "prefill");
@@ -1139,7 +1156,8 @@ extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return set_error(kErrInvalidArgument, "prefill_varlen: tensors must be 16-byte aligned");
   const int64_t nb = (max_seqlen + block_size - 1) / block_size;
-  if (nb * num_seqs * num_q_heads > 0x7fffffffLL || max_seqlen > 0x3fffffffLL)
+  if (nb * (block_size == 128 ? 2 : 1) * num_seqs * num_q_heads > 0x7fffffffLL ||
+      max_seqlen > 0x3fffffffLL)
     return set_error(kErrUnsupported, "prefill_varlen: problem too large for one launch");
 
   PrefillParams p;
@@ -1171,6 +1189,7 @@ extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const
   p.parts = 1;
   p.wg_per_part = 1;
   p.cu_seqlens = cu_seqlens;
+  p.mshift = 0;
   // One workgroup per (sequence, head, query block); never the persistent loop.
   return dispatch_prefill(p, nullptr, head_dim, block_size, dtype, (hipStream_t)stream,
                           "prefill_varlen");
