@@ -252,10 +252,11 @@ def test_prefill_varlen_discriminating_inputs(case, kind):
     (2, 16, 4, 2048, 64, 64),    # 8 KV groups: per-XCD partitions of the work queue
     (2, 6, 3, 1500, 64, 64),     # 6 KV groups: one partition, ragged
     (2, 16, 4, 2048, 128, 64),   # two-wave kernel: the workspace is left unused
-    (1, 8, 2, 1024, 128, 128),   # generic kernel
+    (1, 8, 2, 1024, 128, 128),   # block 128 on the two-wave kernel
+    (2, 16, 4, 1500, 64, 128),   # block 128 on the four-wave kernel's work queue, ragged
 ])
 def test_persistent_queue_is_bit_identical(B, Hq, Hkv, S, D, bs):
-    """The persistent work queue (workspace given; block 64 with head dim 64) must not
+    """The persistent work queue (workspace given; head dim 64 at block 64 or 128) must not
     change any output bit against one workgroup per row."""
     dev = require_gpu()
     q, k, v = ai.qkv("unit", (B, Hq, S, D), (B, Hkv, S, D), 4242 + S + D, bs)
