@@ -29,7 +29,9 @@ CASES = [
     (1, 4, 4, 512, 128, 64, True),
     (2, 8, 2, 1000, 128, 64, True),   # GQA, ragged
     (1, 4, 1, 300, 64, 32, False),    # non-causal, D=64
-    (1, 2, 2, 384, 128, 128, True),   # bs=128
+    (1, 2, 2, 384, 128, 128, True),   # bs=128 (block-64 maxima pooled 2x2)
+    (2, 4, 2, 450, 64, 128, False),   # bs=128, non-causal, ragged, D=64
+    (1, 4, 2, 300, 128, 128, True),   # bs=128 over an odd number of 64-token blocks
     (2, 4, 2, 640, 64, 64, True),     # two query heads per KV head share the K tiles, D=64
     (1, 3, 3, 200, 128, 64, False),   # one head per workgroup, non-causal, ragged
 ]
@@ -52,13 +54,14 @@ def test_block_max_and_targets_match_oracle(B, Hq, Hkv, S, D, bs, causal):
         np.testing.assert_allclose(to_np(got), ref, rtol=1e-3, atol=1e-7)
 
 
-def test_clamp_temperature_variant():
+@pytest.mark.parametrize("bs", (64, 128))
+def test_clamp_temperature_variant(bs):
     dev = require_gpu()
     q, k, _ = wl.qkv(wl.Shape(1, 4, 4, 256, 128), 77)
     # Scale the queries so some block maxima exceed the clamp.
     q = (q.float() * 2000).to(torch.bfloat16)
-    got = _gt(q.to(dev), k.to(dev), 64, normalize="flat", temperature=2.0, clamp=50.0)
-    raw_ref = orc.block_max(to_np(q), to_np(k), 64, True, dtype=np.float64)
+    got = _gt(q.to(dev), k.to(dev), bs, normalize="flat", temperature=2.0, clamp=50.0)
+    raw_ref = orc.block_max(to_np(q), to_np(k), bs, True, dtype=np.float64)
     assert np.nanmax(raw_ref[np.isfinite(raw_ref)]) > 50.0
     ref = orc.normalize_block_max(raw_ref, "flat", temperature=2.0, clamp=50.0)
     np.testing.assert_allclose(to_np(got), ref, rtol=1e-3, atol=1e-7)
@@ -94,7 +97,8 @@ MASK_CASES = [
     (2, 4, 2, 640, 64, 64, "binary_2d"),      # two heads per workgroup; the reference adds 1/0
     (2, 3, 3, 333, 128, 64, "hf_4d"),         # one head per workgroup, HF [B, 1, S, S] mask
     (1, 4, 2, 300, 128, 32, "per_head_4d"),   # generic kernel, full per-head mask
-    (2, 2, 1, 400, 64, 128, "padding_2d"),    # generic kernel, block 128
+    (2, 2, 1, 400, 64, 128, "padding_2d"),    # block 128: block-64 maxima pooled 2x2
+    (1, 4, 4, 333, 128, 128, "hf_4d"),        # block 128, odd block-64 count, HF mask
 ]
 
 
