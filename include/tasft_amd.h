@@ -328,6 +328,8 @@ int tasft_gate_bwd(const float* soft_scores, const float* grad_soft, const void*
  * mask_strides = {s0, s1, s2} (0 broadcasts a dim: a key-padding row has s1 = s2 = 0).
  * It must be addressable for every query and key below NB*block_size (values past
  * seq_len are ignored), 16-byte aligned, strides non-negative multiples of 4.
+ * block_size 128 runs over 64-token blocks: target is first filled with -inf, then each
+ * 64-block maximum is merged into its 128-block by atomic max (exact, order-free).
  */
 int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask, float* target,
                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,

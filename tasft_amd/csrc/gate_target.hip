@@ -32,7 +32,29 @@ struct GateTargetParams {
   int B, Hq, Hkv, G, S, NB;
   float scale;
   int causal;
+  // Block-64 kernel only: 1 when the output holds 128-token blocks. Each 64-block maximum
+  // then goes by atomic max into entry (qb >> 1, kb >> 1) of the [NBO, NBO] grid, which
+  // the host has filled with -inf; 0 for a block-64 output (NBO = NB).
+  int pool;
+  int NBO;
 };
+
+// Float max into global memory by integer atomics: a value with the sign bit clear orders
+// like its bits as a signed integer, one with it set in reverse like its bits unsigned, and
+// -inf (0xff800000) is the largest unsigned pattern of any non-NaN negative value.
+__device__ __forceinline__ void gt_atomic_fmax(float* a, float v) {
+  const int bits = __float_as_int(v);
+  if (bits >= 0)
+    atomicMax((int*)a, bits);
+  else
+    atomicMin((unsigned int*)a, (unsigned int)bits);
+}
+
+__global__ void gate_target_fill_kernel(float* out, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = v;
+}
 
 
 // One 16-byte-per-lane DMA (buffer_load ... lds) of 1 KB into LDS at `dst`.
@@ -241,7 +263,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
 
   const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
   const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
-  float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NB + qb) * p.NB;
+  float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NBO + (qb >> p.pool)) * p.NBO;
 
   const int qrow = qb * BS + rh * 32 + col;
   const bool qvalid = qrow < p.S;
@@ -343,12 +365,17 @@ gate_target_bs64_kernel(const GateTargetParams p) {
       float m = rm[0];
 #pragma unroll
       for (int i = 1; i < WPH; ++i) m = fmaxf(m, rm[i]);
-      orow[kb] = m * post_scale;
+      // Scaling by scale > 0 before the max is exact: rounding is monotonic.
+      if (p.pool)
+        gt_atomic_fmax(orow + (kb >> 1), m * post_scale);
+      else
+        orow[kb] = m * post_scale;
     }
   };
 
   const int kb_end = p.causal ? qb + 1 : p.NB;
-  for (int kb = kb_end + (tid % HT); kb < p.NB; kb += HT) orow[kb] = -INFINITY;
+  if (!p.pool)
+    for (int kb = kb_end + (tid % HT); kb < p.NB; kb += HT) orow[kb] = -INFINITY;
   // Three stages, two blocks in flight. Past the last block the last one is loaded again,
   // so every wave always has exactly UPWX later DMA units outstanding when it waits for a
   // block, and the wait count is a constant.
@@ -406,12 +433,11 @@ static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream)
 template <bool MASKED, int DT>
 static hipError_t dispatch_blockmax_dt(const GateTargetParams& p, int64_t block_size,
                                        int64_t head_dim, hipStream_t s) {
-  if (block_size == 64 && head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
-  if (block_size == 64 && head_dim == 64) return launch_blockmax_bs64<64, MASKED, DT>(p, s);
-  if (block_size == 32 && head_dim == 128) return launch_blockmax<32, 128, MASKED, DT>(p, s);
-  if (block_size == 32 && head_dim == 64) return launch_blockmax<32, 64, MASKED, DT>(p, s);
-  if (block_size == 128 && head_dim == 128) return launch_blockmax<128, 128, MASKED, DT>(p, s);
-  return launch_blockmax<128, 64, MASKED, DT>(p, s);
+  // Block 128 runs the block-64 kernel with its maxima pooled 2x2 (p.pool).
+  if (block_size != 32 && head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
+  if (block_size != 32) return launch_blockmax_bs64<64, MASKED, DT>(p, s);
+  if (head_dim == 128) return launch_blockmax<32, 128, MASKED, DT>(p, s);
+  return launch_blockmax<32, 64, MASKED, DT>(p, s);
 }
 
 template <bool MASKED>
@@ -525,7 +551,10 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
                          "gate_target: attn_mask strides must be non-negative multiples of 4");
   }
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  if (nb * batch * num_q_heads > 0x7fffffffLL)
+  // Block 128 runs over 64-token blocks (one workgroup per 64-block row and head group).
+  const int pool = block_size == 128 ? 1 : 0;
+  const int64_t nb_run = pool ? (seq_len + 63) / 64 : nb;
+  if (nb_run * batch * num_q_heads > 0x7fffffffLL)
     return set_error(kErrUnsupported, "gate_target: problem too large for one launch");
 
   GateTargetParams p;
@@ -543,12 +572,23 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
   p.Hkv = (int)num_kv_heads;
   p.G = (int)(num_q_heads / num_kv_heads);
   p.S = (int)seq_len;
-  p.NB = (int)nb;
+  p.NB = (int)nb_run;
   p.scale = scale;
   p.causal = causal ? 1 : 0;
+  p.pool = pool;
+  p.NBO = (int)nb;
 
   hipStream_t s = (hipStream_t)stream;
-  hipError_t err = attn_mask ? dispatch_blockmax<true>(p, block_size, head_dim, dtype, s)
+  hipError_t err;
+  if (pool) {
+    const int64_t n = batch * num_q_heads * nb * nb;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(gate_target_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, s, target,
+                       n, -INFINITY);
+    if ((err = hipGetLastError()) != hipSuccess)
+      return set_error(kErrLaunch, "gate_target: fill launch failed: %s", hipGetErrorString(err));
+  }
+  err = attn_mask ? dispatch_blockmax<true>(p, block_size, head_dim, dtype, s)
                              : dispatch_blockmax<false>(p, block_size, head_dim, dtype, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate_target: block-max launch failed: %s", hipGetErrorString(err));

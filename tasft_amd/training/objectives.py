@@ -138,19 +138,6 @@ def gate_target_from_qk(
         raise ValueError(f"normalize must be one of {sorted(_NORMALIZE)}, got {normalize!r}")
     if not temperature > 0.0:
         raise ValueError(f"temperature must be > 0, got {temperature}")
-    if block_size == 128 and D in (64, 128):
-        # A block-128 maximum is the largest of its four block-64 maxima (rows and keys past S
-        # are -inf in both): the raw block-64 maxima from the specialised kernel, pooled 2x2
-        # here and normalised as the kernel's normalisation pass does (1.6x faster than the
-        # generic block-128 kernel at config-5 geometry).
-        raw = gate_target_from_qk(q, k, 64, causal=causal, scale=scale,
-                                  attention_mask=attention_mask, normalize="none")
-        nb = math.ceil(S / 128)
-        if raw.shape[-1] < 2 * nb:
-            pad = 2 * nb - raw.shape[-1]
-            raw = torch.nn.functional.pad(raw, (0, pad, 0, pad), value=float("-inf"))
-        pooled = raw.view(B, H, nb, 2, nb, 2).amax(dim=(3, 5))
-        return _normalize_block_maxima(pooled, normalize, temperature, clamp)
     lib = _native.load_library()
     q = q if (q.stride(-1) == 1 and all(s % 8 == 0 for s in q.stride()[:-1])) else q.contiguous()
     k = k if (k.stride(-1) == 1 and all(s % 8 == 0 for s in k.stride()[:-1])) else k.contiguous()
@@ -168,21 +155,6 @@ def gate_target_from_qk(
     )
     _native.check(status, "tasft_gate_target_fwd", {"shape": [B, H, S, D]})
     return out
-
-
-def _normalize_block_maxima(x: torch.Tensor, normalize: str, temperature: float,
-                            clamp: float | None) -> torch.Tensor:
-    """The kernel's normalisation pass on block maxima ``[B, H, NB, NB]``: finite values
-    clamped to ``[-clamp, clamp]``, divided by the temperature, then a softmax over each head's
-    grid ("flat") or each row ("row"); "none" returns them unchanged."""
-    if normalize == "none":
-        return x
-    if clamp is not None and clamp > 0:
-        x = torch.where(x > float("-inf"), x.clamp(-clamp, clamp), x)
-    x = x / temperature
-    if normalize == "flat":
-        return torch.softmax(x.flatten(-2), dim=-1).view_as(x)
-    return torch.softmax(x, dim=-1)
 
 
 def _padded_attention_mask(mask: torch.Tensor, B: int, H: int, S: int, padded: int,
