@@ -91,6 +91,24 @@ def test_config5_full_size_sampled_heads():
         np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)
 
 
+def test_config5_block128_is_the_2x2_max_of_block64():
+    """Block 128 merges each 64-block maximum into its 128-block by atomic max: at full size
+    the raw maxima equal the 2x2 max of the block-64 raw maxima exactly (max is exact and
+    order-free), and a sampled head matches the oracle's block-128 target."""
+    dev = require_gpu()
+    shape = wl.CONFIG_SHAPES[5]
+    q, k, _ = wl.qkv(shape, 1005)
+    qd, kd = q.to(dev), k.to(dev)
+    r64 = _gt(qd, kd, 64, normalize="none")
+    r128 = _gt(qd, kd, 128, normalize="none")
+    B, H, nb, _ = r128.shape
+    assert torch.equal(r128, r64.view(B, H, nb, 2, nb, 2).amax(dim=(3, 5)))
+    got = to_np(_gt(qd, kd, 128))
+    b, h = 2, 17
+    ref = orc.gate_target_from_qk(to_np(q[b : b + 1, h : h + 1]), to_np(k[b : b + 1, h // 4 : h // 4 + 1]), 128)
+    np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)
+
+
 MASK_CASES = [
     # B, Hq, Hkv, S, D, bs, form
     (2, 8, 2, 700, 128, 64, "padding_2d"),    # four heads per workgroup, ragged, key padding
