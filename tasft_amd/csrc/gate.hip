@@ -22,8 +22,8 @@
 // the query chunks (half at B=4, 32 heads, S=8192); gate_qpool_pair64_kernel then takes
 // every query chunk, pooling the others itself, and evaluates each chunk's rows as soon as
 // its units exist. No workgroup
-// waits for another within a launch. Otherwise one pooling launch (streaming for block 64,
-// generic else) is followed by gate_pairwise_kernel.
+// waits for another within a launch. Otherwise one pooling launch (streaming for blocks 64
+// and 128 with D in {64, 128}, generic else) is followed by gate_pairwise_kernel.
 #include <algorithm>
 #include <type_traits>
 
@@ -177,17 +177,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
-// Pools kFusePB blocks (chunk `chunk`) of one (b, head) row stream of Q (is_q) or K and
-// projects their means; `red` is the workgroup's LDS (4 x kFusePB x D floats).
-template <int D, int DT>
+// Pools kFusePB blocks (chunk `chunk`) of BSZ rows (64 or 128) of one (b, head) row stream
+// of Q (is_q) or K and projects their means; `red` is the workgroup's LDS (4 x kFusePB x D
+// floats).
+template <int D, int DT, int BSZ = 64>
 __device__ __forceinline__ void pool_proj64(const GatePoolParams& p, bool is_q, int64_t bh,
                                             int chunk, float (&red)[4][kFusePB][D]) {
-  constexpr int BSZ = 64;
+  static_assert(BSZ == 64 || BSZ == 128, "block rows");
   constexpr int DOCT = D / 8;        // 16-byte chunks per row
   constexpr int RG = 256 / DOCT;     // row groups in the workgroup
   constexpr int RPT = BSZ / RG;      // rows per thread per block
   constexpr int WRG = kWave / DOCT;  // row groups per wave
-  constexpr int GB = 4;              // blocks per load group
+  constexpr int GB = 256 / BSZ;      // blocks per load group (the same loads in flight)
   static_assert(WRG == 4 || WRG == 8, "row groups per wave");
 
   const int tid = threadIdx.x;
@@ -312,7 +313,7 @@ __device__ __forceinline__ void pool_proj64(const GatePoolParams& p, bool is_q, 
 
 // Workgroup wg0 + blockIdx.x pools query chunks first (B x Hq x chunks, see query_chunk),
 // then key chunks.
-template <int D, int DT>
+template <int D, int DT, int BSZ = 64>
 __global__ void __launch_bounds__(256)
 gate_pool_proj64_kernel(const GatePoolParams p) {
   __shared__ __attribute__((aligned(16))) float red[4][kFusePB][D];  // per-wave sums, then means
@@ -324,9 +325,9 @@ gate_pool_proj64_kernel(const GatePoolParams p) {
     int64_t bh;
     int chunk;
     query_chunk(p, wg, chunks, bh, chunk);
-    pool_proj64<D, DT>(p, true, bh, chunk, red);
+    pool_proj64<D, DT, BSZ>(p, true, bh, chunk, red);
   } else {
-    pool_proj64<D, DT>(p, false, (wg - nq) / chunks, (int)((wg - nq) % chunks), red);
+    pool_proj64<D, DT, BSZ>(p, false, (wg - nq) / chunks, (int)((wg - nq) % chunks), red);
   }
 }
 
@@ -1155,14 +1156,17 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  const bool fast = block_size == 64 && (head_dim == 64 || head_dim == 128) &&
-                    seq_len * std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
+  // The streaming pool's 32-bit row offsets reach the end of a chunk's last load group.
+  const bool fast = (block_size == 64 || block_size == 128) &&
+                    (head_dim == 64 || head_dim == 128) &&
+                    std::max<int64_t>(seq_len, kFusePB * block_size) *
+                            std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
   if (fast) {
     const int64_t fchunks = (nb + kFusePB - 1) / kFusePB;
     // With hidden a multiple of kFuseHid, at most kFuseMaxHid: the first launch pools and projects the key
     // chunks only, and gate_qpool_pair64_kernel pools each query chunk and evaluates its
     // rows. Otherwise one launch pools both and gate_pairwise_kernel follows.
-    const bool fused = hidden % kFuseHid == 0 && hidden <= kFuseMaxHid;
+    const bool fused = block_size == 64 && hidden % kFuseHid == 0 && hidden <= kFuseMaxHid;
     const int64_t nq = batch * num_q_heads * fchunks;
     int64_t n1 = 0;
     if (fused) {
@@ -1177,7 +1181,17 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
     }
     const dim3 g1((unsigned)(fused ? n1 + batch * num_kv_heads * fchunks
                                    : batch * (num_q_heads + num_kv_heads) * fchunks));
-    if (head_dim == 128 && dtype == kF16)
+    if (block_size == 128) {
+      // Block 128: the same streaming pool over 128-row blocks, then gate_pairwise_kernel.
+      if (head_dim == 128 && dtype == kF16)
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16, 128>), g1, dim3(256), 0, s, pp);
+      else if (head_dim == 128)
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kBf16, 128>), g1, dim3(256), 0, s, pp);
+      else if (dtype == kF16)
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kF16, 128>), g1, dim3(256), 0, s, pp);
+      else
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kBf16, 128>), g1, dim3(256), 0, s, pp);
+    } else if (head_dim == 128 && dtype == kF16)
       hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16>), g1, dim3(256), 0, s, pp);
     else if (head_dim == 128)
       hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kBf16>), g1, dim3(256), 0, s, pp);

@@ -76,6 +76,8 @@ CASES = [
     (1, 4, 2, 1300, 128, 64, 200, False),  # block 64, 21 blocks, hidden > one staging tile
     (1, 4, 2, 1300, 128, 64, 64, False),   # block 64, non-causal, fused query-pool + pairwise
     (1, 2, 1, 9000, 128, 64, 32, True),    # 141 blocks: two 128-key groups per row
+    (1, 4, 2, 1000, 128, 128, 64, True),   # block 128 streaming pool, ragged, one partial chunk
+    (2, 4, 2, 2500, 64, 128, 48, False),   # block 128, D=64, non-causal, 20 blocks (two chunks)
 ]
 
 
