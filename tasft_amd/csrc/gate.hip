@@ -22,8 +22,8 @@
 // the query chunks (half at B=4, 32 heads, S=8192); gate_qpool_pair64_kernel then takes
 // every query chunk, pooling the others itself, and evaluates each chunk's rows as soon as
 // its units exist. No workgroup
-// waits for another within a launch. Otherwise one pooling launch (streaming for blocks 64
-// and 128 with D in {64, 128}, generic else) is followed by gate_pairwise_kernel.
+// waits for another within a launch. Otherwise one pooling launch (streaming for blocks 32,
+// 64 and 128 with D in {64, 128}, generic else) is followed by gate_pairwise_kernel.
 #include <algorithm>
 #include <type_traits>
 
@@ -177,13 +177,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
 }
 
-// Pools kFusePB blocks (chunk `chunk`) of BSZ rows (64 or 128) of one (b, head) row stream
+// Pools kFusePB blocks (chunk `chunk`) of BSZ rows (32, 64 or 128) of one (b, head) row stream
 // of Q (is_q) or K and projects their means; `red` is the workgroup's LDS (4 x kFusePB x D
 // floats).
 template <int D, int DT, int BSZ = 64>
 __device__ __forceinline__ void pool_proj64(const GatePoolParams& p, bool is_q, int64_t bh,
                                             int chunk, float (&red)[4][kFusePB][D]) {
-  static_assert(BSZ == 64 || BSZ == 128, "block rows");
+  static_assert(BSZ == 32 || BSZ == 64 || BSZ == 128, "block rows");
   constexpr int DOCT = D / 8;        // 16-byte chunks per row
   constexpr int RG = 256 / DOCT;     // row groups in the workgroup
   constexpr int RPT = BSZ / RG;      // rows per thread per block
@@ -1157,7 +1157,7 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
   // The streaming pool's 32-bit row offsets reach the end of a chunk's last load group.
-  const bool fast = (block_size == 64 || block_size == 128) &&
+  const bool fast = (block_size == 32 || block_size == 64 || block_size == 128) &&
                     (head_dim == 64 || head_dim == 128) &&
                     std::max<int64_t>(seq_len, kFusePB * block_size) *
                             std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
@@ -1181,8 +1181,17 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
     }
     const dim3 g1((unsigned)(fused ? n1 + batch * num_kv_heads * fchunks
                                    : batch * (num_q_heads + num_kv_heads) * fchunks));
-    if (block_size == 128) {
-      // Block 128: the same streaming pool over 128-row blocks, then gate_pairwise_kernel.
+    if (block_size == 32) {
+      if (head_dim == 128 && dtype == kF16)
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16, 32>), g1, dim3(256), 0, s, pp);
+      else if (head_dim == 128)
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kBf16, 32>), g1, dim3(256), 0, s, pp);
+      else if (dtype == kF16)
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kF16, 32>), g1, dim3(256), 0, s, pp);
+      else
+        hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kBf16, 32>), g1, dim3(256), 0, s, pp);
+    } else if (block_size == 128) {
+      // Blocks 32 and 128: the same streaming pool, then gate_pairwise_kernel.
       if (head_dim == 128 && dtype == kF16)
         hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16, 128>), g1, dim3(256), 0, s, pp);
       else if (head_dim == 128)

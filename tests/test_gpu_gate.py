@@ -78,6 +78,8 @@ CASES = [
     (1, 2, 1, 9000, 128, 64, 32, True),    # 141 blocks: two 128-key groups per row
     (1, 4, 2, 1000, 128, 128, 64, True),   # block 128 streaming pool, ragged, one partial chunk
     (2, 4, 2, 2500, 64, 128, 48, False),   # block 128, D=64, non-causal, 20 blocks (two chunks)
+    (1, 4, 2, 1000, 128, 32, 64, True),    # block 32 streaming pool, 32 blocks (two chunks)
+    (2, 2, 2, 600, 64, 32, 32, False),     # block 32, D=64, non-causal, ragged partial chunk
 ]
 
 
