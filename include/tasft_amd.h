@@ -330,6 +330,8 @@ int tasft_gate_bwd(const float* soft_scores, const float* grad_soft, const void*
  * seq_len are ignored), 16-byte aligned, strides non-negative multiples of 4.
  * block_size 128 runs over 64-token blocks: target is first filled with -inf, then each
  * 64-block maximum is merged into its 128-block by atomic max (exact, order-free).
+ * block_size 32 without attn_mask also runs over 64-token blocks, each 32 x 32 quarter of a
+ * 64-block written as one block.
  */
 int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask, float* target,
                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,

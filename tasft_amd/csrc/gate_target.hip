@@ -37,6 +37,10 @@ struct GateTargetParams {
   // the host has filled with -inf; 0 for a block-64 output (NBO = NB).
   int pool;
   int NBO;
+  // Block-64 kernel with two waves per head only: 1 when the output holds 32-token blocks
+  // ([NBO, NBO], filled with -inf by the host). Each wave's two 32 x 32 score tiles are then
+  // whole blocks, written as they are computed.
+  int fine;
 };
 
 // Float max into global memory by integer atomics: a value with the sign bit clear orders
@@ -354,13 +358,27 @@ gate_target_bs64_kernel(const GateTargetParams p) {
       float m2 = fmaxf(fmaxf(s[1][0], s[1][1]), s[1][2]);
 #pragma unroll
       for (int rr = 3; rr < 15; rr += 2) m2 = fmaxf(fmaxf(m2, s[1][rr]), s[1][rr + 1]);
-      m = fmaxf(m, fmaxf(m2, s[1][15]));
+      m2 = fmaxf(m2, s[1][15]);
+      if (p.fine) {
+        // Block-32 output: this wave's rows are query block 2 qb + rh, its key tiles t = 0, 1
+        // are key blocks 2 kb + t (entries past NBO belong to no block).
+        m = wave_max_dpp(m);
+        m2 = wave_max_dpp(m2);
+        const int r = 2 * qb + rh;
+        if (lane == 0 && r < p.NBO) {
+          float* o = p.out + (((int64_t)b * p.Hq + h) * p.NBO + r) * p.NBO + 2 * kb;
+          o[0] = m * post_scale;
+          if (2 * kb + 1 < p.NBO) o[1] = m2 * post_scale;
+        }
+        return 0.f;
+      }
+      m = fmaxf(m, m2);
     }
     return wave_max_dpp(m);
   };
   // Combine the four partial maxima of this head's block kb (slot kb & 1), scaled.
   auto store = [&](int kb) {
-    if ((tid % HT) == 0) {
+    if ((tid % HT) == 0 && !p.fine) {
       const float* rm = red[kb & 1][hw];
       float m = rm[0];
 #pragma unroll
@@ -374,7 +392,7 @@ gate_target_bs64_kernel(const GateTargetParams p) {
   };
 
   const int kb_end = p.causal ? qb + 1 : p.NB;
-  if (!p.pool)
+  if (!p.pool && !p.fine)
     for (int kb = kb_end + (tid % HT); kb < p.NB; kb += HT) orow[kb] = -INFINITY;
   // Three stages, two blocks in flight. Past the last block the last one is loaded again,
   // so every wave always has exactly UPWX later DMA units outstanding when it waits for a
@@ -433,9 +451,10 @@ static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream)
 template <bool MASKED, int DT>
 static hipError_t dispatch_blockmax_dt(const GateTargetParams& p, int64_t block_size,
                                        int64_t head_dim, hipStream_t s) {
-  // Block 128 runs the block-64 kernel with its maxima pooled 2x2 (p.pool).
-  if (block_size != 32 && head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
-  if (block_size != 32) return launch_blockmax_bs64<64, MASKED, DT>(p, s);
+  // Block 128 runs the block-64 kernel with its maxima pooled 2x2 (p.pool), block 32 without
+  // a mask with each wave's 32 x 32 tiles as blocks (p.fine).
+  if ((block_size != 32 || p.fine) && head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
+  if (block_size != 32 || p.fine) return launch_blockmax_bs64<64, MASKED, DT>(p, s);
   if (head_dim == 128) return launch_blockmax<32, 128, MASKED, DT>(p, s);
   return launch_blockmax<32, 64, MASKED, DT>(p, s);
 }
@@ -551,9 +570,11 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
                          "gate_target: attn_mask strides must be non-negative multiples of 4");
   }
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  // Block 128 runs over 64-token blocks (one workgroup per 64-block row and head group).
+  // Blocks 128 and 32 (without a mask, whose rows and keys would be read up to a multiple of
+  // 64) run over 64-token blocks: one workgroup per 64-block row and head group.
   const int pool = block_size == 128 ? 1 : 0;
-  const int64_t nb_run = pool ? (seq_len + 63) / 64 : nb;
+  const int fine = block_size == 32 && !attn_mask ? 1 : 0;
+  const int64_t nb_run = pool || fine ? (seq_len + 63) / 64 : nb;
   if (nb_run * batch * num_q_heads > 0x7fffffffLL)
     return set_error(kErrUnsupported, "gate_target: problem too large for one launch");
 
@@ -577,10 +598,11 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
   p.causal = causal ? 1 : 0;
   p.pool = pool;
   p.NBO = (int)nb;
+  p.fine = fine;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (pool) {
+  if (pool || fine) {
     const int64_t n = batch * num_q_heads * nb * nb;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(gate_target_fill_kernel, dim3((unsigned)blocks), dim3(256), 0, s, target,

@@ -32,6 +32,8 @@ CASES = [
     (1, 2, 2, 384, 128, 128, True),   # bs=128 (block-64 maxima pooled 2x2)
     (2, 4, 2, 450, 64, 128, False),   # bs=128, non-causal, ragged, D=64
     (1, 4, 2, 300, 128, 128, True),   # bs=128 over an odd number of 64-token blocks
+    (2, 4, 2, 1000, 128, 32, True),   # bs=32 as 32x32 tiles of the block-64 kernel, ragged
+    (1, 3, 3, 333, 128, 32, True),    # bs=32, one head per workgroup, last 64-block half empty
     (2, 4, 2, 640, 64, 64, True),     # two query heads per KV head share the K tiles, D=64
     (1, 3, 3, 200, 128, 64, False),   # one head per workgroup, non-causal, ragged
 ]
@@ -54,7 +56,7 @@ def test_block_max_and_targets_match_oracle(B, Hq, Hkv, S, D, bs, causal):
         np.testing.assert_allclose(to_np(got), ref, rtol=1e-3, atol=1e-7)
 
 
-@pytest.mark.parametrize("bs", (64, 128))
+@pytest.mark.parametrize("bs", (32, 64, 128))
 def test_clamp_temperature_variant(bs):
     dev = require_gpu()
     q, k, _ = wl.qkv(wl.Shape(1, 4, 4, 256, 128), 77)
@@ -91,22 +93,26 @@ def test_config5_full_size_sampled_heads():
         np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)
 
 
-def test_config5_block128_is_the_2x2_max_of_block64():
-    """Block 128 merges each 64-block maximum into its 128-block by atomic max: at full size
-    the raw maxima equal the 2x2 max of the block-64 raw maxima exactly (max is exact and
-    order-free), and a sampled head matches the oracle's block-128 target."""
+def test_config5_blocks_32_64_128_nest_by_2x2_max():
+    """Block 128 merges each 64-block maximum into its 128-block by atomic max, and block 32
+    writes the 32 x 32 tiles of the same block-64 kernel: at full size the block-64 raw
+    maxima are exactly the 2x2 max of the block-32 ones, the block-128 maxima exactly the
+    2x2 max of the block-64 ones (max is exact and order-free), and sampled heads match the
+    oracle's block-32 and block-128 targets."""
     dev = require_gpu()
     shape = wl.CONFIG_SHAPES[5]
     q, k, _ = wl.qkv(shape, 1005)
     qd, kd = q.to(dev), k.to(dev)
     r64 = _gt(qd, kd, 64, normalize="none")
     r128 = _gt(qd, kd, 128, normalize="none")
+    r32 = _gt(qd, kd, 32, normalize="none")
     B, H, nb, _ = r128.shape
     assert torch.equal(r128, r64.view(B, H, nb, 2, nb, 2).amax(dim=(3, 5)))
-    got = to_np(_gt(qd, kd, 128))
-    b, h = 2, 17
-    ref = orc.gate_target_from_qk(to_np(q[b : b + 1, h : h + 1]), to_np(k[b : b + 1, h // 4 : h // 4 + 1]), 128)
-    np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)
+    assert torch.equal(r64, r32.view(B, H, 2 * nb, 2, 2 * nb, 2).amax(dim=(3, 5)))
+    for bs, (b, h) in ((128, (2, 17)), (32, (1, 6))):
+        got = to_np(_gt(qd, kd, bs))
+        ref = orc.gate_target_from_qk(to_np(q[b : b + 1, h : h + 1]), to_np(k[b : b + 1, h // 4 : h // 4 + 1]), bs)
+        np.testing.assert_allclose(got[b, h], ref[0, 0], rtol=1e-3, atol=1e-7)
 
 
 MASK_CASES = [
