@@ -326,12 +326,13 @@ int tasft_gate_bwd(const float* soft_scores, const float* grad_soft, const void*
  * attn_mask: NULL, or the additive mask of tasft_attention.py:445-449 as fp32 with
  * element (b, h, query, key) at attn_mask[b*s0 + h*s1 + query*s2 + key] for
  * mask_strides = {s0, s1, s2} (0 broadcasts a dim: a key-padding row has s1 = s2 = 0).
- * It must be addressable for every query and key below NB*block_size (values past
- * seq_len are ignored), 16-byte aligned, strides non-negative multiples of 4.
+ * It must be addressable for every query and key below max(NB*block_size,
+ * 64*ceil(seq_len/64)) (values past seq_len are ignored), 16-byte aligned, strides
+ * non-negative multiples of 4.
  * block_size 128 runs over 64-token blocks: target is first filled with -inf, then each
  * 64-block maximum is merged into its 128-block by atomic max (exact, order-free).
- * block_size 32 without attn_mask also runs over 64-token blocks, each 32 x 32 quarter of a
- * 64-block written as one block.
+ * block_size 32 also runs over 64-token blocks, each 32 x 32 quarter of a 64-block
+ * written as one block (so a block-32 mask is read up to a multiple of 64).
  */
 int tasft_gate_target_fwd(const void* q, const void* k, const float* attn_mask, float* target,
                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,

@@ -11,7 +11,7 @@ asks for float64. How each function is pinned (checked independently of itself):
 * ``pool_to_blocks``: literal vectors of tests/unit/test_numerical_correctness.py:40-98.
 * ``gate_logits_concat``: textbook composition, checked against torch.nn.Linear/ReLU.
 * ``gate_logits``: equals ``gate_logits_concat`` (the decomposition W.[x;y] = Wq x + Wk y).
-* ``gate_forward`` / ``threshold_mask``: sigmoid via torch.sigmoid; invariants of
+* ``threshold_mask``: sigmoid via torch.sigmoid; invariants of
   tests/unit/test_causal_gate_and_single_pass.py:154-270 and test_edge_cases.py:207-238.
 * ``attention_dense_masked``: torch SDPA for all-true masks (causal and not), and a
   pure-Python loop implementation on tiny inputs.
@@ -116,18 +116,6 @@ def threshold_mask(logits: np.ndarray, tau, causal: bool) -> tuple[np.ndarray, n
     return soft, soft >= t
 
 
-def gate_forward(q, k, w_in, b_in, w_out, bs: int, tau, causal: bool = True,
-                 force_diagonal: bool = False):
-    """Full gate (attn_gate.py:241-277): returns (logits, soft, hard, sparsity)."""
-    logits = gate_logits(q, k, w_in, b_in, w_out, bs)
-    soft, hard = threshold_mask(logits, tau, causal)
-    if force_diagonal:
-        nb = hard.shape[-1]
-        hard = hard | np.eye(nb, dtype=bool)
-    sparsity = 1.0 - hard.mean()
-    return logits, soft, hard, float(sparsity)
-
-
 # ----------------------------------------------------------------------------- attention
 def token_mask(block_mask: np.ndarray, s: int, bs: int, causal: bool) -> np.ndarray:
     """Element mask of the reference kernel (block_sparse_fa.py:192-243, host prep :502-508)."""
@@ -146,7 +134,9 @@ def attention_dense_masked(q, k, v, block_mask, bs: int, causal: bool = True,
     """``softmax(QK^T*scale + M) V`` with M from ``token_mask``; empty rows give 0.
 
     Restates the kernel's math (block_sparse_fa.py:228-258): scale after the dot
-    product (:228), -inf outside the mask (:243), and the ``l > 0`` guard (:257-258).
+    product (:228), -inf outside the mask (:243), and the division by
+    ``where(l > 0, l, 1)`` (:255-257), so an empty row gives 0 and a row whose sum is NaN
+    (a NaN score among its keys) stays NaN.
     GQA: query head h uses K/V head h // G. No bf16 rounding of P (the kernel's P->bf16
     cast at :252 is inside the tolerance).
     """
@@ -164,7 +154,7 @@ def attention_dense_masked(q, k, v, block_mask, bs: int, causal: bool = True,
             p = np.exp(sco - np.where(has, mx, 0.0))
             l = p.sum(axis=-1, keepdims=True)
             o = p @ v[b, h // g].astype(dtype)
-            out[b, h] = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
+            out[b, h] = o / np.where(l > 0, l, 1.0)
     return out
 
 
@@ -199,7 +189,7 @@ def attention_block_gather(q, k, v, block_mask, bs: int, causal: bool = True,
             mx = sco.max(axis=-1, keepdims=True)
             p = np.exp(sco - np.where(np.isfinite(mx), mx, 0.0))
             l = p.sum(axis=-1, keepdims=True)
-            out[b, h, q0:q1] = np.where(l > 0, (p @ vh[idx]) / np.where(l > 0, l, 1.0), 0.0)
+            out[b, h, q0:q1] = (p @ vh[idx]) / np.where(l > 0, l, 1.0)
     return out
 
 
@@ -411,15 +401,6 @@ def sparsity_stats(block_mask: np.ndarray) -> tuple[int, int, float]:
 def estimate_speedup(s: float) -> float:
     """``1 / max(1e-6, 1 - 0.98 s)`` (block_sparse_fa.py:616-618)."""
     return 1.0 / max(1e-6, 1.0 - s * 0.98)
-
-
-def executed_blocks(block_mask: np.ndarray, causal: bool = True) -> int:
-    """Number of (query block, key block) tiles the prefill computes."""
-    m = block_mask.astype(bool)
-    if causal:
-        nb = m.shape[-1]
-        m = m & np.tril(np.ones((nb, nb), dtype=bool))
-    return int(np.count_nonzero(m))
 
 
 # ----------------------------------------------------------------------------- formats

@@ -563,8 +563,10 @@ bsfa_decode_split_kernel(const DecodeParams p) {
       O += ((const float*)v_lds[w])[gg * D + d] * f;
     }
     if (p.P == 1) {
-      // One split: this is the whole row, written directly (no combine pass).
-      const float r = L > 0.f ? O / L : 0.f;
+      // One split: this is the whole row, written directly (no combine pass). An empty row
+      // has O = 0; dividing by 1 there (not selecting 0) keeps a NaN row NaN, as the
+      // reference's normalisation does (block_sparse_fa.py:255-257).
+      const float r = O / (L > 0.f ? L : 1.f);
       p.o[b * p.so[0] + (int64_t)(h0 + gg) * p.so[1] + d] = f32_to16<DT>(r);
     } else {
       const int64_t row = ((int64_t)b * p.Hq + h0 + gg) * p.P + s;
@@ -596,7 +598,7 @@ bsfa_decode_combine_kernel(const DecodeParams p) {
     L += ml[2 * sp + 1] * f;
     O += os[(int64_t)sp * D + d] * f;
   }
-  const float r = L > 0.f ? O / L : 0.f;
+  const float r = O / (L > 0.f ? L : 1.f);  // empty rows: O = 0; NaN rows stay NaN
   p.o[b * p.so[0] + h * p.so[1] + d] = f32_to16<DT>(r);
 }
 

@@ -26,7 +26,8 @@ struct GateTargetParams {
   float* out;  // [B, Hq, NB, NB] contiguous
   // Additive fp32 mask (masked kernels only): element (b, h, query, key) at
   // amask[b * sam[0] + h * sam[1] + query * sam[2] + key], addressable for every query and
-  // key below NB * block; strides are multiples of 4 and the base is 16-byte aligned.
+  // key below max(NB * block, 64 * ceil(S / 64)); strides are multiples of 4 and the base is
+  // 16-byte aligned.
   const float* amask;
   int64_t sq[3], sk[3], sam[3];
   int B, Hq, Hkv, G, S, NB;
@@ -66,109 +67,6 @@ __device__ __forceinline__ void gt_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* dst,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TASFT_LDS void*)dst, 16, voff, 0, 0, 0);
 }
 
-// Without a mask (MASKED false) the raw maxima are scaled once at the end (scale > 0
-// commutes with max); with one, each score is scaled and the mask added before the max.
-template <int BS, int D, bool MASKED, int DT>
-__global__ void __launch_bounds__(BS / 32 * kWave)
-gate_target_blockmax_kernel(const GateTargetParams p) {
-  constexpr int WAVES = BS / 32;
-  constexpr int THREADS = WAVES * kWave;
-  constexpr int KSTEPS = D / 16;
-  constexpr int KTILES = BS / 32;
-  constexpr int KST = D + 8;
-
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BS * KST];
-  __shared__ float red[2][WAVES];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int col = lane & 31;
-  const int half = lane >> 5;
-
-  const int64_t per_slab = (int64_t)p.B * p.Hq;
-  const int64_t idx = blockIdx.x;
-  const int slab = (int)(idx / per_slab);
-  const int qb = p.causal ? (p.NB - 1 - slab) : slab;
-  int64_t grp;
-  int g;
-  xcd_group_map(idx % per_slab, (int64_t)p.B * p.Hkv, p.G, &grp, &g);
-  const int b = (int)(grp / p.Hkv);
-  const int kvh = (int)(grp % p.Hkv);
-  const int h = kvh * p.G + g;
-
-  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
-  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
-  float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NB + qb) * p.NB;
-  const float post_scale = MASKED ? 1.f : p.scale;
-
-  const int qrow = qb * BS + wave * 32 + col;
-  const bool qvalid = qrow < p.S;
-  const float* mrow = MASKED ? p.amask + b * p.sam[0] + h * p.sam[1] + (int64_t)qrow * p.sam[2]
-                             : nullptr;
-  u32x4_t qf[KSTEPS];
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks) {
-    u32x4_t val = {0u, 0u, 0u, 0u};
-    if (qvalid) val = *(const u32x4_t*)(qbase + (int64_t)qrow * p.sq[2] + ks * 16 + half * 8);
-    qf[ks] = val;
-  }
-
-  const int kb_end = p.causal ? qb + 1 : p.NB;
-  // Key blocks above the diagonal are -inf in the pooled grid (causal triu mask).
-  for (int kb = kb_end + tid; kb < p.NB; kb += THREADS) orow[kb] = -INFINITY;
-
-  for (int kb = 0; kb < kb_end; ++kb) {
-    const int key0 = kb * BS;
-    __syncthreads();
-    if (tid == 0 && kb > 0) {
-      float mx = red[(kb - 1) & 1][0];
-#pragma unroll
-      for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[(kb - 1) & 1][w]);
-      orow[kb - 1] = mx * post_scale;
-    }
-#pragma unroll
-    for (int c = tid; c < BS * D / 8; c += THREADS) {
-      const int r = c / (D / 8);
-      const int cc = c % (D / 8);
-      u32x4_t val = {0u, 0u, 0u, 0u};
-      if (key0 + r < p.S) val = *(const u32x4_t*)(kbase + (int64_t)(key0 + r) * p.sk[2] + cc * 8);
-      *(u32x4_t*)(k_lds + r * KST + cc * 8) = val;
-    }
-    __syncthreads();
-
-    const bool need_mask = (p.causal && kb == qb) || (key0 + BS > p.S) || !qvalid;
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < KTILES; ++t) {
-      f32x16_t s = (f32x16_t){};
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const u32x4_t a = *(const u32x4_t*)(k_lds + (t * 32 + col) * KST + ks * 16 + half * 8);
-        s = mfma16<DT>(a, qf[ks], s);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[r];
-        const int key = key0 + t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        if constexpr (MASKED) x = x * p.scale + mrow[key];
-        if (need_mask) {
-          if (!qvalid || key >= p.S || (p.causal && key > qrow)) x = -INFINITY;
-        }
-        mloc = fmaxf(mloc, x);
-      }
-    }
-    mloc = wave_max(mloc);
-    if (lane == 0) red[kb & 1][wave] = mloc;
-  }
-  __syncthreads();
-  if (tid == 0 && kb_end > 0) {
-    float mx = red[(kb_end - 1) & 1][0];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[(kb_end - 1) & 1][w]);
-    orow[kb_end - 1] = mx * post_scale;
-  }
-}
 
 // In-place softmax over groups of `group_len` contiguous values. Finite values are
 // optionally clamped to [-clamp, clamp] first, then divided by the temperature;
@@ -440,23 +338,14 @@ static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t st
   return hipGetLastError();
 }
 
-template <int BS, int D, bool MASKED, int DT>
-static hipError_t launch_blockmax(const GateTargetParams& p, hipStream_t stream) {
-  const int64_t grid = (int64_t)p.NB * p.B * p.Hq;
-  hipLaunchKernelGGL((gate_target_blockmax_kernel<BS, D, MASKED, DT>), dim3((unsigned)grid),
-                     dim3(BS / 32 * kWave), 0, stream, p);
-  return hipGetLastError();
-}
-
 template <bool MASKED, int DT>
 static hipError_t dispatch_blockmax_dt(const GateTargetParams& p, int64_t block_size,
                                        int64_t head_dim, hipStream_t s) {
-  // Block 128 runs the block-64 kernel with its maxima pooled 2x2 (p.pool), block 32 without
-  // a mask with each wave's 32 x 32 tiles as blocks (p.fine).
-  if ((block_size != 32 || p.fine) && head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
-  if (block_size != 32 || p.fine) return launch_blockmax_bs64<64, MASKED, DT>(p, s);
-  if (head_dim == 128) return launch_blockmax<32, 128, MASKED, DT>(p, s);
-  return launch_blockmax<32, 64, MASKED, DT>(p, s);
+  // Every block size runs the block-64 kernel: block 128 with its maxima pooled 2x2
+  // (p.pool), block 32 with each wave's 32 x 32 tiles as blocks (p.fine).
+  (void)block_size;
+  if (head_dim == 128) return launch_blockmax_bs64<128, MASKED, DT>(p, s);
+  return launch_blockmax_bs64<64, MASKED, DT>(p, s);
 }
 
 template <bool MASKED>
@@ -570,10 +459,10 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
                          "gate_target: attn_mask strides must be non-negative multiples of 4");
   }
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  // Blocks 128 and 32 (without a mask, whose rows and keys would be read up to a multiple of
-  // 64) run over 64-token blocks: one workgroup per 64-block row and head group.
+  // Blocks 128 and 32 run over 64-token blocks: one workgroup per 64-block row and head
+  // group (a block-32 mask is read up to a multiple of 64 rows and keys).
   const int pool = block_size == 128 ? 1 : 0;
-  const int fine = block_size == 32 && !attn_mask ? 1 : 0;
+  const int fine = block_size == 32 ? 1 : 0;
   const int64_t nb_run = pool || fine ? (seq_len + 63) / 64 : nb;
   if (nb_run * batch * num_q_heads > 0x7fffffffLL)
     return set_error(kErrUnsupported, "gate_target: problem too large for one launch");

@@ -293,7 +293,7 @@ bsfa_prefill_kernel(const PrefillParams p) {
 
   // Epilogue: combine the two half-lane denominators, normalise, store in the input type.
   const float l_tot = l_run + xor32(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float inv = 1.f / (l_tot > 0.f ? l_tot : 1.f);  // empty rows: O = 0; NaN rows stay NaN
   if (qvalid) {
     uint16_t* orow = obase + (int64_t)qrow * p.so[2];
 #pragma unroll
@@ -650,7 +650,7 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
     const float f0 = __builtin_amdgcn_exp2f(m0 - Mu);  // 0 for an empty half
     const float f1 = __builtin_amdgcn_exp2f(m1 - Mu);
     const float L = l0 * f0 + l1 * f1;
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float inv = 1.f / (L > 0.f ? L : 1.f);  // empty rows: O = 0; NaN rows stay NaN
     if (qvalid) {
       uint16_t* orow = obase + (int64_t)qrow * p.so[2];
 #pragma unroll
@@ -916,7 +916,7 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   __builtin_amdgcn_s_waitcnt(0x0f70);  // no DMA into this workgroup's LDS outlives it
 
   const float l_tot = pair_sum32(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // empty rows output 0
+  const float inv = 1.f / (l_tot > 0.f ? l_tot : 1.f);  // empty rows: O = 0; NaN rows stay NaN
   if (qvalid) {
     uint16_t* orow = obase + (int64_t)qrow * p.so[2];
 #pragma unroll

@@ -144,7 +144,10 @@ def gate_target_from_qk(
     nb = math.ceil(S / block_size)
     mask_buf, mask_strides = None, None
     if attention_mask is not None:
-        mask_buf, mask_strides = _padded_attention_mask(attention_mask, B, H, S, nb * block_size, q.device)
+        # The kernels read a mask up to a multiple of 64 rows and keys as well (block 32 runs
+        # over 64-token blocks).
+        padded = max(nb * block_size, 64 * math.ceil(S / 64))
+        mask_buf, mask_strides = _padded_attention_mask(attention_mask, B, H, S, padded, q.device)
     out = torch.empty((B, H, nb, nb), dtype=torch.float32, device=q.device)
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
     status = lib.tasft_gate_target_fwd(

@@ -96,6 +96,9 @@ PREFILL_CASES = [
     (1, 4, 2, 600, 128, 32, True, 0.4, "gen"),
     (1, 2, 2, 520, 64, 128, True, 0.6, "gen"),
     (1, 4, 4, 300, 64, 32, False, 0.5, "gen"),
+    # Rows longer than 128 key blocks (three 64-byte mask chunks per row), G=7.
+    (1, 7, 1, 8300, 128, 64, True, 0.08, "2w"),
+    (1, 2, 1, 8300, 128, 64, False, 0.08, "2w"),
 ]
 
 # Varlen prefill: (lens, Hq, Hkv, D, bs, causal, density).

@@ -87,3 +87,38 @@ def round_f16(x: np.ndarray) -> np.ndarray:
 def require_gpu() -> torch.device:
     assert torch.cuda.is_available(), "this test needs a ROCm GPU"
     return torch.device("cuda:0")
+
+
+def write_bundle(root, gates, per_head, hidden_in_cfg=True, block_size=64, scalar_tau=0.5):
+    """A bundle laid out as the reference exporter writes it (tasft/bundle/export.py:193-290):
+    fp32 gate state dicts, kernel_config.json with the exporter's fields, manifest.json.
+
+    ``gates`` maps layer index to an ``AttnGate``; ``per_head`` maps a layer index to its
+    per-head thresholds (other layers get the scalar ``scalar_tau``)."""
+    import hashlib
+    import json
+
+    from safetensors.torch import save_file
+
+    (root / "gates").mkdir()
+    (root / "model").mkdir()
+    for i, g in gates.items():
+        save_file({k: v.cpu().float() for k, v in g.state_dict().items()},
+                  str(root / "gates" / f"layer_{i}_gate.safetensors"))
+    (root / "model" / "model.safetensors").write_bytes(b"not read by the gate loader")
+    layers = {}
+    for i, g in gates.items():
+        layers[str(i)] = {"layer_idx": i, "threshold_tau": scalar_tau, "target_sparsity": 0.7,
+                          "achieved_sparsity_validation": 0.7, "gate_loss_validation": 0.0,
+                          "block_size": block_size}
+        if hidden_in_cfg:
+            layers[str(i)]["gate_hidden_dim"] = g.gate_hidden_dim
+        if i in per_head:
+            layers[str(i)]["threshold_tau_per_head"] = [float(t) for t in per_head[i]]
+    (root / "kernel_config.json").write_text(json.dumps(
+        {"block_size": block_size, "global_threshold": scalar_tau, "per_layer_config": layers,
+         "min_sparsity_for_speedup": 0.5}))
+    files = sorted((root / "model").iterdir()) + sorted((root / "gates").iterdir()) + [root / "kernel_config.json"]
+    sums = {str(f.relative_to(root)): hashlib.sha256(f.read_bytes()).hexdigest() for f in files}
+    (root / "manifest.json").write_text(json.dumps({"model_name": "t", "num_layers": len(gates),
+                                                    "checksums": sums}))

@@ -120,7 +120,9 @@ MASK_CASES = [
     (2, 8, 2, 700, 128, 64, "padding_2d"),    # four heads per workgroup, ragged, key padding
     (2, 4, 2, 640, 64, 64, "binary_2d"),      # two heads per workgroup; the reference adds 1/0
     (2, 3, 3, 333, 128, 64, "hf_4d"),         # one head per workgroup, HF [B, 1, S, S] mask
-    (1, 4, 2, 300, 128, 32, "per_head_4d"),   # generic kernel, full per-head mask
+    (1, 4, 2, 300, 128, 32, "per_head_4d"),   # block 32 (32 x 32 quarters), per-head mask
+    (2, 8, 2, 700, 128, 32, "padding_2d"),    # block 32, key padding, 22 blocks (11 of 64)
+    (1, 4, 2, 330, 64, 32, "hf_4d"),          # block 32, odd block count: mask read to 384
     (2, 2, 1, 400, 64, 128, "padding_2d"),    # block 128: block-64 maxima pooled 2x2
     (1, 4, 4, 333, 128, 128, "hf_4d"),        # block 128, odd block-64 count, HF mask
 ]

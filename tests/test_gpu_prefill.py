@@ -187,9 +187,23 @@ def test_config2_gate_chain_full_size_sampled_heads():
 
 
 def test_config4_full_size_sampled_heads():
+    """Config 4 (Qwen-2.5-7B: 28/4 heads, G=7, rows of up to 256 key blocks, i.e. four
+    64-byte mask chunks per row) at full size, on the benchmark inputs and again on
+    unit-scale inputs under the same mask, where the softmax is far from uniform. The
+    sampled heads include the first and last query head of a KV group."""
+    dev = require_gpu()
     shape = wl.CONFIG_SHAPES[4]
     mask, _ = wl.qwen_mask(shape, 2004)
-    _sampled_parity(4, mask, 1004, heads=[(0, 0), (1, 27)])
+    heads = [(0, 0), (0, 6), (1, 13), (1, 27)]
+    _sampled_parity(4, mask, 1004, heads=heads)
+    q, k, v = wl.qkv(shape, 1004)
+    qu, ku, vu = ai.qkv("unit", tuple(q.shape), tuple(k.shape), 4004, shape.block)
+    del q, k, v
+    out = _run(qu.to(dev), ku.to(dev), vu.to(dev), mask.to(dev), shape.block, True).cpu()
+    ref = orc.attention_block_gather(to_np(qu), to_np(ku), to_np(vu), mask.numpy(), shape.block,
+                                     True, heads=heads)
+    for b, h in heads:
+        assert_close_bf16(out[b, h], ref[b, h], f"config 4 unit-scale head ({b},{h})")
 
 
 def _prefill_capi(q, k, v, mask, bs, causal, workspace=None):
@@ -331,3 +345,45 @@ def test_prefill_varlen_one_sequence_is_bit_identical_to_forward():
                                  max_seqlen=T, causal=True)
     torch.cuda.synchronize()
     assert torch.equal(packed, dense[0].transpose(0, 1))
+
+
+def _expand128(mask128: torch.Tensor, nb64: int) -> torch.Tensor:
+    """A block-128 mask as the equivalent block-64 mask: every 128-token block is its four
+    64-token quarters."""
+    return mask128.repeat_interleave(2, -1).repeat_interleave(2, -2)[..., :nb64, :nb64].contiguous()
+
+
+@pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "causal"), [
+    (1, 8, 2, 1000, 128, True),    # two-wave kernel, ragged: the last 128-block is partial
+    (2, 4, 2, 1500, 64, True),     # four-wave kernel through its persistent work queue
+    (1, 4, 4, 777, 128, False),    # non-causal, ragged
+])
+def test_block128_is_bit_identical_to_expanded_block64(B, Hq, Hkv, S, D, causal):
+    """A block-128 mask runs on the block-64 kernels through the mask index shift; the
+    output must equal, bit for bit, the block-64 launch on the 2x2-expanded mask."""
+    dev = require_gpu()
+    print(f"block128 bit identity B={B} Hq={Hq} Hkv={Hkv} S={S} D={D} causal={causal}", flush=True)
+    q, k, v = ai.qkv("unit", (B, Hq, S, D), (B, Hkv, S, D), 8800 + S + D, 128)
+    nb128, nb64 = math.ceil(S / 128), math.ceil(S / 64)
+    mask = ai.random_mask((B, Hq, nb128, nb128), 0.4, 8900 + S)
+    mask[0, 0, -1, :] = True
+    q, k, v, mask = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    a = _run(q, k, v, mask, 128, causal)
+    b = _run(q, k, v, _expand128(mask, nb64), 64, causal)
+    assert torch.equal(a, b)
+
+
+def test_block128_varlen_is_bit_identical_to_expanded_block64():
+    dev = require_gpu()
+    lens, Hq, Hkv, D = [513, 200, 64, 1], 7, 1, 128
+    q, k, v, cu = ai.packed_qkv("unit", lens, Hq, Hkv, D, 9010, 128)
+    nb128, nb64 = math.ceil(max(lens) / 128), math.ceil(max(lens) / 64)
+    mask = ai.random_mask((len(lens), Hq, nb128, nb128), 0.5, 9011)
+    bsfa128 = BlockSparseFlashAttention(block_size=128, min_sparsity_for_speedup=0.0)
+    bsfa64 = BlockSparseFlashAttention(block_size=64, min_sparsity_for_speedup=0.0)
+    cu_t = torch.tensor(cu, dtype=torch.int32)
+    q, k, v, mask = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    a = bsfa128.forward_varlen(q, k, v, mask, cu_t, causal=True)
+    b = bsfa64.forward_varlen(q, k, v, _expand128(mask, nb64), cu_t, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import write_bundle
 from tasft_amd.exceptions import KernelError, NaNDetectedError, TASFTError, ValidationError
 from tasft_amd.kernels import (
     BlockSparseFlashAttention,
@@ -394,38 +395,6 @@ def test_kernel_config_loads_reference_and_exporter_files_and_per_head_threshold
 
 
 # ----------------------------------------------------------------------------- bundle gates
-def _write_bundle(root, gates, per_head, hidden_in_cfg=True):
-    """A bundle laid out as the reference exporter writes it (tasft/bundle/export.py:193-290):
-    fp32 gate state dicts, kernel_config.json with the exporter's fields, manifest.json."""
-    import hashlib
-    import json
-
-    from safetensors.torch import save_file
-
-    (root / "gates").mkdir()
-    (root / "model").mkdir()
-    for i, g in gates.items():
-        save_file({k: v.cpu().float() for k, v in g.state_dict().items()},
-                  str(root / "gates" / f"layer_{i}_gate.safetensors"))
-    (root / "model" / "model.safetensors").write_bytes(b"not read by the gate loader")
-    layers = {}
-    for i, g in gates.items():
-        layers[str(i)] = {"layer_idx": i, "threshold_tau": 0.5, "target_sparsity": 0.7,
-                          "achieved_sparsity_validation": 0.7, "gate_loss_validation": 0.0,
-                          "block_size": 64}
-        if hidden_in_cfg:
-            layers[str(i)]["gate_hidden_dim"] = g.gate_hidden_dim
-        if i in per_head:
-            layers[str(i)]["threshold_tau_per_head"] = per_head[i]
-    (root / "kernel_config.json").write_text(json.dumps(
-        {"block_size": 64, "global_threshold": 0.5, "per_layer_config": layers,
-         "min_sparsity_for_speedup": 0.5}))
-    files = sorted((root / "model").iterdir()) + sorted((root / "gates").iterdir()) + [root / "kernel_config.json"]
-    sums = {str(f.relative_to(root)): hashlib.sha256(f.read_bytes()).hexdigest() for f in files}
-    (root / "manifest.json").write_text(json.dumps({"model_name": "t", "num_layers": len(gates),
-                                                    "checksums": sums}))
-
-
 def test_bundle_gates_keep_trained_width_and_per_head_thresholds(tmp_path):
     from tasft_amd.exceptions import BundleError, ChecksumError
     from tasft_amd.inference.bundle_gates import load_bundle_gates
@@ -434,7 +403,7 @@ def test_bundle_gates_keep_trained_width_and_per_head_thresholds(tmp_path):
     gates = {0: AttnGate(num_heads=4, head_dim=32, gate_hidden_dim=48),   # non-default width
              1: AttnGate(num_heads=4, head_dim=32)}                       # default width (32)
     per_head = {0: [0.3, 0.4, 0.5, 0.6]}
-    _write_bundle(tmp_path, gates, per_head)
+    write_bundle(tmp_path, gates, per_head)
     bg = load_bundle_gates(tmp_path, num_heads=4, head_dim=32)
     assert sorted(bg.gates) == [0, 1]
     assert bg.gates[0].gate_hidden_dim == 48 and bg.gates[1].gate_hidden_dim == 32
@@ -454,6 +423,6 @@ def test_bundle_gates_keep_trained_width_and_per_head_thresholds(tmp_path):
     with pytest.raises(ChecksumError):
         load_bundle_gates(tmp_path, num_heads=4, head_dim=32)
     (tmp_path / "b2").mkdir()
-    _write_bundle(tmp_path / "b2", {0: gates[0]}, {})
+    write_bundle(tmp_path / "b2", {0: gates[0]}, {})
     with pytest.raises(BundleError, match="head_dim=64"):
         load_bundle_gates(tmp_path / "b2", num_heads=4, head_dim=64)

@@ -185,6 +185,64 @@ def test_attention_matches_brute_force(causal):
     assert (orc.attention_dense_masked(q, k, v, mask, bs, causal, 0.7)[0, 1, 4:8] == 0).all()
 
 
+def _nan_pattern(q, k, v, mask, bs, causal):
+    """Where the reference kernel's output is NaN (block_sparse_fa.py:215-257): a NaN score
+    among a row's allowed keys makes p, l and the whole accumulator row NaN, and the division
+    by ``where(l > 0, l, 1)`` keeps it (a NaN score at a masked element is replaced by -inf,
+    :243). V is multiplied per active block (:252), so a NaN in V[j, d] reaches column d of
+    every row whose block row has key j's block active, also where the element mask gives
+    p = 0 (0 * NaN is NaN). Explicit loops over the allowed keys and active blocks."""
+    B, H, S, D = q.shape
+    g = H // k.shape[1]
+    out = np.zeros(q.shape, dtype=bool)
+    for b in range(B):
+        for h in range(H):
+            for i in range(S):
+                in_block = [j for j in range(k.shape[2]) if mask[b, h, i // bs, j // bs]
+                            and not (causal and j // bs > i // bs)]
+                allowed = [j for j in in_block if not (causal and j > i)]
+                if not allowed:
+                    continue
+                if np.isnan(q[b, h, i]).any() or any(np.isnan(k[b, h // g, j]).any() for j in allowed):
+                    out[b, h, i] = True
+                    continue
+                for j in in_block:
+                    out[b, h, i] |= np.isnan(v[b, h // g, j])
+    return out
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_nan_follows_reference_normalisation(causal):
+    """NaN in Q, K or V propagates as in the reference kernel; empty rows stay exactly 0.
+    The block-gather oracle (the checker of the kernels) follows the kernel's per-block V
+    product; the dense oracle agrees when no inactive key of V holds a NaN."""
+    rng = np.random.default_rng(16)
+    B, H, Hkv, S, D, bs = 1, 4, 2, 13, 5, 4
+    q = rng.standard_normal((B, H, S, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, D)).astype(np.float32)
+    q[0, 0, 6, 2] = np.nan
+    k[0, 1, 3, 0] = np.nan
+    v[0, 0, 9, 4] = np.nan
+    nb = math.ceil(S / bs)
+    mask = rng.random((B, H, nb, nb)) < 0.6
+    mask[0, 3, 1, :] = False  # an empty block row
+    want = _nan_pattern(q, k, v, mask, bs, causal)
+    assert want.any() and not want.all()
+    got = orc.attention_block_gather(q, k, v, mask, bs, causal=causal)
+    np.testing.assert_array_equal(np.isnan(got), want)
+    assert (got[0, 3, 4:8] == 0).all()
+    clean = ~want
+    ref = orc.attention_block_gather(np.nan_to_num(q), np.nan_to_num(k), np.nan_to_num(v), mask, bs,
+                                     causal)
+    # Rows and columns that no NaN reaches are unchanged by it.
+    np.testing.assert_allclose(got[clean], ref[clean], rtol=1e-6, atol=1e-7)
+    v2 = np.nan_to_num(v)
+    want2 = _nan_pattern(q, k, v2, mask, bs, causal)
+    dense = orc.attention_dense_masked(q, k, v2, mask, bs, causal=causal)
+    np.testing.assert_array_equal(np.isnan(dense), want2)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_all_true_mask_equals_sdpa(causal):
     rng = np.random.default_rng(7)
