@@ -185,8 +185,10 @@ int tasft_bsfa_decode_fwd_noalloc(const void* q, const void* k_cache, const void
  * a table entry outside [0, num_pages) is clamped into it, so a corrupt table gives wrong
  * values but never reads outside the pools. kv_lens: device int32 [B], required.
  * kv_len_max bounds every kv_lens[b]; block_mask [B, Hq, 1, ceil(kv_len_max/bs)].
- * block_size 32 or 64; page_size a power of two >= 8. Other arguments as in
- * tasft_bsfa_decode_fwd (same workspace size).
+ * block_size 32, 64 or 128 (vLLM's per-layer block size, tasft/inference/vllm_patch.py:522-525;
+ * a 128-key block is read as its two 64-key halves, and num_splits then counts 64-key
+ * blocks: ceil(kv_len_max/64) / num_splits <= 1024); page_size a power of two >= 8.
+ * Other arguments as in tasft_bsfa_decode_fwd (same workspace size).
  */
 int tasft_bsfa_decode_paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                                 void* out, const uint8_t* block_mask,

@@ -53,6 +53,9 @@ struct DecodeParams {
   int64_t bt_stride;
   int page_size;
   int num_pages;
+  // Mask index shift: key block t reads mask entry t >> mshift. 1 runs a block-128 mask on
+  // the block-64 kernel (a 128-key block is its two 64-key halves); 0 otherwise.
+  int mshift;
 };
 
 // Raw buffer resource (stride 0) over `bytes` bytes starting at `base`.
@@ -130,7 +133,7 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     uint32_t bitsv = 0;
 #pragma unroll
     for (int gg = 0; gg < MG; ++gg)
-      if (gg < G && mbase[(int64_t)gg * p.sm[1] + (int64_t)t * p.sm[2]]) bitsv |= 1u << gg;
+      if (gg < G && mbase[(int64_t)gg * p.sm[1] + (int64_t)(t >> p.mshift) * p.sm[2]]) bitsv |= 1u << gg;
     return bitsv;
   };
   if constexpr (NSUB != 1) {
@@ -725,6 +728,7 @@ static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, v
   p.bt_stride = 0;
   p.page_size = 0;
   p.num_pages = 0;
+  p.mshift = 0;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
@@ -840,18 +844,21 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
   if (head_dim != 64 && head_dim != 128)
     return set_error(kErrUnsupported, "decode_paged: head_dim must be 64 or 128, got %lld",
                      (long long)head_dim);
-  if (block_size != 32 && block_size != 64)
-    return set_error(kErrUnsupported, "decode_paged: block_size must be 32 or 64, got %lld",
+  if (block_size != 32 && block_size != 64 && block_size != 128)
+    return set_error(kErrUnsupported, "decode_paged: block_size must be 32, 64 or 128, got %lld",
                      (long long)block_size);
   if (page_size < 8 || page_size > 4096 || (page_size & (page_size - 1)) != 0)
     return set_error(kErrUnsupported,
                      "decode_paged: page_size must be a power of two in [8, 4096], got %lld",
                      (long long)page_size);
-  const int64_t nb = (kv_len_max + block_size - 1) / block_size;
+  // A block-128 mask runs on the block-64 kernel: each selected 128-key block is read as
+  // its two 64-key halves (mask entry t >> 1 for half t), so the split counts 64-key blocks.
+  const int64_t run_bs = block_size == 128 ? 64 : block_size;
+  const int64_t nb = (kv_len_max + run_bs - 1) / run_bs;
   if ((nb + num_splits - 1) / num_splits > kDecodeMaxRange)
     return set_error(kErrInvalidArgument,
-                     "decode_paged: num_splits must be >= ceil(num_blocks / %d) (got %lld for %lld blocks)",
-                     kDecodeMaxRange, (long long)num_splits, (long long)nb);
+                     "decode_paged: num_splits must be >= ceil(num_blocks / %d) (got %lld for %lld blocks of %lld keys)",
+                     kDecodeMaxRange, (long long)num_splits, (long long)nb, (long long)run_bs);
   const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
   if (workspace_bytes < need)
     return set_error(kErrWorkspace, "decode_paged: workspace too small: need %zu bytes, got %zu",
@@ -914,11 +921,12 @@ extern "C" int tasft_bsfa_decode_paged_fwd(
   p.bt_stride = block_table_stride;
   p.page_size = (int)page_size;
   p.num_pages = (int)num_pages;
+  p.mshift = block_size == 128 ? 1 : 0;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128, true>(p, dtype, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64, true>(p, dtype, s);
+  if (run_bs == 64 && head_dim == 128) err = launch_decode<64, 128, true>(p, dtype, s);
+  else if (run_bs == 64 && head_dim == 64) err = launch_decode<64, 64, true>(p, dtype, s);
   else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128, true>(p, dtype, s);
   else err = launch_decode<32, 64, true>(p, dtype, s);
   if (err != hipSuccess)

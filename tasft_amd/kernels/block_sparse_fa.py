@@ -537,9 +537,6 @@ class BlockSparseFlashAttention:
         if kv_lens.shape != (B,):
             raise KernelError(f"kv_lens must have shape ({B},), got {tuple(kv_lens.shape)}",
                               context={"kv_lens": list(kv_lens.shape)})
-        if self.block_size not in (32, 64):
-            raise KernelError(f"paged decode supports block_size 32 or 64, got {self.block_size}",
-                              context={"block_size": self.block_size})
         if page_size < 8 or page_size & (page_size - 1):
             raise KernelError(f"page_size must be a power of two >= 8, got {page_size}",
                               context={"page_size": page_size})
@@ -571,7 +568,9 @@ class BlockSparseFlashAttention:
             )
         lib = _native.load_library()
         if num_splits is None:
-            num_splits = default_decode_splits(B, Hkv, nb, H // Hkv)
+            # A block-128 mask runs on the 64-key kernel (each 128-key block as its halves).
+            nb_run = math.ceil(S_kv / 64) if self.block_size == 128 else nb
+            num_splits = default_decode_splits(B, Hkv, nb_run, H // Hkv)
         q = q.contiguous()
         k_pages = _kernel_ready(k_pages)
         v_pages = _kernel_ready(v_pages)

@@ -124,6 +124,7 @@ PAGED_CASES = [
     (3, 32, 8, 1000, 128, 64, 16, None),
     (2, 8, 2, 900, 128, 64, 64, 1),
     (2, 8, 1, 700, 64, 32, 16, 3),
+    (2, 8, 2, 1000, 128, 128, 16, None),
 ]
 
 

@@ -182,7 +182,20 @@ PAGED_CASES = [
     (2, 4, 4, 512, 64, 64, 64, None),      # page = block, D=64
     (2, 8, 1, 300, 128, 32, 64, None),     # page larger than the block
     (1, 16, 2, 640, 64, 32, 16, 3),
+    (3, 32, 8, 1000, 128, 128, 16, None),  # block 128 (two 64-key halves), partial last block
+    (2, 8, 2, 900, 64, 128, 64, 2),
 ]
+
+
+def _contig_reference(bsfa, q, k, v, mask, lens, splits):
+    """The contiguous decode the paged one must equal bit for bit. A block-128 mask runs on
+    the 64-key kernel, as the contiguous call on the same mask expanded to 64-key blocks."""
+    if bsfa.block_size != 128:
+        return bsfa.forward_decode(q, k, v, mask, kv_lens=lens, num_splits=splits)
+    nb64 = math.ceil(k.shape[2] / 64)
+    m64 = mask.repeat_interleave(2, -1)[..., :nb64].contiguous()
+    return BlockSparseFlashAttention(block_size=64, min_sparsity_for_speedup=0.0).forward_decode(
+        q, k, v, m64, kv_lens=lens, num_splits=splits)
 
 
 @pytest.mark.parametrize(("B", "Hq", "Hkv", "S", "D", "bs", "ps", "splits"), PAGED_CASES)
@@ -213,8 +226,7 @@ def test_decode_paged_equals_contiguous_and_oracle(B, Hq, Hkv, S, D, bs, ps, spl
     bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
     paged = bsfa.forward_decode_paged(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
                                       lens.to(dev), mask.to(dev), num_splits=splits)
-    contig = bsfa.forward_decode(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
-                                 kv_lens=lens.to(dev), num_splits=splits)
+    contig = _contig_reference(bsfa, q.to(dev), k.to(dev), v.to(dev), mask.to(dev), lens.to(dev), splits)
     torch.cuda.synchronize()
     assert torch.equal(paged, contig)
     ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),
@@ -232,8 +244,7 @@ def test_decode_paged_discriminating_inputs(case, kind):
     bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
     paged = bsfa.forward_decode_paged(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
                                       lens.to(dev), mask.to(dev), num_splits=splits)
-    contig = bsfa.forward_decode(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
-                                 kv_lens=lens.to(dev), num_splits=splits)
+    contig = _contig_reference(bsfa, q.to(dev), k.to(dev), v.to(dev), mask.to(dev), lens.to(dev), splits)
     torch.cuda.synchronize()
     assert torch.equal(paged, contig)
     ref = orc.sparse_decode_paged(to_np(q), to_np(kp), to_np(vp), table.numpy(), lens.numpy(),

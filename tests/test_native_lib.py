@@ -83,7 +83,7 @@ def test_invalid_arguments_return_errors_without_launch():
                                            64, _i64([8, 8, 2]), st3, st3, st3, st, 1.0, 1, 0, None)
     assert rc == -1 and b"contiguous" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
-                                         8, 1024, 128, 128, 16, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
+                                         8, 1024, 128, 256, 16, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
     assert rc == -2 and b"block_size" in lib.tasft_last_error()
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
                                          8, 1024, 128, 64, 12, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
