@@ -224,8 +224,8 @@ def bench_decode(torch, dev, steps, warmup):
 
 
 def bench_decode_qwen(torch, dev, steps, warmup):
-    """Decode with seven query heads per KV head (Qwen-2.5-7B: 28/4 heads, the kernel built
-    for up to eight heads) at the config-3 batch, cache length and selection density."""
+    """Decode with seven query heads per KV head (Qwen-2.5-7B: 28/4 heads; the kernel takes
+    up to 16) at the config-3 batch, cache length and selection density."""
     from tasft_amd import workloads as wl
     from tasft_amd.kernels import BlockSparseFlashAttention
 

@@ -129,13 +129,13 @@ size_t tasft_bsfa_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int
  * block_mask [B, Hq, 1, ceil(kv_len_max/bs)] bytes; kv_lens [B] int32 valid lengths
  * (NULL = kv_len_max). Every KV block selected by any query head of a KV head is read
  * once for that KV head. workspace: >= tasft_bsfa_decode_workspace_bytes(...) bytes,
- * 16-byte aligned. At most 8 query heads per KV head. num_splits >= ceil(num_blocks /
- * 1024); for block sizes up to 64 the splits of a (b, KV head) share its selected blocks
+ * 16-byte aligned. At most 16 query heads per KV head. A 128-key block is read as its
+ * two 64-key halves, and num_blocks below counts those halves. num_splits >=
+ * ceil(num_blocks / 1024); the splits of a (b, KV head) share its selected blocks
  * equally, and with num_splits == 1 the output is written without a combine pass.
  * Results differ between split counts only by float rounding. One launch runs
- * batch * num_kv_heads * num_splits workgroups; all are resident at once up to 512 (two
- * per CU) for at most 4 query heads per KV head and up to 256 (one per CU) for 5 to 8,
- * and a split count that fills the GPU once measured fastest.
+ * batch * num_kv_heads * num_splits workgroups (two fit per CU); about one per CU
+ * measured fastest.
  */
 int tasft_bsfa_decode_fwd(const void* q, const void* k_cache, const void* v_cache, void* out,
                           const uint8_t* block_mask, const int32_t* kv_lens, void* workspace,

@@ -9,17 +9,19 @@
 // over the tokens < kv_len of the key blocks selected for query head h; a head with no
 // selected block outputs 0.
 //
-// Data path. A workgroup owns (batch b, KV head kvh, split s). For blocks of up to 64
-// keys the split is a share of the selected blocks: the blocks selected by any of the G
-// query heads of kvh are numbered in block order and split s takes entries
-// [s*n/P, (s+1)*n/P), so the splits of a row do equal work. (For 128-key blocks it is
-// the contiguous range of key blocks [s*NB/P, (s+1)*NB/P).) Its 4 waves take the
+// Data path. A workgroup owns (batch b, KV head kvh, split s). The split is a share of
+// the selected blocks: the blocks selected by any of the G query heads of kvh are
+// numbered in block order and split s takes entries [s*n/P, (s+1)*n/P), so the splits of
+// a row do equal work (a 128-key block counts as its two 64-key halves). Its 4 waves take the
 // blocks round-robin. Each selected KV block is read from HBM once per KV
 // head, however many query heads chose it; all its K and V loads are issued together.
-// QK^T runs on MFMA (v_mfma_f32_32x32x16_bf16, or _f16 for fp16 inputs; K is loaded straight into the A-operand
-// layout, the G query heads are the N columns), PV on the VALU. Partial
-// (max, sum, output) triples per (b, h, split) go to a caller-provided workspace and a
-// second kernel merges them.
+// QK^T and PV both run on v_mfma_f32_16x16x32_bf16 (_f16 for fp16 inputs) with the G <= 16
+// query heads of the KV head as the 16 N columns: K is loaded from HBM straight into the
+// A-operand layout, V arrives in LDS by DMA and is read transposed (ds_read_b64_tr_b16) as
+// the A operand of PV, and each lane's scores, probabilities and output columns belong
+// to one head, so the softmax needs no LDS exchange. With one split the workgroup writes
+// the output row; with several, partial (max, sum, output) triples per (b, h, split) go to
+// a caller-provided workspace and a second kernel merges them.
 #include "common.h"
 
 #include <mutex>
@@ -28,7 +30,7 @@
 
 namespace tasft {
 
-constexpr int kDecodeMaxG = 8;    // query heads per KV head handled by one workgroup
+constexpr int kDecodeMaxG = 16;   // query heads per KV head handled by one workgroup
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeMaxRange = 1024;  // key blocks per split (mask bytes staged in LDS)
 
@@ -80,38 +82,68 @@ __device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int voff
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-// SUB keys (<= 64) of one KV block are processed at a time; a block of BS keys is
-// BS/SUB sub-blocks. MG >= G is the head count the loops are unrolled for (padding heads
-// carry zero probability). Up to four heads run two waves per SIMD (at most 256
-// registers each, two workgroups per CU). Five to eight heads need more than that: built
-// for two waves per SIMD they spilled about 120 bytes per lane to scratch inside the
-// block loop, so they run one wave per SIMD (up to 512 registers, one workgroup per CU).
-template <int BS, int D, int MG, bool PAGED, int DT>
-__global__ void __launch_bounds__(kDecodeWaves * kWave, MG == 8 ? 1 : 2)
-bsfa_decode_split_kernel(const DecodeParams p) {
-  static_assert(!PAGED || BS <= 64, "paged caches use the one-sub-block path");
-  constexpr int SUB = BS < 64 ? BS : 64;
-  constexpr int NSUB = BS / SUB;
-  constexpr int KT = SUB / 32;        // 32-key MFMA tiles per sub-block
-  constexpr int KSTEPS = D / 16;      // MFMA k-steps over the head dim
-  constexpr int DOCT = D / 8;         // 16-byte chunks per row
-  constexpr int KG = kWave / DOCT;    // key groups in the PV phase
-  constexpr int VPL = SUB / KG;       // V rows per lane per sub-block
+// v_mfma_f32_16x16x32_{bf16,f16}: 8 elements per lane of A and B as raw words.
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma32k(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
 
-  constexpr int VTILE = SUB * D * 2;  // bytes of one sub-block of V
+// 16-byte chunk position of chunk `cc` of V row `r` in a wave's LDS tile. The PV operand
+// reads (ds_read_b64_tr_b16) of 32 lanes touch rows r0 .. r0+7 (D = 128) or r0 .. r0+7
+// with two 128-byte rows per 256 bytes (D = 64), two chunks each; the XOR spreads those
+// 16 chunks over all 64 banks.
+template <int D>
+__device__ __forceinline__ int swz_dv(int r, int cc) {
+  return D == 128 ? (cc ^ ((r & 7) << 1)) : (cc ^ (((r >> 1) & 3) << 1));
+}
+
+// The rotate-swap helpers of a 16-lane group: max / sum over the four lanes l % 16 + 16 g.
+__device__ __forceinline__ float quad16_max(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return pair_max32(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float quad16_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return pair_sum32(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+
+// Keys of one KV block (BS = 32 or 64; a 128-key block runs as its two halves through the
+// mask index shift) are processed by one wave. QK^T and PV both run on
+// v_mfma_f32_16x16x32 with the query heads of the KV head as the 16 N columns (columns
+// >= G carry zero queries and zero probabilities), so a lane owns one head: its scores,
+// probabilities, rescale factor and output columns stay in its registers, and P^T is
+// directly the B operand of the PV product. Up to 16 heads run two waves per SIMD.
+template <int BS, int D, bool PAGED, int DT>
+__global__ void __launch_bounds__(kDecodeWaves * kWave, 2)
+bsfa_decode_split_kernel(const DecodeParams p) {
+  static_assert(BS == 32 || BS == 64, "32- or 64-key blocks");
+  constexpr int NT = BS / 16;         // 16-key score tiles per block
+  constexpr int NC = BS / 32;         // 32-key PV k-steps per block
+  constexpr int KS = D / 32;          // 32-dim QK k-steps
+  constexpr int DT16 = D / 16;        // 16-dim output tiles
+  constexpr int ROWB = D * 2;         // bytes of one K/V row
+  constexpr int VTILE = BS * ROWB;    // bytes of one block of V
+  constexpr int RPU = 1024 / ROWB;    // V rows per 1 KB DMA unit
+  constexpr int CPR = ROWB / 16;      // 16-byte chunks per row
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kDecodeWaves][VTILE];  // per-wave V tile
-  __shared__ uint8_t hb[kDecodeMaxRange];  // head bits per block of the range / per entry
-  __shared__ int sel[kDecodeMaxRange];      // selected blocks (range offsets / block indices)
+  __shared__ uint16_t hb[kDecodeMaxRange];  // head bits per selected entry
+  __shared__ int sel[kDecodeMaxRange];      // selected blocks
   __shared__ int wsum[kDecodeWaves];
-  __shared__ float p_lds[kDecodeWaves][SUB * MG + kWave];     // probabilities (+ dummy slots)
-  __shared__ float a_lds[kDecodeWaves][MG];                   // rescale factor per head
-  __shared__ float comb_ml[kDecodeWaves][MG][2];
+  __shared__ float comb_ml[kDecodeWaves][kDecodeMaxG][2];
+  static_assert(kDecodeMaxG * D * 4 <= VTILE, "merge buffer size");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop state
-  const int col = lane & 31;   // QK layout: query head of this lane
-  const int half = lane >> 5;
+  const int hc = lane & 15;   // query head (MFMA column) of this lane
+  const int g4 = lane >> 4;   // lane group: keys 4*g4.. of a score tile, k slots 8*g4..
   const int G = p.G;
 
   const int64_t item = blockIdx.x;
@@ -123,436 +155,274 @@ bsfa_decode_split_kernel(const DecodeParams p) {
 
   const int kv_len = p.kv_lens ? min(max(p.kv_lens[b], 0), p.S_kv) : p.S_kv;
   const int nb_valid = (kv_len + BS - 1) / BS;
-  const int lo = (int)(((int64_t)s * p.NB) / p.P);
-  const int hi = min((int)(((int64_t)(s + 1) * p.NB) / p.P), nb_valid);
-  const int range = max(hi - lo, 0);
 
   // Mask bits of key block t for the group's heads.
   const uint8_t* mbase = p.mask + b * p.sm[0] + (int64_t)h0 * p.sm[1];
   auto head_bits = [&](int t) -> uint32_t {
     uint32_t bitsv = 0;
-#pragma unroll
-    for (int gg = 0; gg < MG; ++gg)
-      if (gg < G && mbase[(int64_t)gg * p.sm[1] + (int64_t)(t >> p.mshift) * p.sm[2]]) bitsv |= 1u << gg;
+    for (int gg = 0; gg < G; ++gg)
+      if (mbase[(int64_t)gg * p.sm[1] + (int64_t)(t >> p.mshift) * p.sm[2]]) bitsv |= 1u << gg;
     return bitsv;
   };
-  if constexpr (NSUB != 1) {
-    // Mask bytes of the range for the group's heads, one round trip.
-    for (int t = tid; t < range; t += kDecodeWaves * kWave) hb[t] = (uint8_t)head_bits(lo + t);
-  }
-
-  // Q^T as the MFMA B operand: lane (col, half) holds head h0+col, head dims
-  // ks*16 + half*8 .. +7. Columns >= G are zero.
-  u32x4_t qf[KSTEPS];
+  // Q^T as the B operand: lane (hc, g4) holds head h0+hc, head dims 32 ks + 8 g4 .. +7.
+  u32x4_t qf[KS];
   {
-    const bool hv = col < G;
-    const uint16_t* qrow = p.q + b * p.sq[0] + (int64_t)(h0 + (hv ? col : 0)) * p.sq[1];
+    const bool hv = hc < G;
+    const uint16_t* qrow = p.q + b * p.sq[0] + (int64_t)(h0 + (hv ? hc : 0)) * p.sq[1];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       u32x4_t val = {0u, 0u, 0u, 0u};
-      if (hv) val = *(const u32x4_t*)(qrow + ks * 16 + half * 8);
+      if (hv) val = *(const u32x4_t*)(qrow + ks * 32 + g4 * 8);
       qf[ks] = val;
     }
   }
-  __syncthreads();
 
   const uint16_t* kbase = PAGED ? p.k + kvh * p.sk[1] : p.k + b * p.sk[0] + kvh * p.sk[1];
   const uint16_t* vbase = PAGED ? p.v + kvh * p.sv[1] : p.v + b * p.sv[0] + kvh * p.sv[1];
   const int ks2 = (int)p.sk[2], vs2 = (int)p.sv[2];  // row strides (elements)
 
-  // QK-layout state of this lane's head (identical in lanes l and l^32).
-  float m_run = -INFINITY, l_run = 0.f;
-  // PV-layout accumulators: lane (kg, dc) holds head dims dc*8..+7 of every head.
-  const int dc = lane % DOCT;
-  const int kg = lane / DOCT;
-  float oacc[MG][8];
+  float m_run = -INFINITY, l_run = 0.f;  // this lane's head (equal over its four lane groups)
+  f32x4_t oacc[DT16];                    // O^T tile dt: head hc, dims 16 dt + 4 g4 + j
 #pragma unroll
-  for (int gg = 0; gg < MG; ++gg)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) oacc[gg][i] = 0.f;
-  // Per-lane byte offsets inside a sub-block: K row `col` (A-operand layout); for the V
-  // DMA, lane l of unit u fetches byte u*1024 + 16*l of the row-major tile.
-  const int k_voff = (col * ks2 + half * 8) * 2;
-  // Unit u covers rows u*RPU .. u*RPU+RPU-1 (RPU = 1024 / row bytes): a per-lane base
-  // plus u * v_unit_stride. The whole offset stays in the per-lane (VGPR) offset, which
-  // the buffer range check covers, so rows past kv_len read as zeros.
-  constexpr int RPU = 1024 / (D * 2);
-  const int v_dma_base = (lane / (kWave / RPU)) * vs2 * 2 + (lane % (kWave / RPU)) * 16;
-  const int v_unit_stride = RPU * vs2 * 2;
-  // Where this lane's probabilities go in p_lds (lanes of padding heads: a dummy slot).
-  const bool pcol = col < MG;
+  for (int dt = 0; dt < DT16; ++dt) oacc[dt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  // K as the A operand: lane (hc, g4) loads key row 16 t + hc, dims 32 ks + 8 g4 .. +7.
+  const int k_voff = (hc * ks2 + g4 * 8) * 2;
+  // V DMA: lane l of unit u fetches the 16-byte chunk that the swizzle places at byte
+  // u*1024 + 16*l of the tile, i.e. row u*RPU + l/CPR, position l%CPR. The whole offset
+  // stays in the range-checked per-lane offset, so rows past kv_len read as zeros.
+  auto v_src_off = [&](int u) {
+    const int row = u * RPU + lane / CPR;
+    return row * vs2 * 2 + swz_dv<D>(row, lane % CPR) * 16;
+  };
+  // V^T operand reads: lane (t = hc, g4) of a 16-lane group addresses row r0 + t/4 and the
+  // 8 bytes of dims 16 dt + 4 (t%4) .. +3 (ds_read_b64_tr_b16 then hands lane t rows
+  // r0 .. r0+3 of dim 16 dt + t).
+  auto v_tr = [&](int r0, int dt) {
+    const int row = r0 + (hc >> 2);
+    const int d0 = dt * 16 + 4 * (hc & 3);
+    return ds_read_tr16_b64((const void*)(v_lds[wave] + row * ROWB + swz_dv<D>(row, d0 >> 3) * 16 + (d0 & 7) * 2));
+  };
 
-  if constexpr (NSUB == 1) {
-    // Selected blocks of the range, compacted once (wave 0), then taken round-robin by
-    // the waves. Each wave keeps the next block's loads in flight: its K loads are issued
-    // into the K registers as soon as the S MFMAs have read them, and its V DMA into the
-    // wave's V tile as soon as the PV product has read it.
-    // Balanced splits: the blocks selected by any head of the group are numbered over
-    // the whole row in block order, and split s takes entries [s*n/P, (s+1)*n/P) (a
-    // range split would give the splits of one row unequal counts). Two passes over the
-    // row's mask bytes: count, then gather this split's (block, head bits) entries.
-    // With one split the count pass is skipped: the split takes every entry.
-    constexpr int NT = kDecodeWaves * kWave;
-    int start = 0, end = 0x7fffffff;
-    if (p.P > 1) {
-      int cnt = 0;
-      for (int t = tid; t < nb_valid; t += NT) cnt += head_bits(t) != 0u ? 1 : 0;
+  // Selected blocks of the split, compacted once, then taken round-robin by the waves.
+  // Balanced splits: the blocks selected by any head of the group are numbered over the
+  // whole row in block order, and split s takes entries [s*n/P, (s+1)*n/P). With one split
+  // the count pass is skipped.
+  constexpr int NTH = kDecodeWaves * kWave;
+  int start = 0, end = 0x7fffffff;
+  if (p.P > 1) {
+    int cnt = 0;
+    for (int t = tid; t < nb_valid; t += NTH) cnt += head_bits(t) != 0u ? 1 : 0;
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
-      if (lane == 0) wsum[wave] = cnt;
-      __syncthreads();
-      const int n_all = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-      start = (int)(((int64_t)s * n_all) / p.P);
-      end = (int)(((int64_t)(s + 1) * n_all) / p.P);
-      __syncthreads();  // wsum is rewritten below
+    for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
+    if (lane == 0) wsum[wave] = cnt;
+    __syncthreads();
+    const int n_all = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    start = (int)(((int64_t)s * n_all) / p.P);
+    end = (int)(((int64_t)(s + 1) * n_all) / p.P);
+    __syncthreads();  // wsum is rewritten below
+  }
+  int base = 0;
+  for (int c0 = 0; c0 < nb_valid && base < end; c0 += NTH) {
+    const int t = c0 + tid;
+    const uint32_t bv = t < nb_valid ? head_bits(t) : 0u;
+    const uint64_t bal = __ballot(bv != 0u);
+    if (lane == 0) wsum[wave] = __popcll(bal);
+    __syncthreads();
+    int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
+    for (int w = 0; w < wave; ++w) pos += wsum[w];
+    if (bv != 0u && pos >= start && pos < end) {
+      sel[pos - start] = t;
+      hb[pos - start] = (uint16_t)bv;
     }
-    int base = 0;     // entries before this chunk (uniform)
-    for (int c0 = 0; c0 < nb_valid && base < end; c0 += NT) {
-      const int t = c0 + tid;
-      const uint32_t bv = t < nb_valid ? head_bits(t) : 0u;
-      const uint64_t bal = __ballot(bv != 0u);
-      if (lane == 0) wsum[wave] = __popcll(bal);
-      __syncthreads();
-      int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
-      for (int w = 0; w < wave; ++w) pos += wsum[w];
-      if (bv != 0u && pos >= start && pos < end) {
-        sel[pos - start] = t;
-        hb[pos - start] = (uint8_t)bv;
-      }
-      base += (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-      __syncthreads();
-    }
-    // Uniform values (scalar registers) keep the buffer resources scalar.
-    const int nsel = __builtin_amdgcn_readfirstlane(min(end, base) - start);
-    constexpr int NKL = KT * KSTEPS;  // K load instructions per block
-    u32x4_t ka[KT][KSTEPS];
-    // Paged cache: lane j < npg of `pgv` holds the page of the block's j-th page-sized
-    // piece (one block ahead of use, so its load is covered by the fixed V wait). A block
-    // of BS keys starts at row off0 of its first page.
-    constexpr int RPU_ = 1024 / (D * 2);
-    const int ps = p.page_size;
-    const int npg = ps >= BS ? 1 : BS / ps;
-    auto load_pg = [&](int kb) -> int {
-      const int first = (kb * BS) / ps;
-      // Only pages that hold a token below kv_len are read (later entries may not exist).
-      const int jmax = (kv_len - 1 - kb * BS + (kb * BS) % ps) / ps;
-      const int id = p.block_table[(int64_t)b * p.bt_stride + first + min(lane < npg ? lane : 0, jmax)];
-      return min(max(id, 0), p.num_pages - 1);
-    };
-    auto load_k_paged = [&](int kb, int pgv) {
-      const int key0 = kb * BS;
+    base += (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    __syncthreads();
+  }
+  const int nsel = __builtin_amdgcn_readfirstlane(min(end, base) - start);
+  constexpr int NKL = NT * KS;  // K load instructions per block
+  u32x4_t ka[NT][KS];
+  // Paged cache: lane j < npg of `pgv` holds the page of the block's j-th page-sized piece
+  // (one block ahead of use, so its load is covered by the fixed V wait).
+  const int ps = p.page_size;
+  const int npg = ps >= BS ? 1 : BS / ps;
+  auto load_pg = [&](int kb) -> int {
+    const int first = (kb * BS) / ps;
+    // Only pages that hold a token below kv_len are read (later entries may not exist).
+    const int jmax = (kv_len - 1 - kb * BS + (kb * BS) % ps) / ps;
+    const int id = p.block_table[(int64_t)b * p.bt_stride + first + min(lane < npg ? lane : 0, jmax)];
+    return min(max(id, 0), p.num_pages - 1);
+  };
+  auto load_k = [&](int kb, int pgv) {
+    const int key0 = kb * BS;
+    if constexpr (PAGED) {
       const int off0 = key0 % ps;
       const int last = kv_len - 1 - key0;  // rows past it read row kv_len-1 (masked)
 #pragma unroll
-      for (int t2 = 0; t2 < KT; ++t2) {
-        const int row = min(t2 * 32 + col, last) + off0;
+      for (int t = 0; t < NT; ++t) {
+        const int row = min(t * 16 + hc, last) + off0;
         const int page = __shfl(pgv, row / ps, kWave);
-        const uint16_t* src = kbase + (int64_t)page * p.sk[0] + (int64_t)(row % ps) * ks2 + half * 8;
+        const uint16_t* src = kbase + (int64_t)page * p.sk[0] + (int64_t)(row % ps) * ks2 + g4 * 8;
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) ka[t2][ks] = *(const u32x4_t*)(src + ks * 16);
+        for (int ks = 0; ks < KS; ++ks) ka[t][ks] = *(const u32x4_t*)(src + ks * 32);
       }
-    };
-    auto dma_v_paged = [&](int kb, int pgv) {
-      const int key0 = kb * BS;
-      const int off0 = key0 % ps;
+    } else {
+      const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)BS * ks2 * 2);
+      if (key0 + BS <= kv_len) {
 #pragma unroll
-      for (int u = 0; u < VTILE / 1024; ++u) {
-        // Unit u covers rows u*RPU_ .. +RPU_-1 of the block, inside one page (ps % RPU_ == 0).
-        const int row = u * RPU_ + off0;
-        const int page = __builtin_amdgcn_readlane(pgv, row / ps);
-        const int rows = min(RPU_, kv_len - key0 - u * RPU_);
-        const __amdgpu_buffer_rsrc_t vr = decode_rsrc(
-            vbase + (int64_t)page * p.sv[0] + (int64_t)(row % ps) * vs2, (int64_t)max(rows, 0) * vs2 * 2);
-        dma16(vr, v_lds[wave] + u * 1024, v_dma_base);
-      }
-    };
-    auto load_k = [&](int kb, int pgv) {
-      if constexpr (PAGED) {
-        load_k_paged(kb, pgv);
-        return;
-      }
-      const int key0 = kb * BS;
-      const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)SUB * ks2 * 2);
-      if (key0 + SUB <= kv_len) {
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int t2 = 0; t2 < KT; ++t2)
-#pragma unroll
-          for (int ks = 0; ks < KSTEPS; ++ks)
-            ka[t2][ks] = buf_load16(kr, k_voff + ks * 32, t2 * 32 * ks2 * 2);
+          for (int ks = 0; ks < KS; ++ks) ka[t][ks] = buf_load16(kr, k_voff + ks * 64, t * 16 * ks2 * 2);
       } else {
         // Partial last block: K rows past kv_len are replaced by row kv_len-1; their
         // scores are masked to -inf.
         const int last = kv_len - 1 - key0;
 #pragma unroll
-        for (int t2 = 0; t2 < KT; ++t2) {
-          const int row = min(t2 * 32 + col, last);
+        for (int t = 0; t < NT; ++t) {
+          const int row = min(t * 16 + hc, last);
 #pragma unroll
-          for (int ks = 0; ks < KSTEPS; ++ks)
-            ka[t2][ks] = buf_load16(kr, (row * ks2 + half * 8) * 2 + ks * 32, 0);
+          for (int ks = 0; ks < KS; ++ks) ka[t][ks] = buf_load16(kr, (row * ks2 + g4 * 8) * 2 + ks * 64, 0);
         }
       }
-    };
-    auto dma_v = [&](int kb, int pgv) {
-      if constexpr (PAGED) {
-        dma_v_paged(kb, pgv);
-        return;
+    }
+  };
+  auto dma_v = [&](int kb, int pgv) {
+    const int key0 = kb * BS;
+    if constexpr (PAGED) {
+      const int off0 = key0 % ps;
+#pragma unroll
+      for (int u = 0; u < VTILE / 1024; ++u) {
+        // Unit u covers rows u*RPU .. +RPU-1 of the block, inside one page (ps % RPU == 0).
+        const int row = u * RPU + off0;
+        const int page = __builtin_amdgcn_readlane(pgv, row / ps);
+        const int rows = min(RPU, kv_len - key0 - u * RPU);
+        const __amdgpu_buffer_rsrc_t vr = decode_rsrc(
+            vbase + (int64_t)page * p.sv[0] + (int64_t)(row % ps) * vs2, (int64_t)max(rows, 0) * vs2 * 2);
+        dma16(vr, v_lds[wave] + u * 1024, v_src_off(u) - u * RPU * vs2 * 2);
       }
-      const int key0 = kb * BS;
+    } else {
       // The resource ends at row kv_len-1, so rows past kv_len arrive as zeros.
       const __amdgpu_buffer_rsrc_t vr =
-          decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(SUB, kv_len - key0) * vs2 * 2);
+          decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(BS, kv_len - key0) * vs2 * 2);
 #pragma unroll
-      for (int u = 0; u < VTILE / 1024; ++u) dma16(vr, v_lds[wave] + u * 1024, v_dma_base + u * v_unit_stride);
-    };
-    int e = wave;
-    int pg_n = 0;  // pages of the next block (paged cache)
-    if (e < nsel) {
-      const int t0 = __builtin_amdgcn_readfirstlane((int)sel[e]);
-      const int pg0 = PAGED ? load_pg(t0) : 0;
-      if constexpr (PAGED) {
-        const int e1 = e + kDecodeWaves;
-        pg_n = load_pg(e1 < nsel ? __builtin_amdgcn_readfirstlane((int)sel[e1]) : t0);
-      }
-      load_k(t0, pg0);
-      dma_v(t0, pg0);
+      for (int u = 0; u < VTILE / 1024; ++u) dma16(vr, v_lds[wave] + u * 1024, v_src_off(u));
     }
-    while (e < nsel) {
-      const int kb = __builtin_amdgcn_readfirstlane(sel[e]);
-      const int key0 = kb * BS;
-      const uint32_t hsel = __builtin_amdgcn_readfirstlane((int)hb[e]);
-      const bool head_on = col < G && ((hsel >> col) & 1u);
-      // S^T = K Q^T: rows = keys, cols = heads.
-      f32x16_t sacc[KT];
-#pragma unroll
-      for (int t2 = 0; t2 < KT; ++t2) {
-        sacc[t2] = (f32x16_t){};
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-          sacc[t2] = mfma16<DT>(ka[t2][ks], qf[ks], sacc[t2]);
-      }
-      // The next block of this wave: its K loads go out now (the K registers are free).
-      const int en = e + kDecodeWaves;
-      const bool more = en < nsel;
-      const int tn = more ? __builtin_amdgcn_readfirstlane((int)sel[en]) : 0;
-      int pg_nn = 0;
-      if constexpr (PAGED) {
-        // Pages of the block after the next, issued before the next block's K loads so
-        // the fixed V wait below also covers them.
-        const int enn = en + kDecodeWaves;
-        pg_nn = load_pg(enn < nsel ? __builtin_amdgcn_readfirstlane((int)sel[enn]) : kb);
-      }
-      if (more) load_k(tn, pg_n);
-      // Register r of tile t2 holds key t2*32 + 8*(r/4) + 4*half + r%4 of head `col`.
-      float mx = -INFINITY;
-#pragma unroll
-      for (int t2 = 0; t2 < KT; ++t2) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = key0 + t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const float x = (head_on && key < kv_len) ? sacc[t2][r] * p.scale_log2 : -INFINITY;
-          sacc[t2][r] = x;
-          mx = fmaxf(mx, x);
-        }
-      }
-      mx = pair_max32(mx);
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      float ls = 0.f;
-      float* pw = p_lds[wave];
-#pragma unroll
-      for (int t2 = 0; t2 < KT; ++t2) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e2 = __builtin_amdgcn_exp2f(sacc[t2][r] - m_use);
-          ls += e2;
-          const int key = t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          pw[pcol ? key * MG + col : SUB * MG + lane] = e2;
-        }
-      }
-      l_run = l_run * alpha + ls;
-      m_run = m_new;
-      if (half == 0 && col < MG) a_lds[wave][col] = alpha;
-      // p_lds / a_lds / v_lds are private to this wave: wait for this block's V DMA (the
-      // next block's K loads, issued after it, may still be in flight), then a wave
-      // barrier orders the LDS writes and reads.
-      if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NKL));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // PV: oacc[g] = alpha_g * oacc[g] + sum_key p[key][g] * V[key][dc*8..+7].
-#pragma unroll
-      for (int gg = 0; gg < MG; ++gg) {
-        const float a = a_lds[wave][gg];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) oacc[gg][j] *= a;
-      }
-#pragma unroll 2
-      for (int i = 0; i < VPL; ++i) {
-        const int kk = kg + KG * i;
-        float vf[8];
-        unpack16x8<DT>(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
-#pragma unroll
-        for (int gg = 0; gg < MG; ++gg) {
-          const float pv = pw[kk * MG + gg];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pv, vf[j], oacc[gg][j]);
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (more) {
-        // The DMA writes the V tile through the memory path: every LDS read of it must
-        // have returned first.
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-        dma_v(tn, pg_n);
-      }
-      pg_n = pg_nn;
-      e = en;
+  };
+  int e = wave;
+  int pg_n = 0;  // pages of the next block (paged cache)
+  if (e < nsel) {
+    const int t0 = __builtin_amdgcn_readfirstlane((int)sel[e]);
+    const int pg0 = PAGED ? load_pg(t0) : 0;
+    if constexpr (PAGED) {
+      const int e1 = e + kDecodeWaves;
+      pg_n = load_pg(e1 < nsel ? __builtin_amdgcn_readfirstlane((int)sel[e1]) : t0);
     }
-  } else {
-  int rank = 0;  // union rank of the next entry in this range (uniform)
-  for (int c0 = 0; c0 < range; c0 += kWave) {
-    const int t = c0 + lane;
-    const uint32_t mybits = t < range ? hb[t] : 0u;
-    uint64_t bits = __ballot(mybits != 0);
-    while (bits) {
-      const int pos = __builtin_ctzll(bits);
-      bits &= bits - 1;
-      const int e = rank++;
-      if ((e & (kDecodeWaves - 1)) != wave) continue;
-      const int kb = lo + c0 + pos;
-      const uint32_t hsel = __builtin_amdgcn_readlane(mybits, pos);
-      const bool head_on = col < G && ((hsel >> col) & 1u);
-#pragma unroll 1
-      for (int sb = 0; sb < NSUB; ++sb) {
-        const int key0 = kb * BS + sb * SUB;
-        if (key0 >= kv_len) break;
-        // Issue every K (A-operand layout) and V (PV layout) load of the sub-block.
-        const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)SUB * ks2 * 2);
-        // V: DMA into this wave's LDS tile. The resource ends at row kv_len-1, so rows
-        // past kv_len (possibly never written) arrive as zeros.
-        const __amdgpu_buffer_rsrc_t vr =
-            decode_rsrc(vbase + (int64_t)key0 * vs2, (int64_t)min(SUB, kv_len - key0) * vs2 * 2);
+    load_k(t0, pg0);
+    dma_v(t0, pg0);
+  }
+  while (e < nsel) {
+    const int kb = __builtin_amdgcn_readfirstlane(sel[e]);
+    const int key0 = kb * BS;
+    const uint32_t hsel = __builtin_amdgcn_readfirstlane((int)hb[e]);
+    const bool head_on = hc < G && ((hsel >> hc) & 1u);
+    // S^T = K Q^T: rows = keys, columns = heads.
+    f32x4_t sacc[NT];
 #pragma unroll
-        for (int u = 0; u < VTILE / 1024; ++u)
-          dma16(vr, v_lds[wave] + u * 1024, v_dma_base + u * v_unit_stride);
-        u32x4_t ka[KT][KSTEPS];
-        if (key0 + SUB <= kv_len) {
+    for (int t = 0; t < NT; ++t) {
+      sacc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t2 = 0; t2 < KT; ++t2)
+      for (int ks = 0; ks < KS; ++ks) sacc[t] = mfma32k<DT>(ka[t][ks], qf[ks], sacc[t]);
+    }
+    // The next block of this wave: its K loads go out now (the K registers are free).
+    const int en = e + kDecodeWaves;
+    const bool more = en < nsel;
+    const int tn = more ? __builtin_amdgcn_readfirstlane((int)sel[en]) : 0;
+    int pg_nn = 0;
+    if constexpr (PAGED) {
+      // Pages of the block after the next, issued before the next block's K loads so the
+      // fixed V wait below also covers them.
+      const int enn = en + kDecodeWaves;
+      pg_nn = load_pg(enn < nsel ? __builtin_amdgcn_readfirstlane((int)sel[enn]) : kb);
+    }
+    if (more) load_k(tn, pg_n);
+    // Element j of tile t holds key 16 t + 4 g4 + j of head hc.
+    float mx = -INFINITY;
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks)
-              ka[t2][ks] = buf_load16(kr, k_voff + ks * 32, t2 * 32 * ks2 * 2);
-        } else {
-          // Partial last sub-block: K rows past kv_len are replaced by row kv_len-1; their
-          // scores are masked to -inf.
-          const int last = kv_len - 1 - key0;
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-          for (int t2 = 0; t2 < KT; ++t2) {
-            const int row = min(t2 * 32 + col, last);
+      for (int j = 0; j < 4; ++j) {
+        const int key = key0 + t * 16 + 4 * g4 + j;
+        const float x = (head_on && key < kv_len) ? sacc[t][j] * p.scale_log2 : -INFINITY;
+        sacc[t][j] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = quad16_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float ls = 0.f;
 #pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks)
-              ka[t2][ks] = buf_load16(kr, (row * ks2 + half * 8) * 2 + ks * 32, 0);
-          }
-        }
-        // S^T = K Q^T: rows = keys, cols = heads.
-        f32x16_t sacc[KT];
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int t2 = 0; t2 < KT; ++t2) {
-          sacc[t2] = (f32x16_t){};
+      for (int j = 0; j < 4; ++j) {
+        const float e2 = __builtin_amdgcn_exp2f(sacc[t][j] - m_use);
+        sacc[t][j] = e2;
+        ls += e2;
+      }
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+    // P^T as the B operand of k-step c: k slot 8 g4 + j holds key 32 c + 4 g4 + j (j < 4,
+    // tile 2c) or 32 c + 16 + 4 g4 + j - 4 (tile 2c + 1), the order of the V^T reads below.
+    u32x4_t pb[NC];
 #pragma unroll
-          for (int ks = 0; ks < KSTEPS; ++ks)
-            sacc[t2] = mfma16<DT>(ka[t2][ks], qf[ks], sacc[t2]);
-        }
-        // Register r of tile t2 holds key t2*32 + 8*(r/4) + 4*half + r%4 of head `col`.
-        float mx = -INFINITY;
+    for (int c = 0; c < NC; ++c)
+      pb[c] = (u32x4_t){pack16x2<DT>(sacc[2 * c][0], sacc[2 * c][1]), pack16x2<DT>(sacc[2 * c][2], sacc[2 * c][3]),
+                        pack16x2<DT>(sacc[2 * c + 1][0], sacc[2 * c + 1][1]),
+                        pack16x2<DT>(sacc[2 * c + 1][2], sacc[2 * c + 1][3])};
 #pragma unroll
-        for (int t2 = 0; t2 < KT; ++t2) {
+    for (int dt = 0; dt < DT16; ++dt) oacc[dt] *= alpha;
+    // The V tile is private to this wave: wait for this block's V DMA (the next block's K
+    // loads, issued after it, may still be in flight).
+    if (more) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NKL));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // O^T += V^T P^T.
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            const float x = (head_on && key < kv_len) ? sacc[t2][r] * p.scale_log2 : -INFINITY;
-            sacc[t2][r] = x;
-            mx = fmaxf(mx, x);
-          }
-        }
-        mx = pair_max32(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float ls = 0.f;
-        float* pw = p_lds[wave];
+    for (int c = 0; c < NC; ++c) {
+      const int r0 = 32 * c + 4 * g4;
 #pragma unroll
-        for (int t2 = 0; t2 < KT; ++t2) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float e2 = __builtin_amdgcn_exp2f(sacc[t2][r] - m_use);
-            ls += e2;
-            const int key = t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            pw[pcol ? key * MG + col : SUB * MG + lane] = e2;
-          }
-        }
-        l_run = l_run * alpha + ls;
-        m_run = m_new;
-        if (half == 0 && col < MG) a_lds[wave][col] = alpha;
-        // p_lds / a_lds / v_lds are private to this wave: wait for the V DMA, then a wave
-        // barrier orders the LDS writes and reads.
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // PV: oacc[g] = alpha_g * oacc[g] + sum_key p[key][g] * V[key][dc*8..+7].
-#pragma unroll
-        for (int gg = 0; gg < MG; ++gg) {
-          const float a = a_lds[wave][gg];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) oacc[gg][j] *= a;
-        }
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-          const int kk = kg + KG * i;
-          float vf[8];
-          unpack16x8<DT>(*(const u32x4_t*)(v_lds[wave] + kk * (D * 2) + dc * 16), vf);
-#pragma unroll
-          for (int gg = 0; gg < MG; ++gg) {
-            const float pv = pw[kk * MG + gg];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) oacc[gg][j] = fmaf(pv, vf[j], oacc[gg][j]);
-          }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int dt = 0; dt < DT16; ++dt) {
+        const u32x2_t lo = v_tr(r0, dt), hi = v_tr(r0 + 16, dt);
+        const u32x4_t a = {lo[0], lo[1], hi[0], hi[1]};
+        oacc[dt] = mfma32k<DT>(a, pb[c], oacc[dt]);
       }
     }
+    if (more) {
+      // The DMA writes the V tile through the memory path: every LDS read of it must have
+      // returned first.
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      dma_v(tn, pg_n);
+    }
+    pg_n = pg_nn;
+    e = en;
   }
 
-  }
-  // Per wave: reduce the PV partials over key groups and the denominators over the lane
-  // pair, then merge the 4 waves. Each wave's partial output goes to its own V tile.
-  static_assert(MG * D * 4 <= VTILE, "merge buffer size");
+  // Merge the four waves: each wave's (m, l) per head and its output columns (into its
+  // own V tile).
   __builtin_amdgcn_s_waitcnt(0x0f70);  // no V DMA may still target the tile
-  const float l_tot = pair_sum32(l_run);
-  if (half == 0 && col < MG) {
-    comb_ml[wave][col][0] = m_run;
-    comb_ml[wave][col][1] = l_tot;
+  const float l_tot = quad16_sum(l_run);
+  if (g4 == 0 && hc < G) {
+    comb_ml[wave][hc][0] = m_run;
+    comb_ml[wave][hc][1] = l_tot;
   }
+  if (hc < G) {
+    float* mo = (float*)v_lds[wave];
 #pragma unroll
-  for (int gg = 0; gg < MG; ++gg) {
-#pragma unroll
-    for (int off = DOCT; off < kWave; off <<= 1)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) oacc[gg][j] += __shfl_xor(oacc[gg][j], off, 64);
-    if (lane < DOCT) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ((float*)v_lds[wave])[gg * D + lane * 8 + j] = oacc[gg][j];
-    }
+    for (int dt = 0; dt < DT16; ++dt)
+      *(f32x4_t*)(mo + hc * D + dt * 16 + 4 * g4) = oacc[dt];
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += kDecodeWaves * kWave) {
+  for (int i = tid; i < G * D; i += NTH) {
     const int gg = i / D, d = i % D;
     float M = -INFINITY;
 #pragma unroll
@@ -605,24 +475,16 @@ bsfa_decode_combine_kernel(const DecodeParams p) {
   p.o[b * p.so[0] + h * p.so[1] + d] = f32_to16<DT>(r);
 }
 
-template <int BS, int D, int MG, bool PAGED, int DT>
-static hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
+template <int BS, int D, bool PAGED, int DT>
+static hipError_t launch_decode_dt(const DecodeParams& p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.B * p.Hkv * p.P;
-  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, MG, PAGED, DT>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((bsfa_decode_split_kernel<BS, D, PAGED, DT>), dim3((unsigned)grid),
                      dim3(kDecodeWaves * kWave), 0, stream, p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.P == 1) return err;
   hipLaunchKernelGGL((bsfa_decode_combine_kernel<D, DT>), dim3((unsigned)((int64_t)p.B * p.Hq)), dim3(D),
                      0, stream, p);
   return hipGetLastError();
-}
-
-template <int BS, int D, bool PAGED, int DT>
-static hipError_t launch_decode_dt(const DecodeParams& p, hipStream_t stream) {
-  if (p.G <= 1) return launch_decode_g<BS, D, 1, PAGED, DT>(p, stream);
-  if (p.G <= 2) return launch_decode_g<BS, D, 2, PAGED, DT>(p, stream);
-  if (p.G <= 4) return launch_decode_g<BS, D, 4, PAGED, DT>(p, stream);
-  return launch_decode_g<BS, D, 8, PAGED, DT>(p, stream);
 }
 
 template <int BS, int D, bool PAGED = false>
@@ -668,11 +530,14 @@ static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, v
   if (block_size != 32 && block_size != 64 && block_size != 128)
     return set_error(kErrUnsupported, "decode: block_size must be 32, 64 or 128, got %lld",
                      (long long)block_size);
-  const int64_t nb = (kv_len_max + block_size - 1) / block_size;
+  // A block-128 mask runs on the block-64 kernel: each selected 128-key block is read as
+  // its two 64-key halves (mask entry t >> 1 for half t), so the split counts 64-key blocks.
+  const int64_t run_bs = block_size == 128 ? 64 : block_size;
+  const int64_t nb = (kv_len_max + run_bs - 1) / run_bs;
   if ((nb + num_splits - 1) / num_splits > kDecodeMaxRange)
     return set_error(kErrInvalidArgument,
-                     "decode: num_splits must be >= ceil(num_blocks / %d) (got %lld for %lld blocks)",
-                     kDecodeMaxRange, (long long)num_splits, (long long)nb);
+                     "decode: num_splits must be >= ceil(num_blocks / %d) (got %lld for %lld blocks of %lld keys)",
+                     kDecodeMaxRange, (long long)num_splits, (long long)nb, (long long)run_bs);
   const size_t need = tasft_bsfa_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
   if (workspace_bytes < need)
     return set_error(kErrWorkspace, "decode: workspace too small: need %zu bytes, got %zu", need,
@@ -728,16 +593,14 @@ static int decode_fwd(const void* q, const void* k_cache, const void* v_cache, v
   p.bt_stride = 0;
   p.page_size = 0;
   p.num_pages = 0;
-  p.mshift = 0;
+  p.mshift = block_size == 128 ? 1 : 0;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  if (block_size == 64 && head_dim == 128) err = launch_decode<64, 128>(p, dtype, s);
-  else if (block_size == 64 && head_dim == 64) err = launch_decode<64, 64>(p, dtype, s);
-  else if (block_size == 32 && head_dim == 128) err = launch_decode<32, 128>(p, dtype, s);
-  else if (block_size == 32 && head_dim == 64) err = launch_decode<32, 64>(p, dtype, s);
-  else if (block_size == 128 && head_dim == 128) err = launch_decode<128, 128>(p, dtype, s);
-  else err = launch_decode<128, 64>(p, dtype, s);
+  if (run_bs == 64 && head_dim == 128) err = launch_decode<64, 128>(p, dtype, s);
+  else if (run_bs == 64 && head_dim == 64) err = launch_decode<64, 64>(p, dtype, s);
+  else if (run_bs == 32 && head_dim == 128) err = launch_decode<32, 128>(p, dtype, s);
+  else err = launch_decode<32, 64>(p, dtype, s);
   if (err != hipSuccess)
     return set_error(kErrLaunch, "decode: launch failed: %s", hipGetErrorString(err));
   return kOk;

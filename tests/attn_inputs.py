@@ -117,6 +117,7 @@ DECODE_CASES = [
     (2, 7, 1, 777, 128, 64, 0.4, 2),
     (1, 8, 8, 600, 64, 32, 0.5, None),
     (2, 8, 2, 1024, 128, 128, 0.5, None),
+    (2, 32, 2, 1200, 128, 64, 0.4, 2),      # 16 query heads per KV head
 ]
 
 # Paged decode: (B, Hq, Hkv, S, D, bs, page_size, splits).
@@ -125,6 +126,7 @@ PAGED_CASES = [
     (2, 8, 2, 900, 128, 64, 64, 1),
     (2, 8, 1, 700, 64, 32, 16, 3),
     (2, 8, 2, 1000, 128, 128, 16, None),
+    (2, 32, 2, 900, 128, 64, 16, None),     # 16 query heads per KV head
 ]
 
 

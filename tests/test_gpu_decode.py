@@ -33,6 +33,9 @@ CASES = [
     (4, 32, 8, 4096, 128, 64, 0.1, None),   # config-3 grouping at a smaller cache
     (1, 8, 2, 40000, 128, 64, 0.05, 1),     # 625 blocks in one split (no combine pass)
     (2, 8, 2, 20000, 128, 64, 0.2, 2),      # splits share the selected blocks of a row
+    (2, 32, 2, 1500, 128, 64, 0.3, None),   # 16 query heads per KV head (every MFMA column)
+    (2, 24, 2, 900, 64, 32, 0.4, 3),        # 12 heads, D=64, bs=32, combine pass
+    (1, 16, 1, 1300, 128, 128, 0.4, 1),     # 16 heads at block 128
 ]
 
 
@@ -148,8 +151,8 @@ def test_config3_full_size_default_splits():
 
 
 def test_qwen_geometry_full_size_default_splits():
-    """Seven query heads per KV head (Qwen-2.5-7B: 28/4 heads), the kernel built for up to
-    eight heads with one wave per SIMD, at the config-3 batch and cache (B=64, S_kv=32768,
+    """Seven query heads per KV head (Qwen-2.5-7B: 28/4 heads; seven of the kernel's 16 MFMA
+    head columns carry a query), at the config-3 batch and cache (B=64, S_kv=32768,
     51 of 512 blocks per KV head): the default is one split per (b, KV head), 256
     workgroups, direct writes. Unit-scale Q/K/V drawn on the device; sampled (b, h) pairs,
     including the last head of a group, against the oracle."""
