@@ -38,9 +38,9 @@ struct GateTargetParams {
   // the host has filled with -inf; 0 for a block-64 output (NBO = NB).
   int pool;
   int NBO;
-  // Block-64 kernel with two waves per head only: 1 when the output holds 32-token blocks
-  // ([NBO, NBO], filled with -inf by the host). Each wave's two 32 x 32 score tiles are then
-  // whole blocks, written as they are computed.
+  // Block-64 kernels: 1 when the output holds 32-token blocks ([NBO, NBO], filled with -inf
+  // by the host). Each 32 x 32 quarter of a 64 x 64 score tile is then a whole block,
+  // written as it is computed.
   int fine;
 };
 
@@ -98,9 +98,10 @@ gate_target_normalize_kernel(float* data, int64_t group_len, float inv_temp, flo
 }
 
 
-// Block size 64. A workgroup owns one query block of HPW query heads of the same KV head
-// (the target is dense, so these heads read exactly the same K blocks) with WPH waves per
-// head: with WPH = 2 (the launched form) wave (hw, w) takes head hw, query rows 32*w..+31
+// Block size 64, scores with an additive mask (unmasked scores run the one-wave-per-head
+// kernel below, 7% faster at config 5). A workgroup owns one query block of HPW query heads
+// of the same KV head (the target is dense, so these heads read exactly the same K blocks)
+// with WPH waves per head: with WPH = 2 (the launched form) wave (hw, w) takes head hw, query rows 32*w..+31
 // and all 64 keys of every causal key block (16 MFMAs per block); with WPH = 4 it takes
 // rows 32*(w&1).. and the key half 32*(w>>1).. (8 MFMAs, measured 9% slower at config 5).
 // K tiles are copied HBM -> LDS once for all HPW heads by buffer_load_dwordx4 ... lds
@@ -325,10 +326,199 @@ gate_target_bs64_kernel(const GateTargetParams p) {
   store(kb_end - 1);
 }
 
+// Unmasked scores: one wave per (head, query block), its 64 query rows as two 32-row MFMA
+// column tiles. Every K fragment read from LDS feeds both row tiles, halving the LDS reads
+// per MFMA of the two-waves-per-head kernel above, and the block maximum is one wave's:
+// no exchange between waves. HPW heads of one KV group share each K tile (three stages,
+// two blocks in flight, as above).
+template <int D, int HPW, int DT>
+__global__ void __launch_bounds__(HPW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+gate_target_bs64_w1_kernel(const GateTargetParams p) {
+  constexpr int BS = 64;
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROWB = D * 2;
+  constexpr int TILE = BS * ROWB;
+  constexpr int UNITS = TILE / 1024;
+  static_assert(UNITS % HPW == 0, "equal DMA units per wave");
+  constexpr int UPW = UNITS / HPW;
+  __shared__ __attribute__((aligned(1024))) uint8_t k0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t k1[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t k2[TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;  // head within the workgroup
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  const int chunks = p.G / HPW;
+  const int64_t idx = blockIdx.x;
+  const int64_t groups = (int64_t)p.B * p.Hkv;
+  const int64_t per_group = (int64_t)chunks * p.NB;
+  int64_t grp, r;
+  if ((groups & 7) == 0) {
+    const int64_t j = idx >> 3;
+    grp = (idx & 7) + 8 * (j / per_group);
+    r = j % per_group;
+  } else {
+    grp = idx / per_group;
+    r = idx % per_group;
+  }
+  const int qslot = (int)(r / chunks);
+  const int qb = p.causal ? (p.NB - 1 - qslot) : qslot;
+  const int b = (int)(grp / p.Hkv);
+  const int kvh = (int)(grp % p.Hkv);
+  const int h = kvh * p.G + (int)(r % chunks) * HPW + wave;
+
+  const uint16_t* qbase = p.q + b * p.sq[0] + h * p.sq[1];
+  const uint16_t* kbase = p.k + b * p.sk[0] + kvh * p.sk[1];
+  float* orow = p.out + (((int64_t)b * p.Hq + h) * p.NBO + (qb >> p.pool)) * p.NBO;
+
+  int qrow[2];
+  bool qvalid[2];
+  u32x4_t qf[2][KSTEPS];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    qrow[rt] = qb * BS + rt * 32 + col;
+    qvalid[rt] = qrow[rt] < p.S;
+  }
+  auto load_q = [&]() {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        u32x4_t val = {0u, 0u, 0u, 0u};
+        if (qvalid[rt]) val = *(const u32x4_t*)(qbase + (int64_t)qrow[rt] * p.sq[2] + ks * 16 + half * 8);
+        qf[rt][ks] = val;
+      }
+  };
+  // DMA units of this wave: u = wave, wave + HPW, ...
+  int koff[UPW];
+#pragma unroll
+  for (int i = 0; i < UPW; ++i) {
+    const int u = wave + i * HPW;
+    const int byte = u * 1024 + lane * 16;
+    const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+    koff[i] = (row * (int)p.sk[2] + gt_swz<D>(row, pos) * 8) * 2;
+  }
+  auto issue = [&](uint8_t* kt, int kb) {
+    const int key0 = kb * BS;
+    const int64_t bytes = (int64_t)(p.S - key0) * p.sk[2] * 2;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kbase + (int64_t)key0 * p.sk[2]), (short)0,
+        bytes > 0x7fffffff ? 0x7fffffff : (int)bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) gt_dma16(rs, kt + (wave + i * HPW) * 1024, koff[i]);
+  };
+  // Block kb from stage kt: its maximum (or, for 32-token output blocks, the maxima of its
+  // four 32 x 32 quarters), written by lane 0.
+  auto block_max = [&](const uint8_t* kt, int kb) {
+    f32x16_t s[2][2];  // [row tile][key tile]
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) s[rt][t] = (f32x16_t){};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cc = ks * 2 + half;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int kr = 32 * t + col;
+        const u32x4_t a = *(const u32x4_t*)(kt + kr * ROWB + gt_swz<D>(kr, cc) * 16);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) s[rt][t] = mfma16<DT>(a, qf[rt][ks], s[rt][t]);
+      }
+    }
+    const int key0 = kb * BS;
+    if ((p.causal && kb == qb) || (key0 + BS > p.S) || qb * BS + BS > p.S) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            const int key = key0 + 32 * t + 8 * (rr >> 2) + 4 * half + (rr & 3);
+            s[rt][t][rr] = (!qvalid[rt] || key >= p.S || (p.causal && key > qrow[rt])) ? -INFINITY : s[rt][t][rr];
+          }
+    }
+    float m[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float v = fmaxf(fmaxf(s[rt][t][0], s[rt][t][1]), s[rt][t][2]);
+#pragma unroll
+        for (int rr = 3; rr < 15; rr += 2) v = fmaxf(fmaxf(v, s[rt][t][rr]), s[rt][t][rr + 1]);
+        m[rt][t] = fmaxf(v, s[rt][t][15]);
+      }
+    if (p.fine) {
+      // Block-32 output: quarter (rt, t) is block (2 qb + rt, 2 kb + t); entries past NBO
+      // belong to no block.
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) m[rt][t] = wave_max_dpp(m[rt][t]);
+      if (lane == 0) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const int rq = 2 * qb + rt;
+          if (rq >= p.NBO) continue;
+          float* o = p.out + (((int64_t)b * p.Hq + h) * p.NBO + rq) * p.NBO + 2 * kb;
+          o[0] = m[rt][0] * p.scale;
+          if (2 * kb + 1 < p.NBO) o[1] = m[rt][1] * p.scale;
+        }
+      }
+      return;
+    }
+    // Scaling by scale > 0 after the max is exact: rounding is monotonic.
+    const float mx = wave_max_dpp(fmaxf(fmaxf(m[0][0], m[0][1]), fmaxf(m[1][0], m[1][1]))) * p.scale;
+    if (lane == 0) {
+      if (p.pool)
+        gt_atomic_fmax(orow + (kb >> 1), mx);
+      else
+        orow[kb] = mx;
+    }
+  };
+
+  const int kb_end = p.causal ? qb + 1 : p.NB;
+  if (!p.pool && !p.fine)
+    for (int kb = kb_end + lane; kb < p.NB; kb += kWave) orow[kb] = -INFINITY;
+  // Three stages, two blocks in flight; past the last block the last one is loaded again,
+  // so every wave has exactly UPW later DMA units outstanding when it waits for a block.
+  constexpr int kWaitBlock = (UPW & 15) | ((UPW >> 4) << 14) | 0x0070;  // vmcnt(UPW)
+  auto step = [&](int kb, const uint8_t* cur, uint8_t* nxt) {
+    __builtin_amdgcn_s_waitcnt(kWaitBlock);  // this wave's DMA of block kb landed
+    asm volatile("s_barrier" ::: "memory");  // every wave's; stage nxt is free
+    issue(nxt, min(kb + 2, kb_end - 1));
+    block_max(cur, kb);
+  };
+  issue(k0, 0);
+  load_q();
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  issue(k1, min(1, kb_end - 1));
+  for (int kb = 0; kb < kb_end; kb += 3) {
+    step(kb, k0, k2);
+    if (kb + 1 >= kb_end) break;
+    step(kb + 1, k1, k0);
+    if (kb + 2 >= kb_end) break;
+    step(kb + 2, k2, k1);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): no DMA outlives the workgroup
+}
+
 template <int D, bool MASKED, int DT>
 static hipError_t launch_blockmax_bs64(const GateTargetParams& p, hipStream_t stream) {
   const int hpw = (p.G % 4 == 0) ? 4 : (p.G % 2 == 0 ? 2 : 1);
   const int64_t grid = (int64_t)p.NB * p.B * p.Hq / hpw;
+  if constexpr (!MASKED) {
+    if (hpw == 4)
+      hipLaunchKernelGGL((gate_target_bs64_w1_kernel<D, 4, DT>), dim3((unsigned)grid), dim3(4 * 64), 0, stream, p);
+    else if (hpw == 2)
+      hipLaunchKernelGGL((gate_target_bs64_w1_kernel<D, 2, DT>), dim3((unsigned)grid), dim3(2 * 64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gate_target_bs64_w1_kernel<D, 1, DT>), dim3((unsigned)grid), dim3(64), 0, stream, p);
+    return hipGetLastError();
+  }
   if (hpw == 4)
     hipLaunchKernelGGL((gate_target_bs64_kernel<D, 4, MASKED, DT>), dim3((unsigned)grid), dim3(4 * 128), 0, stream, p);
   else if (hpw == 2)
