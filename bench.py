@@ -39,7 +39,7 @@ FLOP_PER_BLOCK = 4 * 64 * 64 * 128  # QK^T + PV of one 64x64 tile at D=128
 # 673.2 MB algorithmic bytes (Q + K + V + O + mask) this is 1.66x: between launches the gate
 # streams 335 MB of Q and K, and K/V blocks are fetched again by the rows of a KV group
 # (4 MB of K/V per group against a 4 MB L2 per XCD).
-PREFILL_TRAFFIC_BYTES = 413213 * 1024 * 2.0 + 265793 * 1024
+PREFILL_TRAFFIC_BYTES = 412721 * 1024 * 2.0 + 266181 * 1024
 # Untimed decode launches before the decode timing (steady state, see main()).
 DECODE_SETTLE = 150
 # Untimed config-2 steps between the timed steps and the per-kernel (event) split.
