@@ -44,6 +44,10 @@ PREFILL_TRAFFIC_BYTES = 412721 * 1024 * 2.0 + 266181 * 1024
 DECODE_SETTLE = 150
 # Untimed config-2 steps between the timed steps and the per-kernel (event) split.
 SPLIT_SETTLE = 100
+# Untimed launches of each MFMA extra (varlen, config 4, config 5) before its timing: after
+# the idle setup of a workload the clocks ramp, and the varlen prefill measured 363 us on
+# its first launches against 323 us settled.
+EXTRA_SETTLE = 60
 
 
 def log(msg: str) -> None:
@@ -258,7 +262,10 @@ def bench_decode_qwen(torch, dev, steps, warmup):
 def bench_varlen(torch, dev, steps, warmup):
     """Packed variable-length prefill: four sequences of 8192, 6144, 4096 and 2048 tokens
     (Llama-3-8B heads) in one [T, H, D] batch, each with a causal block mask keeping the
-    diagonal and 20% of the other causal blocks, through ``forward_varlen``."""
+    diagonal and 20% of the other causal blocks, through ``forward_varlen``. ``cu_seqlens``
+    stays on the device with ``max_seqlen`` given, as a serving loop holds them: a CPU
+    ``cu_seqlens`` is copied to the device on every call, and that synchronous copy idles
+    the GPU for tens of microseconds per call."""
     from tasft_amd import workloads as wl
     from tasft_amd.kernels import BlockSparseFlashAttention
 
@@ -268,7 +275,7 @@ def bench_varlen(torch, dev, steps, warmup):
     q = wl.randn_bf16((total, hq, d), 1011).to(dev)
     k = wl.randn_bf16((total, hkv, d), 1012).to(dev)
     v = wl.randn_bf16((total, hkv, d), 1013).to(dev)
-    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32).to(dev)
     nb = max(lens) // bs
     g = torch.Generator().manual_seed(2011)
     keep = torch.rand((len(lens), hq, nb, nb), generator=g) < 0.2
@@ -280,12 +287,12 @@ def bench_varlen(torch, dev, steps, warmup):
         executed += int((mask[n, :, :nb_n, :nb_n] & tri).sum().item())
     bsfa = BlockSparseFlashAttention(block_size=bs, min_sparsity_for_speedup=0.0)
     for _ in range(warmup):
-        bsfa.forward_varlen(q, k, v, mask, cu, causal=True)
+        bsfa.forward_varlen(q, k, v, mask, cu, max_seqlen=max(lens), causal=True)
     torch.cuda.synchronize()
     t = LaunchTimer(torch)
     for _ in range(steps):
         with _Span(t):
-            bsfa.forward_varlen(q, k, v, mask, cu, causal=True)
+            bsfa.forward_varlen(q, k, v, mask, cu, max_seqlen=max(lens), causal=True)
     torch.cuda.synchronize()
     ms = t.total_ms() / steps
     return {"ms": ms, "tflops": executed * FLOP_PER_BLOCK / (ms * 1e-3) / 1e12, "tokens": total}
@@ -550,7 +557,7 @@ def main() -> int:
                       "decode_qwen_hbm_frac": round(dq["gbps"] / PEAK_HBM_GBPS, 4)})
     if "varlen" in extras:
         log("bench: packed varlen prefill")
-        vl = bench_varlen(torch, dev, max(10, args.steps // 2), max(10, args.warmup // 10))
+        vl = bench_varlen(torch, dev, max(10, args.steps // 2), max(EXTRA_SETTLE, args.warmup // 10))
         extra.update({"varlen_prefill_ms": round(vl["ms"], 4),
                       "varlen_prefill_tflops_executed": round(vl["tflops"], 1)})
     if "decode_step" in extras:
@@ -563,12 +570,12 @@ def main() -> int:
         extra.update({"gate_train_step_ms": round(gt["ms"], 4)})
     if "qwen" in extras:
         log("bench: config 4 Qwen prefill")
-        qw = bench_qwen(torch, dev, max(5, args.steps // 2), max(10, args.warmup // 4))
+        qw = bench_qwen(torch, dev, max(5, args.steps // 2), max(EXTRA_SETTLE, args.warmup // 4))
         extra.update({"qwen_prefill_ms": round(qw["qwen_prefill_ms"], 4),
                       "qwen_prefill_tflops_executed": round(qw["qwen_prefill_tflops"], 1)})
     if "gate_target" in extras:
         log("bench: config 5 gate target")
-        gt = bench_gate_target(torch, dev, max(5, args.steps // 2), max(10, args.warmup // 4))
+        gt = bench_gate_target(torch, dev, max(5, args.steps // 2), max(EXTRA_SETTLE, args.warmup // 4))
         extra.update({"gate_target_ms": round(gt["gate_target_ms"], 4),
                       "gate_target_tflops": round(gt["gate_target_tflops"], 1)})
     cpu = None

@@ -104,6 +104,18 @@ int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const void* v, v
                                   int dtype, void* stream);
 
 /*
+ * Zeroes the rows of out [T, H, D] (strides of token, head, dim in elements, dim
+ * contiguous) for the tokens at or after cu_seqlens[num_seqs], reading that offset from
+ * device memory, so a caller holding cu_seqlens on the device gets the zero rows of
+ * tasft_bsfa_prefill_varlen_fwd's contract without a host round trip. Launch it on the
+ * same stream as the prefill; the two write disjoint rows. No reference counterpart: the
+ * reference's flat-token prefill has no uncovered rows (tasft/inference/vllm_patch.py:172-176).
+ */
+int tasft_bsfa_varlen_zero_tail(void* out, const int32_t* cu_seqlens, int64_t num_seqs,
+                                int64_t tokens, int64_t num_heads, int64_t head_dim,
+                                const int64_t* o_strides, void* stream);
+
+/*
  * Bytes of the optional workspace of tasft_bsfa_prefill_fwd (work-queue counters).
  * No reference counterpart: the reference launches one program per query block in
  * grid order (tasft/kernels/block_sparse_fa.py:517-550).

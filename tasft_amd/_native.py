@@ -24,6 +24,7 @@ EXPORTED_SYMBOLS = (
     "tasft_bsfa_prefill_workspace_bytes",
     "tasft_bsfa_prefill_fwd",
     "tasft_bsfa_prefill_varlen_fwd",
+    "tasft_bsfa_varlen_zero_tail",
     "tasft_bsfa_decode_workspace_bytes",
     "tasft_bsfa_decode_fwd",
     "tasft_bsfa_decode_paged_fwd",
@@ -65,6 +66,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
          _I64P, _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P],
     ),
+    "tasft_bsfa_varlen_zero_tail": (_I, [_P, _P, _I64, _I64, _I64, _I64, _I64P, _P]),
     "tasft_bsfa_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "tasft_bsfa_decode_fwd": (
         _I,

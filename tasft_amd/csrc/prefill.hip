@@ -1110,6 +1110,54 @@ extern "C" int tasft_bsfa_prefill_fwd(const void* q, const void* k, const void* 
                           "prefill");
 }
 
+namespace tasft {
+
+// Zeroes the output rows of the tokens at or after cu_seqlens[num_seqs] of a packed
+// [T, H, D] batch (rows no sequence covers), reading that offset on the device: with no
+// such row (the usual case) every thread makes one check and exits. Each thread writes
+// 16 bytes per step; the grid strides over the tail.
+__global__ void __launch_bounds__(256)
+varlen_zero_tail_kernel(uint16_t* out, const int32_t* end_ptr, int64_t T, int H, int D,
+                        int64_t st_t, int64_t st_h) {
+  const int64_t end = *end_ptr;
+  const int64_t first = end < 0 ? 0 : (end > T ? T : end);
+  const int chunks = D / 8;
+  const int64_t per_row = (int64_t)H * chunks;
+  const int64_t n = (T - first) * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = first + i / per_row;
+    const int64_t rem = i % per_row;
+    const int64_t h = rem / chunks, c = rem % chunks;
+    *(u32x4_t*)(out + row * st_t + h * st_h + c * 8) = (u32x4_t){0u, 0u, 0u, 0u};
+  }
+}
+
+}  // namespace tasft
+
+extern "C" int tasft_bsfa_varlen_zero_tail(void* out, const int32_t* cu_seqlens, int64_t num_seqs,
+                                           int64_t tokens, int64_t num_heads, int64_t head_dim,
+                                           const int64_t* o_strides, void* stream) {
+  if (!out || !cu_seqlens || !o_strides)
+    return set_error(kErrInvalidArgument, "varlen_zero_tail: null pointer argument");
+  if (num_seqs <= 0 || tokens < 0 || num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0)
+    return set_error(kErrInvalidArgument,
+                     "varlen_zero_tail: num_seqs, num_heads positive, tokens >= 0, head_dim a positive multiple of 8");
+  if (!strides_nonneg(o_strides, 3) || o_strides[2] != 1 || o_strides[0] % 8 != 0 ||
+      o_strides[1] % 8 != 0 || !aligned16(out))
+    return set_error(kErrInvalidArgument,
+                     "varlen_zero_tail: out must be 16-byte aligned with a contiguous head_dim and "
+                     "token and head strides multiples of 8 elements");
+  if (tokens == 0) return kOk;
+  hipLaunchKernelGGL(varlen_zero_tail_kernel, dim3(256), dim3(256), 0, (hipStream_t)stream,
+                     (uint16_t*)out, cu_seqlens + num_seqs, tokens, (int)num_heads, (int)head_dim,
+                     o_strides[0], o_strides[1]);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return set_error(kErrLaunch, "varlen_zero_tail: launch failed: %s", hipGetErrorString(err));
+  return kOk;
+}
+
 extern "C" int tasft_bsfa_prefill_varlen_fwd(const void* q, const void* k, const void* v,
                                              void* out, const uint8_t* block_mask,
                                              const int32_t* cu_seqlens, int64_t num_seqs,

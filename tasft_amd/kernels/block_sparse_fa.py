@@ -368,7 +368,7 @@ class BlockSparseFlashAttention:
         v = _kernel_ready(v)
         mask = _mask_bytes(block_mask.to(q.device))
         cu_dev = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
-        out = (torch.empty_like(q) if covered == T else torch.zeros_like(q))
+        out = torch.empty_like(q)
         status = lib.tasft_bsfa_prefill_varlen_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(),
             cu_dev.data_ptr(), n_seq, H, k.shape[1], max_seqlen, D, self.block_size,
@@ -378,6 +378,13 @@ class BlockSparseFlashAttention:
         )
         _native.check(status, "tasft_bsfa_prefill_varlen_fwd",
                       {"tokens": T, "sequences": n_seq, "max_seqlen": max_seqlen})
+        if covered != T:
+            # Rows no sequence covers are zeroed on the device (cu_seqlens[N] is read there,
+            # so a device cu_seqlens needs no host round trip).
+            status = lib.tasft_bsfa_varlen_zero_tail(
+                out.data_ptr(), cu_dev.data_ptr(), n_seq, T, H, D, _native.strides(out),
+                _native.stream_handle(q.device))
+            _native.check(status, "tasft_bsfa_varlen_zero_tail", {"tokens": T, "sequences": n_seq})
         return out
 
     # ------------------------------------------------------------------ decode

@@ -327,6 +327,16 @@ def test_prefill_varlen_matches_oracle(lens, Hq, Hkv, D, bs, causal, density):
     ref = orc.attention_varlen(to_np(q), to_np(k), to_np(v), cu, mask.numpy(), bs, causal)
     assert_close_bf16(out, ref, f"varlen prefill {lens}")
     assert (out[cu[-1]:] == 0).all()
+    # cu_seqlens on the device (no host round trip): the same rows, and the uncovered ones
+    # zeroed on the device. The freed NaN block makes a stale output visible.
+    poison = torch.full_like(out, float("nan"))
+    del poison
+    out_d = bsfa.forward_varlen(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                torch.tensor(cu, dtype=torch.int32, device=dev),
+                                max_seqlen=max(max(lens), 1), causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out_d[:cu[-1]], out[:cu[-1]])
+    assert (out_d[cu[-1]:] == 0).all()
 
 
 def test_prefill_varlen_one_sequence_is_bit_identical_to_forward():

@@ -82,6 +82,13 @@ def test_invalid_arguments_return_errors_without_launch():
     rc = lib.tasft_bsfa_prefill_varlen_fwd(fake, fake, fake, fake, fake, fake, 2, 32, 8, 128, 128,
                                            64, _i64([8, 8, 2]), st3, st3, st3, st, 1.0, 1, 0, None)
     assert rc == -1 and b"contiguous" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_varlen_zero_tail(None, fake, 2, 100, 32, 128, _i64([4096, 128, 1]), None)
+    assert rc == -1 and b"null pointer" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_varlen_zero_tail(fake, fake, 2, 100, 32, 12, _i64([384, 12, 1]), None)
+    assert rc == -1 and b"multiple of 8" in lib.tasft_last_error()
+    rc = lib.tasft_bsfa_varlen_zero_tail(fake, fake, 2, 100, 32, 128, _i64([4096, 128, 2]), None)
+    assert rc == -1 and b"contiguous" in lib.tasft_last_error()
+    assert lib.tasft_bsfa_varlen_zero_tail(fake, fake, 2, 0, 32, 128, _i64([4096, 128, 1]), None) == 0
     rc = lib.tasft_bsfa_decode_paged_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 0, 1, 32,
                                          8, 1024, 128, 256, 16, 100, 4, st, st, st, st, st, 64, 1.0, 0, None)
     assert rc == -2 and b"block_size" in lib.tasft_last_error()
