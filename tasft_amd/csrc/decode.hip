@@ -255,14 +255,30 @@ bsfa_decode_split_kernel(const DecodeParams p) {
     const int key0 = kb * BS;
     if constexpr (PAGED) {
       const int off0 = key0 % ps;
-      const int last = kv_len - 1 - key0;  // rows past it read row kv_len-1 (masked)
+      if (ps >= 16) {
+        // Every 16-key tile lies in one page (pages are powers of two >= 16, tiles start at
+        // multiples of 16): one buffer resource per tile at a scalar page base, the per-lane
+        // offsets of the contiguous path, and rows past kv_len read as zeros (masked).
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int row = min(t * 16 + hc, last) + off0;
-        const int page = __shfl(pgv, row / ps, kWave);
-        const uint16_t* src = kbase + (int64_t)page * p.sk[0] + (int64_t)(row % ps) * ks2 + g4 * 8;
+        for (int t = 0; t < NT; ++t) {
+          const int row0 = off0 + t * 16;
+          const int page = __builtin_amdgcn_readlane(pgv, row0 / ps);
+          const int rows = min(16, kv_len - key0 - t * 16);
+          const __amdgpu_buffer_rsrc_t kr = decode_rsrc(
+              kbase + (int64_t)page * p.sk[0] + (int64_t)(row0 % ps) * ks2, (int64_t)max(rows, 0) * ks2 * 2);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) ka[t][ks] = *(const u32x4_t*)(src + ks * 32);
+          for (int ks = 0; ks < KS; ++ks) ka[t][ks] = buf_load16(kr, k_voff + ks * 64, 0);
+        }
+      } else {
+        const int last = kv_len - 1 - key0;  // rows past it read row kv_len-1 (masked)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int row = min(t * 16 + hc, last) + off0;
+          const int page = __shfl(pgv, row / ps, kWave);
+          const uint16_t* src = kbase + (int64_t)page * p.sk[0] + (int64_t)(row % ps) * ks2 + g4 * 8;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) ka[t][ks] = *(const u32x4_t*)(src + ks * 32);
+        }
       }
     } else {
       const __amdgpu_buffer_rsrc_t kr = decode_rsrc(kbase + (int64_t)key0 * ks2, (int64_t)BS * ks2 * 2);
