@@ -187,6 +187,8 @@ PAGED_CASES = [
     (1, 16, 2, 640, 64, 32, 16, 3),
     (3, 32, 8, 1000, 128, 128, 16, None),  # block 128 (two 64-key halves), partial last block
     (2, 8, 2, 900, 64, 128, 64, 2),
+    (2, 8, 2, 700, 128, 64, 8, None),      # 8-token pages: a 16-key tile spans two pages
+    (1, 4, 1, 333, 64, 32, 8, 2),
 ]
 
 
