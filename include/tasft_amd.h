@@ -36,7 +36,7 @@ extern "C" {
 /* Message of the last error on this thread ("" if none). */
 const char* tasft_last_error(void);
 
-/* ABI version of this library (8). */
+/* ABI version of this library (9). */
 int tasft_abi_version(void);
 
 /* Element types of the 16-bit tensors (the `dtype` argument). The reference kernel takes
@@ -238,6 +238,12 @@ size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t nu
  * flags: TASFT_GATE_CAUSAL (zero the upper block triangle, reference is_causal) |
  * TASFT_GATE_FORCE_DIAGONAL (set the diagonal blocks in hard_mask regardless of tau).
  * head_dim a multiple of 8, at most 256; any block_size >= 1.
+ * Block size 64 with head_dim 64 or 128 and hidden a multiple of 32 up to 128 runs as one
+ * kernel (after a one-workgroup reset of its counters in the workspace): workgroups that
+ * pool the query blocks wait, bounded by 1 ms of wall clock, for the workgroups that pool
+ * the key blocks. Should that wait ever give up, bit 63 of active_count is set and the
+ * affected rows hold NaN scores and no mask bit; callers that read active_count check it.
+ * One call at a time per workspace: calls that overlap on one workspace race.
  */
 #define TASFT_GATE_CAUSAL 1
 #define TASFT_GATE_FORCE_DIAGONAL 2
@@ -248,6 +254,14 @@ int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float*
                    int64_t num_q_heads, int64_t num_kv_heads, int64_t seq_len, int64_t head_dim,
                    int64_t block_size, int64_t hidden, const int64_t* q_strides,
                    const int64_t* k_strides, int flags, int dtype, void* stream);
+
+/*
+ * Diagnostic for tests of the error path above; no counterpart in the reference. While
+ * enable is nonzero, the one-launch gate's key workgroups publish nothing and every query
+ * workgroup's wait gives up after 20 us (bit 63 of active_count set, NaN scores); every
+ * workgroup still exits normally. Returns 0.
+ */
+int tasft_gate_debug_wait_fault(int enable);
 
 /*
  * The pairwise stage of the gate on precomputed projected units, for query-block rows that

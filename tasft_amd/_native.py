@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "tasft_bsfa_decode_fwd_noalloc",
     "tasft_gate_workspace_bytes",
     "tasft_gate_fwd",
+    "tasft_gate_debug_wait_fault",
     "tasft_gate_rows_fwd",
     "tasft_gate_decode_rows_fwd",
     "tasft_gate_bwd_workspace_bytes",
@@ -55,6 +56,7 @@ _SZ = ctypes.c_size_t
 _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tasft_last_error": (ctypes.c_char_p, []),
     "tasft_abi_version": (_I, []),
+    "tasft_gate_debug_wait_fault": (_I, [_I]),
     "tasft_bsfa_prefill_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "tasft_bsfa_prefill_fwd": (
         _I,

@@ -28,4 +28,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* tasft_last_error(void) { return tasft::g_last_error; }
 
-extern "C" int tasft_abi_version(void) { return 8; }
+extern "C" int tasft_abi_version(void) { return 9; }

@@ -18,13 +18,13 @@
 // diagonal blocks on in the hard mask (soft scores unchanged).
 //
 // Block size 64, D in {64, 128}, hidden a multiple of 32 up to 128 (the benchmarked gate):
-// two launches. gate_pool_proj64_kernel pools and projects every key chunk and a share of
-// the query chunks (half at B=4, 32 heads, S=8192); gate_qpool_pair64_kernel then takes
-// every query chunk, pooling the others itself, and evaluates each chunk's rows as soon as
-// its units exist. No workgroup
-// waits for another within a launch. Otherwise one pooling launch (streaming for blocks 32,
-// 64 and 128 with D in {64, 128}, generic else) is followed by gate_pairwise_kernel.
+// one kernel, gate_fused64_kernel, after a one-workgroup reset of its completion counters.
+// Its first workgroups pool and project the key chunks; every other workgroup pools and
+// projects one query chunk, waits for its KV group's key units and evaluates the chunk's
+// rows. Otherwise one pooling launch (streaming for blocks 32, 64 and 128 with D in
+// {64, 128}, generic else) is followed by gate_pairwise_kernel.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -49,22 +49,9 @@ struct GatePoolParams {
   unsigned long long* counter;
   int64_t sq[3], sk[3];
   int64_t wg0;  // first workgroup index of the launch (gate_pool_proj64_kernel)
-  int64_t mix;  // gate_qpool_pair64_kernel: workgroups per round (the CU count)
-  int64_t rounds;  // gate_qpool_pair64_kernel: rounds per group (see there)
-  int64_t pre;     // gate_qpool_pair64_kernel: rounds per group on pre-pooled chunks
   int B, Hq, Hkv, S, D, bs, NB, hidden, chunks;
   int rotate;   // chunk-major query chunk order (query_chunk)
 };
-
-// Query chunks gate_qpool_pair64_kernel pools itself: the last rounds - pre rounds of every
-// group of `rounds` rounds of `mix` workgroups (a partial last group fills its first rounds
-// first).
-__host__ __device__ __forceinline__ int64_t gate_fresh_chunks(int64_t nq, int64_t mix,
-                                                              int64_t rounds, int64_t pre) {
-  const int64_t tail = nq % (rounds * mix);
-  const int64_t rest = tail - pre * mix;
-  return (nq / (rounds * mix)) * (rounds - pre) * mix + (rest > 0 ? rest : 0);
-}
 
 // Query chunk index g (0 .. B*Hq*chunks - 1) to its (b, head) and chunk: (b, head)-major,
 // or with `rotate` chunk-major (g = chunk * B*Hq + bh), so that low indices are the early
@@ -180,7 +167,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gate_rsrc(const void* base, in
 // Pools kFusePB blocks (chunk `chunk`) of BSZ rows (32, 64 or 128) of one (b, head) row stream
 // of Q (is_q) or K and projects their means; `red` is the workgroup's LDS (4 x kFusePB x D
 // floats).
-template <int D, int DT, int BSZ = 64>
+template <int D, int DT, int BSZ = 64, bool PUBLISH = false>
 __device__ __forceinline__ void pool_proj64(const GatePoolParams& p, bool is_q, int64_t bh,
                                             int chunk, float (&red)[4][kFusePB][D]) {
   static_assert(BSZ == 32 || BSZ == 64 || BSZ == 128, "block rows");
@@ -305,7 +292,14 @@ __device__ __forceinline__ void pool_proj64(const GatePoolParams& p, bool is_q, 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int blk = 4 * lq + r;
-        if (blk < nblk) dst[(int64_t)blk * p.hidden + c] = acc[r] + bias;
+        if (blk >= nblk) continue;
+        // PUBLISH: agent-scope atomic stores (written through to the device coherence
+        // point), for units that workgroups on other XCDs read in the same launch.
+        if (PUBLISH)
+          __hip_atomic_store(dst + (int64_t)blk * p.hidden + c, acc[r] + bias, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        else
+          dst[(int64_t)blk * p.hidden + c] = acc[r] + bias;
       }
     }
   }
@@ -527,8 +521,6 @@ gate_pairwise_kernel(const GatePairParams p) {
 // split as gate_pairwise_kernel, with A_i and B_j summed in a fixed order.
 constexpr int kFuseHid = 32;
 constexpr int kFuseMaxHid = 128;
-constexpr int kGateRounds = 3;     // rounds per group in gate_qpool_pair64_kernel
-constexpr int kGatePreRounds = 1;  // of which on chunks the first launch pooled
 constexpr int kFuseKeys = 128;
 constexpr int kFuseLdq = kFusePB + 4;
 constexpr int kFuseLdw = 32 + 4;
@@ -536,35 +528,15 @@ constexpr int kFuseWave = kFuseHid * kFuseLdw + 32;  // one wave's key units + i
 constexpr int kFuseFloats = kFuseMaxHid * kFuseLdq + kFuseMaxHid + 16 * kFusePB + kFusePB +
                             4 * kFuseWave;
 
-template <int D, int DT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
-gate_qpool_pair64_kernel(const GatePoolParams p, const GatePairParams q) {
-  constexpr int kRed = 4 * kFusePB * D;
-  constexpr int kLds = kRed > kFuseFloats ? kRed : kFuseFloats;
-  __shared__ __attribute__((aligned(16))) float lds[kLds];
-  __shared__ unsigned int wave_count[4];
-  static_assert(kFuseHid == 32 && kFusePB == 16 && kFuseKeys == 128, "thread layouts below");
-
-  // Workgroups come in rounds of `mix` (the CU count, so every CU holds both kinds), in
-  // groups of `rounds` rounds: the first `pre` rounds take query chunks the first launch
-  // already pooled (the last n1 of the nq chunk indices), which go straight to the pairwise
-  // MLP; the other rounds take the rest, pooled and projected here first. One kind's MLP
-  // then runs while the other streams Q. In chunk-major order (query_chunk) the chunks
-  // pooled here are the early query rows, whose MLP is the shortest, and the pre-pooled
-  // ones the late rows.
-  const int fchunks = (p.NB + kFusePB - 1) / kFusePB;
-  const int64_t nq = (int64_t)p.B * p.Hq * fchunks;
-  const int64_t n1 = nq - gate_fresh_chunks(nq, p.mix, p.rounds, p.pre);
-  const int64_t grp = blockIdx.x / (p.rounds * p.mix), o = blockIdx.x % (p.rounds * p.mix);
-  const bool pooled = o < p.pre * p.mix;
-  const int64_t g = pooled ? nq - n1 + grp * p.pre * p.mix + o
-                           : grp * (p.rounds - p.pre) * p.mix + (o - p.pre * p.mix);
-  int64_t bh;
-  int chunk;
-  query_chunk(p, g, fchunks, bh, chunk);
-  if (!pooled)
-    pool_proj64<D, DT>(p, true, bh, chunk, *reinterpret_cast<float(*)[4][kFusePB][D]>(lds));
-
+// The pairwise rows of query chunk `chunk` of (b, head) `bh`, whose units are in q.uq: the
+// chunk's query units and w_out staged once, A_i, then the key blocks in groups of
+// kFuseKeys (see the layout note above), sigmoid, causal zero, tau and the forced
+// diagonal; the chunk's active count is added to q.counter. `keys_ready` is called by every
+// thread before the first key unit is read and returns whether the key units may be read.
+template <typename KeysReady>
+__device__ __forceinline__ void pair_chunk64(const GatePairParams& q, int64_t bh, int chunk,
+                                             float* lds, unsigned int* wave_count,
+                                             KeysReady&& keys_ready) {
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
   const int tr = lane / 8, tc = lane % 8;
@@ -611,6 +583,19 @@ gate_qpool_pair64_kernel(const GatePoolParams p, const GatePairParams q) {
     arow[tid] = a;
   }
   __syncthreads();
+
+  // The key units are read from here on: the caller's wait for them (a no-op when an
+  // earlier launch wrote them). Without them the chunk's rows get NaN scores and an empty
+  // mask, and nothing is added to the active count.
+  if (!keys_ready()) {
+    for (int e = tid; e < nrows * q.NBk; e += 256) {
+      const int64_t o = (bh * q.NBq + i0 + e / q.NBk) * (int64_t)q.NBk + e % q.NBk;
+      q.soft[o] = __builtin_nanf("");
+      q.mask[o] = 0;
+      if (q.logits) q.logits[o] = __builtin_nanf("");
+    }
+    return;
+  }
 
   // Staging role of this lane: key block kk of the wave's 32, units 16*hh .. +15 of a round.
   const int kk = lane % 32, hh = lane / 32;
@@ -713,6 +698,108 @@ gate_qpool_pair64_kernel(const GatePoolParams p, const GatePairParams q) {
     const unsigned int t = (wave_count[0] + wave_count[1]) + (wave_count[2] + wave_count[3]);
     if (t) atomicAdd(q.counter, (unsigned long long)t);
   }
+}
+
+
+// ---------------------------------------------------------------------------------------
+// One-launch gate (block 64, D 64 or 128, hidden a multiple of kFuseHid up to kFuseMaxHid).
+//
+// Workgroups 0 .. nk-1 pool and project the key chunks of every (b, KV head), then raise
+// that group's completion counter. Each later workgroup pools and projects one query
+// chunk, stages its units and A_i, waits until every key chunk of its group is complete,
+// and evaluates its rows (pair_chunk64). Query chunks run in reverse chunk-major order:
+// the late query rows (the longest MLP) start first, and the workgroups dispatched last,
+// once key workgroups have left, take the early rows, whose MLP is short.
+//
+// Publication follows the gfx950 memory model at agent scope: every thread of a key
+// workgroup makes its unit stores visible device-wide (release fence: L2 written back)
+// before one relaxed agent-scope add to the counter; thread 0 of a query workgroup polls
+// the counter with acquire loads (device-level reads), and after the barrier every thread
+// runs an acquire fence (L1 and L2 invalidated) before reading units. Measured on the box
+// with a bounded probe: a counter raised on one XCD is seen by pollers on all eight, and the
+// data published with it reads back exactly.
+//
+// The wait cannot deadlock: a workgroup waits only on workgroups of lower index, which wait
+// on nothing, and each XCD dispatches its workgroups in index order. It is bounded anyway
+// by the wall clock (s_memrealtime, 100 MHz): after kGateWaitTicks the workgroup gives up,
+// writes NaN scores and an empty mask for its rows and sets bit 63 of the active count,
+// which the host reports as an error.
+// ---------------------------------------------------------------------------------------
+constexpr unsigned long long kGateWaitTicks = 100000;  // 1 ms
+constexpr int kGateSyncStride = 16;                   // u32 per completion counter (64 bytes)
+constexpr unsigned long long kGateTimeoutBit = 1ull << 63;
+
+struct GateSync {
+  unsigned int* done;  // [B * Hkv] completion counters, kGateSyncStride apart, zeroed per call
+  unsigned long long wait_ticks;  // bound of a query workgroup's wait (kGateWaitTicks)
+  // Diagnostic (tasft_gate_debug_wait_fault): key workgroups do not raise their counter, so
+  // every wait runs into its bound and the error path is taken.
+  int skip_publish;
+};
+
+template <int D, int DT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
+gate_fused64_kernel(const GatePoolParams p, const GatePairParams q, const GateSync sy) {
+  constexpr int kRed = 4 * kFusePB * D;
+  constexpr int kLds = kRed > kFuseFloats + 8 ? kRed : kFuseFloats + 8;
+  // The pooling sums, then the pairwise staging; the per-wave counts and the wait result
+  // sit past the staging area, so the workgroup needs exactly kLds floats (32 KB at D 128:
+  // five workgroups per CU, every workgroup of config 2 resident at once).
+  __shared__ __attribute__((aligned(16))) float lds[kLds];
+  unsigned int* wave_count = reinterpret_cast<unsigned int*>(lds + kFuseFloats);
+  int& ready_s = *reinterpret_cast<int*>(lds + kFuseFloats + 4);
+  static_assert(kFuseHid == 32 && kFusePB == 16 && kFuseKeys == 128, "thread layouts");
+
+  auto& red = *reinterpret_cast<float(*)[4][kFusePB][D]>(lds);
+  const int fchunks = (p.NB + kFusePB - 1) / kFusePB;
+  const int64_t nk = (int64_t)p.B * p.Hkv * fchunks;
+  const int64_t nq = (int64_t)p.B * p.Hq * fchunks;
+  const int64_t wg = blockIdx.x;
+  if (wg < nk) {
+    const int64_t bkv = wg / fchunks;
+    pool_proj64<D, DT, 64, true>(p, false, bkv, (int)(wg % fchunks), red);
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this thread's unit stores are performed
+    __syncthreads();
+    if (threadIdx.x == 0 && !sy.skip_publish)
+      __hip_atomic_fetch_add(sy.done + bkv * kGateSyncStride, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  int64_t bh;
+  int chunk;
+  query_chunk(p, nq - 1 - (wg - nk), fchunks, bh, chunk);
+  pool_proj64<D, DT>(p, true, bh, chunk, red);
+  const int b = (int)(bh / q.Hq), kvh = (int)(bh % q.Hq) / q.G;
+  const unsigned int* cnt = sy.done + ((int64_t)b * q.Hkv + kvh) * kGateSyncStride;
+  pair_chunk64(q, bh, chunk, lds, wave_count, [&]() -> bool {
+    if (threadIdx.x == 0) {
+      const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+      int ok = 0;
+      for (;;) {
+        if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (unsigned)fchunks) {
+          ok = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > sy.wait_ticks) break;
+        __builtin_amdgcn_s_sleep(8);
+      }
+      if (!ok) atomicOr(q.counter, kGateTimeoutBit);
+      ready_s = ok;
+      // One acquire for the workgroup: it invalidates this CU's L1 and the XCD's L2 lines,
+      // which the barrier below orders before every thread's unit reads.
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    return ready_s != 0;
+  });
+}
+
+// Zeroes the completion counters of gate_fused64_kernel and the active count (a kernel on
+// the caller's stream, so the call can be captured in a graph).
+__global__ void __launch_bounds__(256)
+gate_sync_reset_kernel(unsigned int* done, int n, unsigned long long* counter) {
+  for (int i = threadIdx.x; i < n; i += 256) done[(int64_t)i * kGateSyncStride] = 0u;
+  if (threadIdx.x == 0) *counter = 0ull;
 }
 
 // One cached decode step's gate rows, for a KV head and its G <= kRowMaxG query heads per
@@ -1046,6 +1133,23 @@ static int gate_device_cus() {
   return cached[dev];
 }
 
+// Diagnostic switch of tasft_gate_debug_wait_fault: while set, the one-launch gate's key
+// workgroups publish nothing and each query workgroup's wait gives up after kGateFaultTicks.
+static std::atomic<int> g_gate_wait_fault{0};
+constexpr unsigned long long kGateFaultTicks = 2000;  // 20 us
+
+extern "C" int tasft_gate_debug_wait_fault(int enable) {
+  g_gate_wait_fault.store(enable ? 1 : 0);
+  return kOk;
+}
+
+// Bytes of the projected units at the front of the gate workspace, rounded up to 256.
+static size_t gate_units_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                               int64_t nb, int64_t hidden) {
+  const size_t b = (size_t)(batch * (num_q_heads + num_kv_heads) * nb * hidden) * sizeof(float);
+  return (b + 255) & ~(size_t)255;
+}
+
 extern "C" size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads,
                                              int64_t num_kv_heads, int64_t seq_len,
                                              int64_t head_dim, int64_t block_size,
@@ -1054,8 +1158,11 @@ extern "C" size_t tasft_gate_workspace_bytes(int64_t batch, int64_t num_q_heads,
       block_size <= 0 || hidden <= 0)
     return 0;
   const int64_t nb = (seq_len + block_size - 1) / block_size;
-  // Projected units, hidden fp32 values per query block and per key block.
-  return (size_t)(batch * (num_q_heads + num_kv_heads) * nb * hidden) * sizeof(float);
+  // Projected units, hidden fp32 values per query block and per key block, then (at a
+  // 256-byte boundary) one 64-byte completion counter per (b, KV head) for the one-launch
+  // gate.
+  return gate_units_bytes(batch, num_q_heads, num_kv_heads, nb, hidden) +
+         (size_t)(batch * num_kv_heads) * kGateSyncStride * sizeof(unsigned int);
 }
 
 extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, const float* b_in,
@@ -1126,9 +1233,6 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
   pp.chunks = (int)chunks;
 
   pp.wg0 = 0;
-  pp.mix = 1;
-  pp.rounds = 2;
-  pp.pre = 1;
   pp.rotate = 0;
 
   GatePairParams qp;
@@ -1163,24 +1267,35 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
                             std::max(q_strides[2], k_strides[2]) * 2 < 0x7fffffffLL;
   if (fast) {
     const int64_t fchunks = (nb + kFusePB - 1) / kFusePB;
-    // With hidden a multiple of kFuseHid, at most kFuseMaxHid: the first launch pools and projects the key
-    // chunks only, and gate_qpool_pair64_kernel pools each query chunk and evaluates its
-    // rows. Otherwise one launch pools both and gate_pairwise_kernel follows.
+    // Block 64 with hidden a multiple of kFuseHid, at most kFuseMaxHid: the whole gate in
+    // gate_fused64_kernel. Otherwise one launch pools and projects Q and K, and
+    // gate_pairwise_kernel follows.
     const bool fused = block_size == 64 && hidden % kFuseHid == 0 && hidden <= kFuseMaxHid;
-    const int64_t nq = batch * num_q_heads * fchunks;
-    int64_t n1 = 0;
     if (fused) {
-      // The first launch pools the key chunks and the n1 query chunks that the fused
-      // kernel's even rounds take (see gate_qpool_pair64_kernel).
-      pp.mix = gate_device_cus();
-      pp.rounds = kGateRounds;
-      pp.pre = kGatePreRounds;
+      // One launch: key chunks, then query chunks (gate_fused64_kernel), after the
+      // completion counters and the active count are zeroed.
       pp.rotate = 1;
-      n1 = nq - gate_fresh_chunks(nq, pp.mix, pp.rounds, pp.pre);
-      pp.wg0 = nq - n1;
+      GateSync sy;
+      sy.done = (unsigned int*)((uint8_t*)workspace +
+                                gate_units_bytes(batch, num_q_heads, num_kv_heads, nb, hidden));
+      sy.wait_ticks = g_gate_wait_fault ? kGateFaultTicks : kGateWaitTicks;
+      sy.skip_publish = g_gate_wait_fault ? 1 : 0;
+      hipLaunchKernelGGL(gate_sync_reset_kernel, dim3(1), dim3(256), 0, s, sy.done,
+                         (int)(batch * num_kv_heads), active_count);
+      const dim3 g((unsigned)(batch * (num_q_heads + num_kv_heads) * fchunks));
+      if (head_dim == 128 && dtype == kF16)
+        hipLaunchKernelGGL((gate_fused64_kernel<128, kF16>), g, dim3(256), 0, s, pp, qp, sy);
+      else if (head_dim == 128)
+        hipLaunchKernelGGL((gate_fused64_kernel<128, kBf16>), g, dim3(256), 0, s, pp, qp, sy);
+      else if (dtype == kF16)
+        hipLaunchKernelGGL((gate_fused64_kernel<64, kF16>), g, dim3(256), 0, s, pp, qp, sy);
+      else
+        hipLaunchKernelGGL((gate_fused64_kernel<64, kBf16>), g, dim3(256), 0, s, pp, qp, sy);
+      if ((err = hipGetLastError()) != hipSuccess)
+        return set_error(kErrLaunch, "gate: fused launch failed: %s", hipGetErrorString(err));
+      return kOk;
     }
-    const dim3 g1((unsigned)(fused ? n1 + batch * num_kv_heads * fchunks
-                                   : batch * (num_q_heads + num_kv_heads) * fchunks));
+    const dim3 g1((unsigned)(batch * (num_q_heads + num_kv_heads) * fchunks));
     if (block_size == 32) {
       if (head_dim == 128 && dtype == kF16)
         hipLaunchKernelGGL((gate_pool_proj64_kernel<128, kF16, 32>), g1, dim3(256), 0, s, pp);
@@ -1210,20 +1325,6 @@ extern "C" int tasft_gate_fwd(const void* q, const void* k, const float* w_in, c
       hipLaunchKernelGGL((gate_pool_proj64_kernel<64, kBf16>), g1, dim3(256), 0, s, pp);
     if ((err = hipGetLastError()) != hipSuccess)
       return set_error(kErrLaunch, "gate: pool launch failed: %s", hipGetErrorString(err));
-    if (fused) {
-      const dim3 g2((unsigned)nq);
-      if (head_dim == 128 && dtype == kF16)
-        hipLaunchKernelGGL((gate_qpool_pair64_kernel<128, kF16>), g2, dim3(256), 0, s, pp, qp);
-      else if (head_dim == 128)
-        hipLaunchKernelGGL((gate_qpool_pair64_kernel<128, kBf16>), g2, dim3(256), 0, s, pp, qp);
-      else if (dtype == kF16)
-        hipLaunchKernelGGL((gate_qpool_pair64_kernel<64, kF16>), g2, dim3(256), 0, s, pp, qp);
-      else
-        hipLaunchKernelGGL((gate_qpool_pair64_kernel<64, kBf16>), g2, dim3(256), 0, s, pp, qp);
-      if ((err = hipGetLastError()) != hipSuccess)
-        return set_error(kErrLaunch, "gate: fused launch failed: %s", hipGetErrorString(err));
-      return kOk;
-    }
   } else {
     const dim3 g1((unsigned)(batch * (num_q_heads + num_kv_heads) * chunks));
     if (dtype == kF16)

@@ -83,6 +83,14 @@ class GateOutput:
     def sparsity_ratio(self) -> float:
         if self._sparsity is None:
             active = int(self._active.item())
+            if active < 0:
+                # Bit 63 of the device count: the one-launch gate kernel's bounded wait for
+                # its key workgroups gave up; the rows it covers hold NaN scores.
+                raise KernelError(
+                    "tasft_gate_fwd: a query workgroup's wait for the key units timed out; "
+                    "the gate outputs of this call are invalid",
+                    context={"active_count": hex(active & 0xFFFFFFFFFFFFFFFF)},
+                )
             object.__setattr__(self, "_sparsity", 1.0 - active / max(self._total, 1))
         return self._sparsity
 

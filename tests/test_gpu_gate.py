@@ -196,3 +196,89 @@ def test_fp32_inputs_run_the_reference_formula_and_fp16_the_kernel():
     assert f32.soft_scores.dtype == torch.float32 and f16.soft_scores.dtype == torch.float32
     torch.testing.assert_close(f32.logits, hip.logits, rtol=1e-4, atol=1e-5)
     torch.testing.assert_close(f16.logits, hip.logits, rtol=1e-5, atol=1e-6)
+
+
+def _gate_c_abi(gate, q, k, taus, workspace, flags=3):
+    """tasft_gate_fwd through the C ABI on a caller-held workspace; returns (soft, mask, count)."""
+    from tasft_amd import _native
+
+    lib = _native.load_library()
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    nb = math.ceil(S / gate.block_size)
+    dev = q.device
+    w_in = gate.gate_proj_in.weight.detach().float().contiguous()
+    b_in = gate.gate_proj_in.bias.detach().float().contiguous()
+    w_out = gate.gate_proj_out.weight.detach().float().reshape(-1).contiguous()
+    soft = torch.full((B, H, nb, nb), 7.0, dtype=torch.float32, device=dev)
+    mask = torch.full((B, H, nb, nb), 9, dtype=torch.uint8, device=dev)
+    count = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    rc = lib.tasft_gate_fwd(
+        q.data_ptr(), k.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(), taus.data_ptr(),
+        soft.data_ptr(), None, mask.data_ptr(), count.data_ptr(), None, None, workspace.data_ptr(),
+        workspace.numel(), B, H, Hkv, S, D, gate.block_size, gate.gate_hidden_dim,
+        _native.strides(q), _native.strides(k), flags, _native.dtype_code(q.dtype, "gate"),
+        _native.stream_handle(dev))
+    assert rc == 0, lib.tasft_last_error()
+    return soft, mask, count
+
+
+def test_one_launch_gate_reuses_its_workspace():
+    """The one-launch gate (block 64) on one workspace, first filled with 0xFF bytes (its
+    completion counters included), twice in a row with different inputs: each call's outputs
+    equal a fresh-workspace call's bit for bit, and the count (bit 63 clear) is the mask's sum."""
+    from tasft_amd import _native
+
+    dev = require_gpu()
+    B, Hq, Hkv, S, D, hidden = 2, 8, 2, 2048, 128, 64
+    gate = _gate(Hq, D, 64, hidden, True, seed=91).to(dev).requires_grad_(False)
+    taus = torch.linspace(0.4, 0.6, Hq, device=dev)
+    lib = _native.load_library()
+    n = lib.tasft_gate_workspace_bytes(B, Hq, Hkv, S, D, 64, hidden)
+    shared = torch.full((n,), 0xFF, dtype=torch.uint8, device=dev)
+    for seed in (5, 6):
+        q = wl.randn_bf16((B, Hq, S, D), seed, scale=1.0).to(dev)
+        k = wl.randn_bf16((B, Hkv, S, D), seed + 50, scale=1.0).to(dev)
+        soft, mask, count = _gate_c_abi(gate, q, k, taus, shared)
+        fresh = _gate_c_abi(gate, q, k, taus, torch.zeros((n,), dtype=torch.uint8, device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(soft, fresh[0]) and torch.equal(mask, fresh[1])
+        c = int(count.item())
+        assert c >= 0 and c == int(mask.sum().item()) == int(fresh[2].item())
+        with torch.no_grad():
+            mod = gate(q, k, threshold=taus, force_diagonal=True)
+        assert torch.equal(mod.hard_mask.to(torch.uint8), mask)
+
+
+def test_one_launch_gate_wait_error_path():
+    """With the diagnostic switch on, the key workgroups publish nothing: every query
+    workgroup's bounded wait gives up (every workgroup still exits), its rows get NaN scores
+    and no mask bit, bit 63 of the count is set and GateOutput.sparsity_ratio raises
+    KernelError. Switched off again, the same call gives the normal result."""
+    from tasft_amd import _native
+    from tasft_amd.exceptions import KernelError
+
+    dev = require_gpu()
+    gate = _gate(4, 128, 64, 64, True, seed=17).to(dev).requires_grad_(False)
+    q = wl.randn_bf16((1, 4, 1024, 128), 71, scale=1.0).to(dev)
+    k = wl.randn_bf16((1, 2, 1024, 128), 72, scale=1.0).to(dev)
+    with torch.no_grad():
+        good = gate(q, k, threshold=0.5)
+    good_sparsity = good.sparsity_ratio
+    lib = _native.load_library()
+    try:
+        assert lib.tasft_gate_debug_wait_fault(1) == 0
+        with torch.no_grad():
+            bad = gate(q, k, threshold=0.5)
+        torch.cuda.synchronize()
+    finally:
+        lib.tasft_gate_debug_wait_fault(0)
+    assert torch.isnan(bad.soft_scores).all()
+    assert not bad.hard_mask.any()
+    with pytest.raises(KernelError, match="timed out"):
+        _ = bad.sparsity_ratio
+    with torch.no_grad():
+        again = gate(q, k, threshold=0.5)
+    assert torch.equal(again.soft_scores, good.soft_scores)
+    assert torch.equal(again.hard_mask, good.hard_mask)
+    assert again.sparsity_ratio == good_sparsity

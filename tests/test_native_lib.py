@@ -33,13 +33,14 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace_sizes():
     lib = _native.load_library()
-    assert lib.tasft_abi_version() == 8
+    assert lib.tasft_abi_version() == 9
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 8192, 64) == 256
     assert lib.tasft_bsfa_prefill_workspace_bytes(4, 32, 0, 64) == 0
     assert lib.tasft_bsfa_decode_workspace_bytes(64, 32, 128, 4) == 64 * 32 * 4 * 130 * 4
     assert lib.tasft_bsfa_decode_workspace_bytes(0, 32, 128, 4) == 0
     nb = 8192 // 64
-    assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 128, 64, 128) == 4 * 40 * nb * 128 * 4
+    # Projected units, then one 64-byte completion counter per (b, KV head).
+    assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 128, 64, 128) == 4 * 40 * nb * 128 * 4 + 4 * 8 * 64
     assert lib.tasft_gate_workspace_bytes(4, 32, 8, 8192, 0, 64, 128) == 0
     assert lib.tasft_mask_compact_workspace_bytes(4, 32, 128) == 4 * 32 * 128 * 4
     assert lib.tasft_mask_compact_workspace_bytes(0, 32, 128) == 0
