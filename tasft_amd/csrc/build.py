@@ -36,9 +36,11 @@ def _flags() -> list[str]:
         "-Wno-unused-function",
         # Packed fp32 VALU ops are disabled for all device code.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # No NaN is ever produced or tested for (scores are finite or -inf; infinities stay
-        # honoured), so fmaxf() need not quiet its inputs first: without this flag every
-        # max over MFMA results costs an extra v_max_f32 x, x per input.
+        # fmaxf() need not quiet its inputs first (without this flag every max over MFMA
+        # results costs an extra v_max_f32 x, x per input). A NaN score may then be dropped
+        # from a running maximum, but it still reaches the output through exp2 and the PV
+        # product, so NaN in Q, K or V gives NaN output rows as in the reference
+        # (tests/test_gpu_nan.py); infinities stay honoured.
         "-fno-honor-nans",
     ]
 
