@@ -590,9 +590,10 @@ __device__ __forceinline__ void pair_chunk64(const GatePairParams& q, int64_t bh
   if (!keys_ready()) {
     for (int e = tid; e < nrows * q.NBk; e += 256) {
       const int64_t o = (bh * q.NBq + i0 + e / q.NBk) * (int64_t)q.NBk + e % q.NBk;
-      q.soft[o] = __builtin_nanf("");
+      // The quiet-NaN bit pattern, stored as an integer (the build assumes no NaN arithmetic).
+      reinterpret_cast<uint32_t*>(q.soft)[o] = 0x7fc00000u;
       q.mask[o] = 0;
-      if (q.logits) q.logits[o] = __builtin_nanf("");
+      if (q.logits) reinterpret_cast<uint32_t*>(q.logits)[o] = 0x7fc00000u;
     }
     return;
   }

@@ -25,6 +25,7 @@
 
 #include "common.h"
 
+
 #include "../../include/tasft_amd.h"
 
 namespace tasft {
@@ -703,6 +704,11 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 // instruction moves 1 KB; one LDS base (M0) serves four of them
 // through the instruction offset, which the hardware adds to both the global and the LDS
 // address (the field holds 12 bits, so units four apart need their own base).
+// Q and O pass through the V tile, which is free before the row's first V DMA and after
+// its last PV: Q arrives by DMA in the K layout (whole 256-byte rows per request) and is
+// read into the MFMA operand registers like K; O is written there per wave and stored as
+// whole rows, four per instruction. Loading Q and storing O directly in the MFMA layouts
+// touched 32 rows, 32 bytes each, per instruction (1 KB of data in 32 cache lines).
 // ---------------------------------------------------------------------------------------
 // Workgroup barrier without a memory fence. The caller waits (s_waitcnt) for what the
 // barrier publishes; the memory clobber keeps the compiler from moving memory accesses
@@ -774,19 +780,25 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   const uint8_t* mrow = p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)(qb >> p.mshift) * p.sm[2];
 
   const int qrow = qb * BS + wave * 32 + col;
-  const bool qvalid = qrow < S;
   const int kb_end = p.causal ? qb + 1 : NB;
   // Blocks from here on need element masks (causal diagonal or partial last block).
   const int mask_from = p.causal ? qb : ((S % BS) != 0 ? NB - 1 : NB);
   // Loads in the order their results are needed: mask bytes, Q, then the first K DMA.
   uint8_t mb = 0;
   if (lane < kb_end) mb = mrow[(int64_t)(lane >> p.mshift) * p.sm[3]];
-  u32x4_t qf[KSTEPS];
+  // The query block's rows go HBM->LDS by DMA into the V tile (unused until the first V
+  // DMA), in the K tile's swizzled layout: each 1 KB unit is 4 whole rows, so every
+  // request covers full cache lines. Rows past the end arrive as zeros (never stored).
   {
-    // Rows past the end read row S-1: per-row results, never stored.
-    const uint16_t* qr = qbase + (int64_t)(qvalid ? qrow : S - 1) * p.sq[2] + half * 8;
+    int qvoff[UPW];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = *(const u32x4_t*)(qr + ks * 16);
+    for (int i = 0; i < UPW; ++i) {
+      const int byte = (wave * UPW + i) * 1024 + lane * 16;
+      const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+      qvoff[i] = (row * (int)p.sq[2] + swz_k<D>(row, pos) * 8) * 2 - (i & 3) * 1024;
+    }
+    dma_tile_2w<D>(vS, tile_rsrc(qbase + (int64_t)qb * BS * p.sq[2], (int64_t)(S - qb * BS) * p.sq[2] * 2),
+                   qvoff, wave);
   }
   // Buffer resource of key block kb of K or V (rows >= S are out of range: zeros).
   auto block_rsrc = [&](const uint16_t* base, uint32_t rb, int64_t stride, int kb) {
@@ -808,7 +820,20 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   int chunk = 0;
   uint64_t bits = __ballot(mb != 0);
   int kb = next_active_block(mrow, p.sm[3], kb_end, lane, chunk, bits, p.mshift);
-  if (kb >= 0) dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb), kvoff, wave);
+  u32x4_t qf[KSTEPS];
+  if (kb >= 0) {
+    dma_tile_2w<D>(kS, block_rsrc(kbase, krb, p.sk[2], kb), kvoff, wave);
+    __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8): own share of Q landed, K in flight
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  }
+  block_barrier();  // Q visible; the loop's first barrier orders these reads before V's DMA
+  {
+    const int r = wave * 32 + col;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = *(const u32x4_t*)(vS + r * ROWB + swz_k<D>(r, ks * 2 + half) * 16);
+  }
 
   while (kb >= 0) {
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): own share of K(kb) landed
@@ -917,17 +942,28 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
 
   const float l_tot = pair_sum32(l_run);
   const float inv = 1.f / (l_tot > 0.f ? l_tot : 1.f);  // empty rows: O = 0; NaN rows stay NaN
-  if (qvalid) {
-    uint16_t* orow = obase + (int64_t)qrow * p.so[2];
+  // The output through LDS: each wave writes its 32 rows into its own 8 KB of the V tile
+  // (16-byte chunk c of row r at position c ^ (r & 15)), then stores whole 256-byte rows,
+  // four rows per instruction.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's V reads returned
+  block_barrier();                      // every wave is done with the V tile
+  uint8_t* ost = vS + wave * (32 * ROWB);
 #pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt)
+  for (int dt = 0; dt < DTILES; ++dt)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int d0 = dt * 32 + 8 * gq + 4 * half;
-        const u32x2_t w = {pack16x2<DT>(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
-                           pack16x2<DT>(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
-        *(u32x2_t*)(orow + d0) = w;
-      }
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d0 = dt * 32 + 8 * gq + 4 * half;
+      const u32x2_t w = {pack16x2<DT>(oacc[dt][4 * gq + 0] * inv, oacc[dt][4 * gq + 1] * inv),
+                         pack16x2<DT>(oacc[dt][4 * gq + 2] * inv, oacc[dt][4 * gq + 3] * inv)};
+      *(u32x2_t*)(ost + col * ROWB + (((d0 >> 3) ^ (col & 15)) << 4) + (d0 & 7) * 2) = w;
+    }
+  constexpr int CPR = ROWB / 16;  // 16-byte chunks per row
+  const int row0 = qb * BS + wave * 32;
+#pragma unroll
+  for (int j = 0; j < 32 * CPR / kWave; ++j) {
+    const int r = j * (kWave / CPR) + lane / CPR, c = lane % CPR;
+    const u32x4_t v = *(const u32x4_t*)(ost + r * ROWB + ((c ^ (r & 15)) << 4));
+    if (row0 + r < S) *(u32x4_t*)(obase + (int64_t)(row0 + r) * p.so[2] + c * 8) = v;
   }
 }
 
