@@ -302,7 +302,8 @@ int tasft_gate_rows_fwd(const float* uq, const float* uk, const float* w_out,
  * divided by the block size (a zero-padded block mean is then sum x W); b_in, w_out
  * [hidden]; thresholds [Hq]. Outputs [B, Hq, 1, row + 1] contiguous: soft_scores (sigmoid
  * of w_out . relu(q_sum x wq_t + b_in + v_j)), hard_mask (soft >= tau, and the diagonal
- * j = row with TASFT_GATE_FORCE_DIAGONAL). active_count is zeroed and counted by the call.
+ * j = row with TASFT_GATE_FORCE_DIAGONAL). active_count is zeroed and counted by the call;
+ * it may be NULL, and then no count is kept (one launch fewer).
  * Limits: Hq / Hkv <= 8, head_dim <= 256, hidden <= 256 and a multiple of 4.
  */
 int tasft_gate_decode_rows_fwd(const void* q_new, const void* k_new, const int64_t* q_strides,

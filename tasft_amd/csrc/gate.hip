@@ -954,7 +954,7 @@ gate_decode_row_kernel(const GateDecodeRowParams p) {
   __syncthreads();
   if (tid == 0) {
     const unsigned int t = (wave_count[0] + wave_count[1]) + (wave_count[2] + wave_count[3]);
-    if (t) atomicAdd(p.counter, (unsigned long long)t);
+    if (t && p.counter) atomicAdd(p.counter, (unsigned long long)t);
   }
 }
 
@@ -1466,7 +1466,7 @@ extern "C" int tasft_gate_decode_rows_fwd(
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t hidden, int64_t row,
     int reset_sums, int flags, int dtype, void* stream) {
   if (!q_new || !k_new || !q_strides || !k_strides || !q_sum || !k_sum || !uk || !wq_t ||
-      !wk_t || !b_in || !w_out || !thresholds || !soft_scores || !hard_mask || !active_count)
+      !wk_t || !b_in || !w_out || !thresholds || !soft_scores || !hard_mask)
     return set_error(kErrInvalidArgument, "gate_decode_rows: null pointer argument");
   if (dtype != kBf16 && dtype != kF16)
     return set_error(kErrUnsupported, "gate_decode_rows: dtype must be bf16 (0) or fp16 (1), got %d",
@@ -1522,7 +1522,7 @@ extern "C" int tasft_gate_decode_rows_fwd(
   rp.reset = reset_sums ? 1 : 0;
   rp.force_diag = (flags & 2) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(gate_counter_reset_kernel, dim3(1), dim3(64), 0, s, active_count);
+  if (active_count) hipLaunchKernelGGL(gate_counter_reset_kernel, dim3(1), dim3(64), 0, s, active_count);
   const dim3 grid((unsigned)(batch * num_kv_heads));
   auto launch = [&](auto mg) {
     constexpr int MG = decltype(mg)::value;

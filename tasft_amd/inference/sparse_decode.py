@@ -56,6 +56,17 @@ class SparseAttentionDecoder:
         self._ksum = None
         self._qsum = None
         self._ws: dict[int, tuple[torch.Tensor, int]] = {}  # decode workspace per split count
+        # ctypes stride arrays per stride tuple: a step's tensors keep their strides, and
+        # building the arrays was a measurable share of a step's host time.
+        self._stride_arrays: dict[tuple[int, ...], object] = {}
+
+    def _strides(self, t: torch.Tensor):
+        st = t.stride()
+        arr = self._stride_arrays.get(st)
+        if arr is None:
+            arr = _native.strides_array(st)
+            self._stride_arrays[st] = arr
+        return arr
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -118,7 +129,7 @@ class SparseAttentionDecoder:
         dev = q_new.device
         soft = torch.empty((B, Hq, 1, nbk), dtype=torch.float32, device=dev)
         mask = torch.empty((B, Hq, 1, nbk), dtype=torch.uint8, device=dev)
-        active = torch.empty((1,), dtype=torch.int64, device=dev)
+        active = None
         lib = _native.load_library()
         if (Hq // Hkv <= 8 and D <= 256 and hid <= 256 and hid % 4 == 0
                 and q_new.dtype in (torch.bfloat16, torch.float16) and k_new.dtype == q_new.dtype
@@ -126,15 +137,17 @@ class SparseAttentionDecoder:
             # One launch per (b, KV head): block sums, both projections, the kept key unit of
             # block i and the rows (tasft_gate_decode_rows_fwd).
             status = lib.tasft_gate_decode_rows_fwd(
-                q_new.data_ptr(), k_new.data_ptr(), _native.strides(q_new), _native.strides(k_new),
+                q_new.data_ptr(), k_new.data_ptr(), self._strides(q_new), self._strides(k_new),
                 self._qsum.data_ptr(), self._ksum.data_ptr(), self._vk.data_ptr(),
                 self._vk.shape[2] * hid, self._wq_t.data_ptr(), self._wk_t.data_ptr(),
                 self._b_in.data_ptr(), self._w_out.data_ptr(), self._taus.data_ptr(),
-                soft.data_ptr(), mask.data_ptr(), active.data_ptr(), B, Hq, Hkv, D, hid, i,
+                # No device count: the row's sparsity is counted from the mask if asked for.
+                soft.data_ptr(), mask.data_ptr(), None, B, Hq, Hkv, D, hid, i,
                 1 if t % bs == 0 else 0, self._flags, _native.dtype_code(q_new.dtype, "decode rows"),
                 _native.stream_handle(dev))
             _native.check(status, "tasft_gate_decode_rows_fwd", {"position": t})
         else:
+            active = torch.empty((1,), dtype=torch.int64, device=dev)
             if t % bs == 0:
                 self._ksum.zero_()
                 self._qsum.zero_()
@@ -190,8 +203,8 @@ class SparseAttentionDecoder:
         status = lib.tasft_bsfa_decode_fwd(
             q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), m8.data_ptr(),
             None, ws[0].data_ptr(), ws[1], B, Hq, Hkv, S_kv, D, self.bsfa.block_size, splits,
-            _native.strides(q), _native.strides(k_cache), _native.strides(v_cache),
-            _native.strides(out), _native.strides(m8), 1.0 / math.sqrt(D),
+            self._strides(q), self._strides(k_cache), self._strides(v_cache),
+            self._strides(out), self._strides(m8), 1.0 / math.sqrt(D),
             _native.dtype_code(q.dtype, "decode"), _native.stream_handle(q.device))
         _native.check(status, "tasft_bsfa_decode_fwd", {"shape": [B, Hq, S_kv, D]})
         return out

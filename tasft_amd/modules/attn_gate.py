@@ -48,7 +48,8 @@ class GateOutput:
             when causal): fp32 from the HIP kernel, the computation dtype otherwise.
         hard_mask: ``[B, H, NB_q, NB_k]`` bool, ``soft_scores >= threshold``.
         sparsity_ratio: fraction of False entries over the full grid (reference
-            ``attn_gate.py:277``); read lazily from a device counter.
+            ``attn_gate.py:277``); read lazily from a device counter (or, without one, counted
+            from ``hard_mask``).
         num_blocks_q, num_blocks_k: block grid size.
         logits: pre-sigmoid logits (same dtype as ``soft_scores``) when requested, else None.
     """
@@ -67,8 +68,7 @@ class GateOutput:
         logits: torch.Tensor | None = None,
         active_count: torch.Tensor | None = None,
     ) -> None:
-        if sparsity_ratio is None and active_count is None:
-            raise ValueError("GateOutput needs sparsity_ratio or active_count")
+        # With neither, the ratio is counted from hard_mask on first access.
         init = object.__setattr__
         init(self, "soft_scores", soft_scores)
         init(self, "hard_mask", hard_mask)
@@ -82,6 +82,10 @@ class GateOutput:
     @property
     def sparsity_ratio(self) -> float:
         if self._sparsity is None:
+            if self._active is None:
+                object.__setattr__(self, "_sparsity",
+                                   1.0 - int(self.hard_mask.sum().item()) / max(self._total, 1))
+                return self._sparsity
             active = int(self._active.item())
             if active < 0:
                 # Bit 63 of the device count: the one-launch gate kernel's bounded wait for
