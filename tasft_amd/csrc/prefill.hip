@@ -715,20 +715,22 @@ bsfa_prefill_bs64_kernel(const PrefillParams p) {
 // across it.
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int D>
+// AUX: the DMA's cache policy bits (0: default; 2: non-temporal, for Q, which a row reads
+// once, so that it does not push its KV group's K and V out of L2).
+template <int D, int AUX = 0>
 __device__ __forceinline__ void dma_tile_2w(uint8_t* tile, __amdgpu_buffer_rsrc_t rsrc,
                                             const int* voff, int wave) {
   static_assert(D == 128, "eight 1 KB units per wave and tile");
   TASFT_LDS void* b0 = (TASFT_LDS void*)(tile + wave * 8192);
   TASFT_LDS void* b1 = (TASFT_LDS void*)(tile + wave * 8192 + 4096);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[0], 0, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[1], 0, 1024, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[2], 0, 2048, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[3], 0, 3072, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[4], 0, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[5], 0, 1024, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[6], 0, 2048, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[7], 0, 3072, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[0], 0, 0, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[1], 0, 1024, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[2], 0, 2048, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b0, 16, voff[3], 0, 3072, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[4], 0, 0, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[5], 0, 1024, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[6], 0, 2048, AUX);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, b1, 16, voff[7], 0, 3072, AUX);
 }
 
 template <int D, int DT>
@@ -797,8 +799,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
       const int row = byte / ROWB, pos = (byte % ROWB) / 16;
       qvoff[i] = (row * (int)p.sq[2] + swz_k<D>(row, pos) * 8) * 2 - (i & 3) * 1024;
     }
-    dma_tile_2w<D>(vS, tile_rsrc(qbase + (int64_t)qb * BS * p.sq[2], (int64_t)(S - qb * BS) * p.sq[2] * 2),
-                   qvoff, wave);
+    dma_tile_2w<D, 2>(vS, tile_rsrc(qbase + (int64_t)qb * BS * p.sq[2], (int64_t)(S - qb * BS) * p.sq[2] * 2),
+                      qvoff, wave);
   }
   // Buffer resource of key block kb of K or V (rows >= S are out of range: zeros).
   auto block_rsrc = [&](const uint16_t* base, uint32_t rb, int64_t stride, int kb) {
@@ -963,7 +965,8 @@ bsfa_prefill_bs64_2w_kernel(const PrefillParams p) {
   for (int j = 0; j < 32 * CPR / kWave; ++j) {
     const int r = j * (kWave / CPR) + lane / CPR, c = lane % CPR;
     const u32x4_t v = *(const u32x4_t*)(ost + r * ROWB + ((c ^ (r & 15)) << 4));
-    if (row0 + r < S) *(u32x4_t*)(obase + (int64_t)(row0 + r) * p.so[2] + c * 8) = v;
+    // Non-temporal: the output is not read again here, and K/V stay in L2.
+    if (row0 + r < S) __builtin_nontemporal_store(v, (u32x4_t*)(obase + (int64_t)(row0 + r) * p.so[2] + c * 8));
   }
 }
 
