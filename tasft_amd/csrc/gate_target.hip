@@ -98,6 +98,54 @@ gate_target_normalize_kernel(float* data, int64_t group_len, float inv_temp, flo
 }
 
 
+// The same softmax with the group held in registers: 1024 threads, up to 16 values each
+// (groups of at most 16384, e.g. the flat 128 x 128 target of one (b, head)), so each value
+// is read once and written once instead of read three times.
+constexpr int kNormThreads = 1024;
+constexpr int kNormRegs = 16;
+
+__global__ void __launch_bounds__(kNormThreads)
+gate_target_normalize_reg_kernel(float* data, int64_t group_len, float inv_temp, float clamp) {
+  __shared__ float red[kNormThreads / kWave];
+  float* x = data + (int64_t)blockIdx.x * group_len;
+  const int tid = threadIdx.x;
+  float v[kNormRegs];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < kNormRegs; ++r) {
+    const int64_t i = tid + (int64_t)r * kNormThreads;
+    float t = i < group_len ? x[i] : -INFINITY;
+    if (clamp > 0.f && t > -INFINITY) t = fminf(fmaxf(t, -clamp), clamp);
+    v[r] = t * inv_temp;
+    mx = fmaxf(mx, v[r]);
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < kNormThreads / kWave; ++w) mx = fmaxf(mx, red[w]);
+  __syncthreads();
+  float sum = 0.f;
+#pragma unroll
+  for (int r = 0; r < kNormRegs; ++r) {
+    v[r] = expf(v[r] - mx);
+    sum += v[r];
+  }
+  sum = wave_sum(sum);
+  if ((tid & 63) == 0) red[tid >> 6] = sum;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) tot += red[w];
+  const float inv = 1.f / tot;
+#pragma unroll
+  for (int r = 0; r < kNormRegs; ++r) {
+    const int64_t i = tid + (int64_t)r * kNormThreads;
+    if (i < group_len) x[i] = v[r] * inv;
+  }
+}
+
 // Block size 64, scores with an additive mask (unmasked scores run the one-wave-per-head
 // kernel below, 7% faster at config 5). A workgroup owns one query block of HPW query heads
 // of the same KV head (the target is dense, so these heads read exactly the same K blocks)
@@ -598,6 +646,66 @@ gate_kl_kernel(const float* soft, const float* target, int64_t n, float inv_batc
   }
 }
 
+
+// The same loss with the (b, head)'s scores and target held in registers: 1024 threads, up
+// to kKlRegs elements each (NB_q * NB_k <= 16384, i.e. 128 x 128 blocks), so each value is
+// read from memory once instead of three (g) and twice (t) times.
+constexpr int kKlThreads = 1024;
+constexpr int kKlRegs = 16;
+
+__device__ __forceinline__ float block_sum1024(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kKlThreads / 64; ++w) s += red[w];
+  return s;
+}
+
+__global__ void __launch_bounds__(kKlThreads)
+gate_kl_reg_kernel(const float* soft, const float* target, int64_t n, float inv_batch,
+                   float* loss_part, float* grad) {
+  __shared__ float red[kKlThreads / 64];
+  const int64_t bh = blockIdx.x;
+  const float* g = soft + bh * n;
+  const float* t = target + bh * n;
+  const int tid = threadIdx.x;
+  float gv[kKlRegs], tv[kKlRegs];
+  float z = 0.f;
+#pragma unroll
+  for (int r = 0; r < kKlRegs; ++r) {
+    const int64_t i = tid + (int64_t)r * kKlThreads;
+    gv[r] = i < n ? g[i] : 0.f;
+    tv[r] = i < n ? t[i] : 0.f;
+    z += gv[r];
+  }
+  z = block_sum1024(z, red) + kKlEps;
+  const float inv_z = 1.f / z;
+  float l = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int r = 0; r < kKlRegs; ++r) {
+    if (tv[r] > 0.f) {
+      const float u = gv[r] * inv_z + kKlEps;
+      l += tv[r] * (logf(tv[r]) - logf(u));
+      s2 += tv[r] * gv[r] / u;
+    }
+  }
+  l = block_sum1024(l, red);
+  s2 = block_sum1024(s2, red);
+  if (tid == 0) loss_part[bh] = l;
+  if (grad) {
+    float* gr = grad + bh * n;
+    const float c = s2 * inv_z;
+#pragma unroll
+    for (int r = 0; r < kKlRegs; ++r) {
+      const int64_t i = tid + (int64_t)r * kKlThreads;
+      if (i < n) gr[i] = inv_batch * inv_z * (c - tv[r] / (gv[r] * inv_z + kKlEps));
+    }
+  }
+}
+
 }  // namespace tasft
 
 using namespace tasft;
@@ -697,8 +805,12 @@ extern "C" int tasft_gate_target_fwd(const void* q, const void* k, const float* 
   if (normalize != 2) {
     const int64_t groups = normalize == 0 ? batch * num_q_heads : batch * num_q_heads * nb;
     const int64_t len = normalize == 0 ? nb * nb : nb;
-    hipLaunchKernelGGL(gate_target_normalize_kernel, dim3((unsigned)groups), dim3(256), 0, s,
-                       target, len, 1.f / temperature, clamp);
+    if (len > 1024 && len <= (int64_t)kNormThreads * kNormRegs)
+      hipLaunchKernelGGL(gate_target_normalize_reg_kernel, dim3((unsigned)groups), dim3(kNormThreads), 0,
+                         s, target, len, 1.f / temperature, clamp);
+    else
+      hipLaunchKernelGGL(gate_target_normalize_kernel, dim3((unsigned)groups), dim3(256), 0, s,
+                         target, len, 1.f / temperature, clamp);
     if ((err = hipGetLastError()) != hipSuccess)
       return set_error(kErrLaunch, "gate_target: normalize launch failed: %s", hipGetErrorString(err));
   }
@@ -714,9 +826,15 @@ extern "C" int tasft_gate_kl_fwd(const float* gate_scores, const float* target, 
     return set_error(kErrInvalidArgument, "gate_kl: sizes must be positive");
   if (batch * num_heads > 0x7fffffffLL)
     return set_error(kErrUnsupported, "gate_kl: problem too large for one launch");
-  hipLaunchKernelGGL(gate_kl_kernel, dim3((unsigned)(batch * num_heads)), dim3(256), 0,
-                     (hipStream_t)stream, gate_scores, target, num_blocks_q * num_blocks_k,
-                     1.f / (float)batch, loss_partials, grad_scores);
+  const int64_t n = num_blocks_q * num_blocks_k;
+  if (n <= (int64_t)kKlThreads * kKlRegs)
+    hipLaunchKernelGGL(gate_kl_reg_kernel, dim3((unsigned)(batch * num_heads)), dim3(kKlThreads), 0,
+                       (hipStream_t)stream, gate_scores, target, n, 1.f / (float)batch,
+                       loss_partials, grad_scores);
+  else
+    hipLaunchKernelGGL(gate_kl_kernel, dim3((unsigned)(batch * num_heads)), dim3(256), 0,
+                       (hipStream_t)stream, gate_scores, target, n, 1.f / (float)batch,
+                       loss_partials, grad_scores);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     return set_error(kErrLaunch, "gate_kl: launch failed: %s", hipGetErrorString(err));

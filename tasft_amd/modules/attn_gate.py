@@ -431,6 +431,21 @@ def _launch_gate(gate: AttnGate, q: torch.Tensor, k: torch.Tensor, taus: torch.T
             "q_means": qm, "k_means": km, "workspace": workspace, "w_in": w_in, "w_out": w_out}
 
 
+def _weight_grad(d: torch.Tensor, m: torch.Tensor, chunk: int = 256) -> torch.Tensor:
+    """``d^T @ m`` for tall fp32 operands ([K, hidden] and [K, D], K = B * H * NB).
+
+    The output is one small tile while K runs to tens of thousands, so a single GEMM runs
+    on a handful of workgroups that each walk all of K. Split K into chunks of ``chunk``
+    rows as a batched product and sum the partial products instead (K not a multiple of
+    ``chunk``, or a single chunk: one plain GEMM).
+    """
+    K = d.shape[0]
+    if K % chunk or K < 2 * chunk:
+        return d.t() @ m
+    c = K // chunk
+    return torch.bmm(d.view(c, chunk, -1).transpose(1, 2), m.view(c, chunk, -1)).sum(0)
+
+
 class _HipGateFunction(torch.autograd.Function):
     """AttnGate forward/backward on the HIP kernels (gate training).
 
@@ -476,8 +491,8 @@ class _HipGateFunction(torch.autograd.Function):
               .sum((0, 3)) * w_out)
         dw_out = partials[2 * tiles * plane:].view(-1, hidden).sum(0)
         db_in = du.sum((0, 1, 2))
-        dw_q = du.reshape(-1, hidden).t() @ qm.reshape(-1, D)
-        dw_k = dv.reshape(-1, hidden).t() @ km.reshape(-1, D)
+        dw_q = _weight_grad(du.reshape(-1, hidden), qm.reshape(-1, D))
+        dw_k = _weight_grad(dv.reshape(-1, hidden), km.reshape(-1, D))
         dw_in = torch.cat([dw_q, dw_k], dim=1)
         gq = gk = None
         if ctx.needs_input_grad[0]:

@@ -36,6 +36,7 @@ CASES = [
     (1, 3, 3, 333, 128, 32, True),    # bs=32, one head per workgroup, last 64-block half empty
     (2, 4, 2, 640, 64, 64, True),     # two query heads per KV head share the K tiles, D=64
     (1, 3, 3, 200, 128, 64, False),   # one head per workgroup, non-causal, ragged
+    (1, 2, 1, 2000, 64, 32, True),    # flat groups of 63 x 63 > 1024: register-resident softmax
 ]
 
 
@@ -56,10 +57,10 @@ def test_block_max_and_targets_match_oracle(B, Hq, Hkv, S, D, bs, causal):
         np.testing.assert_allclose(to_np(got), ref, rtol=1e-3, atol=1e-7)
 
 
-@pytest.mark.parametrize("bs", (32, 64, 128))
-def test_clamp_temperature_variant(bs):
+@pytest.mark.parametrize(("bs", "S"), [(32, 256), (64, 256), (128, 256), (32, 2048)])
+def test_clamp_temperature_variant(bs, S):
     dev = require_gpu()
-    q, k, _ = wl.qkv(wl.Shape(1, 4, 4, 256, 128), 77)
+    q, k, _ = wl.qkv(wl.Shape(1, 4, 4, S, 128), 77)
     # Scale the queries so some block maxima exceed the clamp.
     q = (q.float() * 2000).to(torch.bfloat16)
     got = _gt(q.to(dev), k.to(dev), bs, normalize="flat", temperature=2.0, clamp=50.0)

@@ -25,12 +25,15 @@ from tasft_amd.training import TASFTObjective, gate_loss_from_qk, gate_target_fr
 pytestmark = pytest.mark.gpu
 
 
-def test_gate_kl_kernel_matches_oracle():
+@pytest.mark.parametrize("NB", [37, 128, 160])
+def test_gate_kl_kernel_matches_oracle(NB):
+    """NB 37 and 128 (16384 entries per (b, head), the largest) run the register-resident
+    kernel; NB 160 runs the streaming one."""
     from tasft_amd.training.objectives import _GateKL
 
     dev = require_gpu()
-    g = torch.Generator().manual_seed(31)
-    B, H, NB = 3, 5, 37
+    g = torch.Generator().manual_seed(31 + NB)
+    B, H = 3, 5
     soft = torch.sigmoid(torch.randn(B, H, NB, NB, generator=g)) * torch.ones(NB, NB).tril()
     raw = torch.randn(B, H, NB, NB, generator=g) * 4
     target = torch.softmax(raw.view(B, H, -1), -1).view(B, H, NB, NB)
@@ -89,6 +92,7 @@ GATE_CASES = [
     (1, 4, 4, 700, 64, 64, 48, True, True),       # D=64, hidden not a multiple of 64, Q/K grads
     (2, 4, 2, 300, 128, 32, 200, False, True),    # generic pool kernel, non-causal, two unit rounds
     (1, 2, 1, 2100, 128, 64, 32, True, False),    # 33 blocks: partial last tile
+    (4, 8, 4, 4096, 64, 64, 64, True, False),     # weight gradients split over K (8 and 4 chunks)
 ]
 
 

@@ -426,3 +426,17 @@ def test_bundle_gates_keep_trained_width_and_per_head_thresholds(tmp_path):
     write_bundle(tmp_path / "b2", {0: gates[0]}, {})
     with pytest.raises(BundleError, match="head_dim=64"):
         load_bundle_gates(tmp_path / "b2", num_heads=4, head_dim=64)
+
+
+@pytest.mark.parametrize("K", [100, 256, 512, 4096 + 256])
+def test_gate_weight_grad_split_over_k_equals_one_product(K):
+    """The gate backward's d^T @ m, summed over K chunks as a batched product (K a multiple
+    of the chunk, at least two chunks) or taken as one product (otherwise)."""
+    from tasft_amd.modules.attn_gate import _weight_grad
+
+    g = torch.Generator().manual_seed(K)
+    d = torch.randn(K, 48, generator=g, dtype=torch.float64)
+    m = torch.randn(K, 80, generator=g, dtype=torch.float64)
+    got = _weight_grad(d, m)
+    assert got.shape == (48, 80)
+    torch.testing.assert_close(got, d.t() @ m, rtol=1e-12, atol=1e-10)
