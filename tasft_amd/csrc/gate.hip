@@ -712,13 +712,15 @@ __device__ __forceinline__ void pair_chunk64(const GatePairParams& q, int64_t bh
 // the late query rows (the longest MLP) start first, and the workgroups dispatched last,
 // once key workgroups have left, take the early rows, whose MLP is short.
 //
-// Publication follows the gfx950 memory model at agent scope: every thread of a key
-// workgroup makes its unit stores visible device-wide (release fence: L2 written back)
-// before one relaxed agent-scope add to the counter; thread 0 of a query workgroup polls
-// the counter with acquire loads (device-level reads), and after the barrier every thread
-// runs an acquire fence (L1 and L2 invalidated) before reading units. Measured on the box
-// with a bounded probe: a counter raised on one XCD is seen by pollers on all eight, and the
-// data published with it reads back exactly.
+// Publication at agent scope without an L2 writeback: a key workgroup stores its units
+// with agent-scope atomic stores (written through to the device coherence point), waits
+// for them (vmcnt(0)), meets the workgroup barrier, and thread 0 adds 1 to the group's
+// counter with a relaxed agent-scope atomic. Thread 0 of a query workgroup polls the
+// counter with relaxed agent-scope loads (device-level reads) and s_sleep, then runs one
+// agent-scope acquire fence (this CU's L1 and the XCD's L2 invalidated) before the barrier
+// that releases every thread's unit reads. Measured on the box with a bounded probe: a
+// counter raised on one XCD is seen by pollers on all eight, and the data published with it
+// reads back exactly.
 //
 // The wait cannot deadlock: a workgroup waits only on workgroups of lower index, which wait
 // on nothing, and each XCD dispatches its workgroups in index order. It is bounded anyway
