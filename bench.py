@@ -36,10 +36,10 @@ FLOP_PER_BLOCK = 4 * 64 * 64 * 128  # QK^T + PV of one 64x64 tile at D=128
 # HBM bytes per launch of the config-2 prefill kernel, measured offline with rocprofv3:
 # FETCH_SIZE (KiB per dispatch, scaled by 2.0, the factor a plain 256 MiB copy shows) plus
 # WRITE_SIZE (scale 1.0), on `bench.py --no-cpu-baseline --steps 3 --warmup 1`. Against the
-# 673.2 MB algorithmic bytes (Q + K + V + O + mask) this is 1.71x: between launches the gate
-# streams 335 MB of Q and K, and K/V blocks are fetched again by the rows of a KV group
-# (4 MB of K/V per group against a 4 MB L2 per XCD).
-PREFILL_TRAFFIC_BYTES = 427615 * 1024 * 2.0 + 266602 * 1024
+# 673.2 MB algorithmic bytes (Q + K + V + O + mask) this is 1.25x: K/V blocks are fetched
+# again by the rows of a KV group (4 MB of K/V per group against a 4 MB L2 per XCD); Q and O
+# go through non-temporal loads and stores.
+PREFILL_TRAFFIC_BYTES = 279177 * 1024 * 2.0 + 262144 * 1024
 # Untimed decode launches before the decode timing (steady state, see main()).
 DECODE_SETTLE = 150
 # Untimed config-2 steps between the timed steps and the per-kernel (event) split.
