@@ -25,7 +25,7 @@ from tasft_amd.training import TASFTObjective, gate_loss_from_qk, gate_target_fr
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("NB", [37, 128, 160])
+@pytest.mark.parametrize("NB", [20, 37, 128, 160])
 def test_gate_kl_kernel_matches_oracle(NB):
     """NB 37 and 128 (16384 entries per (b, head), the largest) run the register-resident
     kernel; NB 160 runs the streaming one."""
